@@ -1,0 +1,100 @@
+// MI355X (gfx950) compute backend for the streaming sparse INT4 MLP.
+//
+// Replaces the CUDA reference enqueue (LeanStream kernels/streaming_mlp.cu:85-93,
+// streaming_mlp_candidates.cu:3-11) and the native Triton pre-enqueue
+// (backends/triton/enqueue.cpp:26-46, include/leanstream/triton_cuda.h:21-47) behind
+// the unchanged ComputeBackend contract (include/leanstream/runtime.h:10-22).
+//
+// Caller owns every data buffer. bind() is the cold path (validation, occupancy
+// query, small device sync state); enqueue() performs no allocation, compilation,
+// profiling, device query or synchronisation: it selects a candidate in O(1) and
+// launches pre-specialised kernels on the caller's HIP stream.
+#pragma once
+#include "kernel_selector.h"
+#include "runtime.h"
+
+namespace leanstream::runtime {
+
+// CDNA4 candidate catalog. `workers` = persistent workgroups (256 threads each);
+// entry_point 0 = one fused launch (core + ready queue + compact reduction),
+// entry_point 1 = split launches (stage A -> stage B -> reduction kernel).
+inline constexpr KernelCandidate kHipCandidates[] = {
+    {0, 256, "hip_fused_w256", 256, 0, 0, 0, 0},
+    {1, 512, "hip_fused_w512", 512, 0, 0, 0, 0},
+    {2, 1024, "hip_fused_w1024", 1024, 0, 0, 0, 0},
+    {3, 256, "hip_split_w256", 256, 0, 0, 0, 1},
+    {4, 512, "hip_split_w512", 512, 0, 0, 0, 1},
+};
+inline constexpr uint32_t kHipCandidateCount = 5;
+inline constexpr KernelCandidate kHipDefault = kHipCandidates[0];
+inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexcept {
+    return KernelSelector(offline_table, {kHipCandidates, kHipCandidateCount}, kHipDefault);
+}
+
+// Geometry and caller-owned device buffers of one layer family (same shapes for every
+// layer the backend serves). Pointers are device addresses; hidden/partial may be
+// null, in which case bind() allocates them (cold path).
+struct HipLayerBuffers {
+    uint32_t width = 0;            // d, multiple of 256 (256..8192)
+    uint32_t group_size = 0;       // G neurons per group
+    uint32_t batch = 1;            // tokens per call (1 supported)
+    uint32_t slot_capacity = 0;    // destination rows (>= core + queue capacity)
+    uint32_t cache_groups = 0;     // slots in the cache arena
+    uint32_t staging_groups = 0;   // slots in the staging arena
+    uint32_t physical_groups = 0;  // scale rows / G
+    uint32_t queue_capacity = 0;   // largest DeviceExecQueue::capacity used
+    const void* cache = nullptr;   // packed groups [cache_groups][G][3][d/2]
+    const void* staging = nullptr; // packed groups [staging_groups][G][3][d/2]
+    const void* scales = nullptr;  // fp16 [physical_groups*G][3][d/128]
+    void* hidden = nullptr;        // fp32 [slot_capacity][G]
+    void* partial = nullptr;       // fp32 [slot_capacity][d]
+    void* y32 = nullptr;           // optional fp32 [d] pre-rounding output
+    uint32_t* executions = nullptr;     // optional per-destination execution counts
+    uint64_t* first_compute = nullptr;  // optional per-destination start stamps
+    uint32_t* claim_log = nullptr;      // optional claim log (queue positions)
+};
+
+class HipBackend {
+public:
+    explicit HipBackend(KernelDecisionTable table = {});
+    ~HipBackend();
+    HipBackend(const HipBackend&) = delete;
+    HipBackend& operator=(const HipBackend&) = delete;
+
+    int bind(const HipLayerBuffers&);
+    // One layer epoch: A/B/reduction work on `stream` (a hipStream_t).
+    int enqueue(KernelRuntimeState, const void* input, void* output, void* stream, Span<ExecDesc> core,
+                DeviceExecQueue, uint32_t epoch, ConsumerMode);
+    ComputeBackend view();
+
+    // Latest caller-supplied selector state (layer is overwritten per enqueue).
+    KernelRuntimeState state{};
+    // Optional lifecycle hooks (as in the Triton backend): completion proof and cache
+    // installation belong to the application. Without `completed`, completion is the
+    // backend's own event recorded after the last kernel of the latest enqueue.
+    void* lifecycle_context = nullptr;
+    bool (*completed)(void*, uint32_t) = nullptr;
+    int (*install_cache)(void*, uint32_t, Span<GroupId>) = nullptr;
+
+    uint32_t status() const;       // sticky device status bits (timeout, bad descriptor)
+    void clear_status();
+    void set_spin_limit_ticks(uint64_t ticks) { spin_limit_ = ticks; }
+    uint32_t slices() const { return slices_; }
+    uint32_t selected(KernelRuntimeState s) const { return selector_.select(s); }
+    int last_candidate() const { return last_candidate_; }
+    uint32_t max_workers() const { return max_workers_; }
+
+private:
+    struct Impl;
+    Impl* impl_ = nullptr;
+    KernelSelector selector_;
+    uint64_t spin_limit_ = 200000000ull;  // 2 s of the 100 MHz device clock
+    uint32_t slices_ = 0, ns_ = 0, max_workers_ = 0;
+    int last_candidate_ = -1;
+    static int submit(void*, uint32_t, const void*, void*, void*, Span<ExecDesc>, DeviceExecQueue, uint32_t,
+                      ConsumerMode);
+    static bool complete(void*, uint32_t);
+    static int commit(void*, uint32_t, Span<GroupId>);
+};
+
+}  // namespace leanstream::runtime

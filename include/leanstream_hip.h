@@ -1,0 +1,122 @@
+/* C ABI of the MI355X streaming sparse INT4 MLP library (libleanstream_hip.so).
+ *
+ * Plain pointers and sizes only. Every entry point names the LeanStream interface it
+ * replaces; a binding written against those interfaces maps one-to-one:
+ *
+ *   ls_hip_create / _create_table / _destroy    <- ls_triton_create / _create_table / _destroy
+ *                                                  (include/leanstream/triton_cuda.h:50-52)
+ *   ls_hip_bind                                 <- ls_triton_bind (triton_cuda.h:54-55); HIP kernels are
+ *                                                  compiled in, so bind takes buffers + geometry
+ *   ls_hip_enqueue                              <- ls_triton_enqueue (triton_cuda.h:56) merged with
+ *                                                  ComputeBackend::enqueue (include/leanstream/runtime.h:12-13)
+ *   ls_hip_complete                             <- ComputeBackend::complete (runtime.h:14)
+ *   ls_hip_compute_backend                      <- TritonBackend::view (backends/triton/enqueue.cpp:46)
+ *   ls_hip_select / ls_quantize_io_load         <- KernelSelector::select / quantize_io_load
+ *                                                  (include/leanstream/kernel_selector.h:26,33)
+ *   ls_hip_host_alloc / _free / _release_u32 /
+ *   ls_hip_acquire_all                          <- tm_alloc / tm_free / tm_release / tm_acquire_all
+ *                                                  (backends/triton/mapped.cpp:9-30)
+ *   ls_queue_*                                  <- ExecutionQueue (include/leanstream/execution_queue.h:19-34)
+ *   ls_rank_groups                              <- top-k ranking of ls_predict (predictor/predictor_cpu.cpp:192-201)
+ *
+ * Return values: 0 on success, a positive errno (EINVAL, ENOTSUP, ...) for rejected
+ * arguments, or a positive hipError_t for a failed launch.
+ */
+#ifndef LEANSTREAM_HIP_H
+#define LEANSTREAM_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Five 32-bit words, identical to leanstream::runtime::ExecDesc. */
+typedef struct ls_exec_desc {
+    uint32_t logical_group, physical_group, source_slot, dest_slot, source_kind;
+} ls_exec_desc;
+
+/* Identical to leanstream::runtime::DeviceExecQueue. */
+typedef struct ls_device_queue {
+    ls_exec_desc* descriptors;
+    uint32_t* ready_indices;
+    void* control; /* 128-byte QueueControl in host-coherent memory */
+    uint32_t capacity;
+} ls_device_queue;
+
+/* Identical to leanstream::runtime::HipLayerBuffers. */
+typedef struct ls_hip_layer_buffers {
+    uint32_t width, group_size, batch, slot_capacity;
+    uint32_t cache_groups, staging_groups, physical_groups, queue_capacity;
+    const void* cache;
+    const void* staging;
+    const void* scales;
+    void* hidden;
+    void* partial;
+    void* y32;
+    uint32_t* executions;
+    uint64_t* first_compute;
+    uint32_t* claim_log;
+} ls_hip_layer_buffers;
+
+/* Consumer modes (leanstream::runtime::ConsumerMode). */
+enum { LS_MODE_BATCH_COMPAT = 0, LS_MODE_PROGRESSIVE = 1, LS_MODE_AUTO = 2 };
+/* Device status bits returned by ls_hip_status. */
+enum { LS_STATUS_TIMEOUT = 1, LS_STATUS_QUEUE_ERROR = 2, LS_STATUS_BAD_DESCRIPTOR = 4 };
+
+/* ---- backend ---- */
+void* ls_hip_create(void);
+void* ls_hip_create_table(const uint8_t* entries, uint32_t layers, uint32_t buckets);
+void ls_hip_destroy(void* backend);
+int ls_hip_bind(void* backend, const ls_hip_layer_buffers* buffers);
+int ls_hip_enqueue(void* backend, uint32_t layer, uint32_t bucket, uint32_t epoch, const void* input, void* output,
+                   void* stream, const ls_exec_desc* core, uint32_t core_count, const ls_device_queue* queue,
+                   uint32_t mode);
+int ls_hip_complete(void* backend, uint32_t layer);
+/* Writes a leanstream::runtime::ComputeBackend (context + 5 function pointers). */
+int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t out_bytes);
+uint32_t ls_hip_status(void* backend);
+void ls_hip_clear_status(void* backend);
+void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
+uint32_t ls_hip_slices(void* backend);
+uint32_t ls_hip_select(void* backend, uint32_t layer, uint32_t bucket);
+int ls_hip_last_candidate(void* backend);
+uint32_t ls_hip_max_workers(void* backend);
+uint32_t ls_quantize_io_load(uint32_t remaining, uint32_t total, uint32_t buckets);
+
+/* ---- coherent host memory (fine-grained, GPU-visible at system scope) ---- */
+void* ls_hip_host_alloc(uint64_t bytes);
+void ls_hip_host_free(void* ptr);
+void ls_hip_release_u32(void* base, int64_t index, uint32_t value);
+int ls_hip_acquire_all(const void* base, int32_t count, uint32_t value, int32_t timeout_ms);
+
+/* ---- ready-queue producer (serialized; see ExecutionQueue) ---- */
+void* ls_queue_create(const ls_device_queue* view);
+void ls_queue_destroy(void* queue);
+void ls_queue_reset(void* queue, uint32_t epoch);
+void ls_queue_prepare(void* queue, uint32_t total);
+void ls_queue_append_unpublished(void* queue, uint32_t index);
+void ls_queue_activate(void* queue);
+void ls_queue_seal(void* queue, uint32_t total);
+void ls_queue_publish_all(void* queue);
+void ls_queue_publish(void* queue, uint32_t index);
+void ls_queue_fail(void* queue, uint32_t error);
+/* Background publisher: publishes order[i] at time offset_ns[i] after start (busy
+ * wait on the host clock). If fail_after < count, publishes fail_after entries and
+ * then fails the queue with fail_code. Returns a handle for ls_publisher_join. */
+void* ls_publisher_start(void* queue, const uint32_t* order, const uint64_t* offset_ns, uint32_t count,
+                         uint32_t fail_after, uint32_t fail_code);
+int ls_publisher_join(void* publisher);
+
+/* ---- group selection ---- */
+/* Top-k logical ids by (score descending, id ascending); -1 on non-finite scores. */
+int ls_rank_groups(const float* scores, uint32_t count, uint32_t k, int32_t* out);
+
+/* ---- synthetic workload generation on the device (counter-based splitmix64) ---- */
+int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream);
+int ls_synth_uniform_f16(void* dst, uint64_t count, uint64_t seed, double lo, double hi, void* stream);
+int ls_synth_normal_f16(void* dst, uint64_t count, uint64_t seed, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,209 @@
+// HipBackend: the MI355X ComputeBackend for the streaming sparse INT4 MLP.
+// Cold path (bind): validation, geometry choice, occupancy query, device sync state.
+// Hot path (enqueue): O(1) candidate selection + one (fused) or three (split) launches
+// + one completion event, all on the caller's stream.
+#include "leanstream/hip_backend.h"
+#include <hip/hip_runtime_api.h>
+#include <algorithm>
+#include <cerrno>
+#include <cstring>
+#include "mlp_launch.h"
+
+namespace leanstream::runtime {
+
+struct HipBackend::Impl {
+    HipLayerBuffers buf{};
+    lsamd::MlpArgs base{};
+    lsamd::Bounds bounds{};
+    uint32_t* sync = nullptr;
+    uint32_t slot_words = 0;
+    uint32_t* status = nullptr;  // host-coherent
+    void* owned_hidden = nullptr;
+    void* owned_partial = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+    bool needs_clear = true;
+    uint32_t seq = 0;
+    int cus = 0, per_cu_fused = 0, per_cu_split = 0;
+    bool bound = false;
+
+    void release() {
+        if (sync) (void)hipFree(sync);
+        if (owned_hidden) (void)hipFree(owned_hidden);
+        if (owned_partial) (void)hipFree(owned_partial);
+        if (status) (void)hipHostFree(status);
+        if (done) (void)hipEventDestroy(done);
+        sync = nullptr;
+        owned_hidden = owned_partial = nullptr;
+        status = nullptr;
+        done = nullptr;
+        bound = false;
+    }
+    ~Impl() { release(); }
+};
+
+HipBackend::HipBackend(KernelDecisionTable table) : impl_(new Impl), selector_(hip_selector(table)) {}
+HipBackend::~HipBackend() { delete impl_; }
+
+namespace {
+
+// Items per unit: S = G / NS with NS in {8,4,2,1}, column tile d/S of whole packed
+// words, and at most 16 down-projection rows per thread (G * d/S <= 32768).
+bool choose_slices(uint32_t G, uint32_t d, uint32_t* slices, uint32_t* ns) {
+    for (uint32_t n : {8u, 4u, 2u, 1u}) {
+        if (G % n) continue;
+        const uint32_t S = G / n;
+        if (S == 0 || S > lsamd::kMaxSlices || d % S) continue;
+        const uint32_t tc = d / S, dwr = tc / 8;
+        if (tc % 8 || dwr == 0 || dwr > 256 || 256 % dwr) continue;
+        if (static_cast<uint64_t>(G) * tc > 32768) continue;
+        if (!lsamd::variant_available(static_cast<int>(d), static_cast<int>(n))) continue;
+        *slices = S;
+        *ns = n;
+        return true;
+    }
+    return false;
+}
+
+}  // namespace
+
+int HipBackend::bind(const HipLayerBuffers& b) {
+    Impl& p = *impl_;
+    if (p.bound) return EBUSY;
+    if (!b.width || b.width % 256 || !b.group_size || b.group_size > 256 || !b.slot_capacity || !b.physical_groups ||
+        !b.scales || (b.cache_groups && !b.cache) || (b.staging_groups && !b.staging))
+        return EINVAL;
+    if (b.batch != 1) return ENOTSUP;
+    uint32_t S = 0, ns = 0;
+    if (!choose_slices(b.group_size, b.width, &S, &ns)) return ENOTSUP;
+    p.buf = b;
+    const uint32_t units_cap = b.slot_capacity + b.queue_capacity;
+    p.slot_words = lsamd::sync_slot_words(units_cap);
+    hipError_t e = hipMalloc(&p.sync, sizeof(uint32_t) * 2 * p.slot_words);
+    if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(float) * b.slot_capacity * b.group_size);
+    if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p.done, hipEventDisableTiming);
+    int dev = 0;
+    if (e == hipSuccess) e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntryFused, &p.per_cu_fused);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntrySplit, &p.per_cu_split);
+    if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1)) e = hipErrorInvalidConfiguration;
+    if (e == hipSuccess) e = lsamd::clear_sync(p.sync, 2 * p.slot_words, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        p.release();
+        return static_cast<int>(e);
+    }
+    *p.status = 0;
+    lsamd::MlpArgs& a = p.base;
+    a = lsamd::MlpArgs{};
+    a.cache = static_cast<const uint8_t*>(b.cache);
+    a.staging = static_cast<const uint8_t*>(b.staging);
+    a.scales = static_cast<const uint16_t*>(b.scales);
+    a.hbuf = static_cast<float*>(b.hidden ? b.hidden : p.owned_hidden);
+    a.partial = static_cast<float*>(b.partial ? b.partial : p.owned_partial);
+    a.y32 = static_cast<float*>(b.y32);
+    a.executions = b.executions;
+    a.first_compute = b.first_compute;
+    a.claim_log = b.claim_log;
+    a.claim_log_cap = b.claim_log ? b.queue_capacity : 0;
+    a.sync = p.sync;
+    a.status = p.status;
+    a.group_size = b.group_size;
+    a.slices = S;
+    a.slot_words = p.slot_words;
+    a.units_cap = units_cap;
+    a.slot_capacity = b.slot_capacity;
+    p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
+    slices_ = S;
+    ns_ = ns;
+    max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused);
+    p.needs_clear = false;
+    p.recorded = false;
+    p.bound = true;
+    return 0;
+}
+
+int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, void* stream, Span<ExecDesc> core,
+                        DeviceExecQueue q, uint32_t epoch, ConsumerMode mode) {
+    Impl& p = *impl_;
+    if (!p.bound || !epoch || !input || !output || !q.control || !q.descriptors || !q.ready_indices) return EINVAL;
+    if ((core.size && !core.data) || core.size > p.buf.slot_capacity || q.capacity > p.buf.queue_capacity) return EINVAL;
+    const KernelCandidate c = selector_.candidate(selector_.select(s));
+    const int entry = c.entry_point == lsamd::kEntrySplit ? lsamd::kEntrySplit : lsamd::kEntryFused;
+    const int per_cu = entry == lsamd::kEntryFused ? p.per_cu_fused : p.per_cu_split;
+    // Persistent workers must be co-resident: items of one unit wait for each other.
+    const uint32_t resident = static_cast<uint32_t>(p.cus * per_cu);
+    const uint32_t workers = std::max<uint32_t>(1, std::min<uint32_t>(c.workers ? c.workers : resident, resident));
+    lsamd::MlpArgs a = p.base;
+    a.core = core.data;
+    a.core_count = static_cast<uint32_t>(core.size);
+    a.qdesc = q.descriptors;
+    a.ready = q.ready_indices;
+    a.control = q.control;
+    a.capacity = q.capacity;
+    a.x = static_cast<const uint16_t*>(input);
+    a.y = static_cast<uint16_t*>(output);
+    a.epoch = epoch;
+    a.batch_mode = mode == ConsumerMode::Progressive ? 0u : 1u;
+    a.spin_limit = spin_limit_;
+    auto hs = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    if (p.needs_clear) {
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, hs);
+        if (e != hipSuccess) return static_cast<int>(e);
+        p.needs_clear = false;
+        p.seq = 0;
+    }
+    a.seq = ++p.seq;
+    const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(ns_), static_cast<int>(workers), entry};
+    e = lsamd::launch_layer(plan, a, p.bounds, hs);
+    last_candidate_ = static_cast<int>(c.id);
+    if (e != hipSuccess) {
+        p.needs_clear = true;  // a partial launch may have left a ring slot dirty
+        p.recorded = false;
+        return static_cast<int>(e);
+    }
+    e = hipEventRecord(p.done, hs);
+    p.recorded = e == hipSuccess;
+    return static_cast<int>(e);
+}
+
+uint32_t HipBackend::status() const { return impl_->status ? __atomic_load_n(impl_->status, __ATOMIC_ACQUIRE) : 0; }
+void HipBackend::clear_status() {
+    if (impl_->status) __atomic_store_n(impl_->status, 0u, __ATOMIC_RELEASE);
+}
+
+int HipBackend::submit(void* ctx, uint32_t layer, const void* input, void* output, void* stream, Span<ExecDesc> core,
+                       DeviceExecQueue q, uint32_t epoch, ConsumerMode mode) {
+    auto& b = *static_cast<HipBackend*>(ctx);
+    KernelRuntimeState s = b.state;
+    s.layer = layer;
+    return b.enqueue(s, input, output, stream, core, q, epoch, mode);
+}
+
+bool HipBackend::complete(void* ctx, uint32_t layer) {
+    auto& b = *static_cast<HipBackend*>(ctx);
+    if (b.completed) return b.completed(b.lifecycle_context, layer);
+    if (!b.impl_->recorded) return true;
+    return hipEventQuery(b.impl_->done) == hipSuccess;
+}
+
+int HipBackend::commit(void* ctx, uint32_t layer, Span<GroupId> ids) {
+    auto& b = *static_cast<HipBackend*>(ctx);
+    // Cache installation is application policy; without a hook there is nothing to install.
+    return b.install_cache ? b.install_cache(b.lifecycle_context, layer, ids) : 0;
+}
+
+ComputeBackend HipBackend::view() {
+    ComputeBackend v;
+    v.context = this;
+    v.enqueue = submit;
+    v.complete = complete;
+    v.commit = commit;
+    return v;
+}
+
+}  // namespace leanstream::runtime

@@ -1,0 +1,840 @@
+// gfx950 kernels for LeanStream's streaming sparse INT4 MLP.
+//
+// Arithmetic (LeanStream kernels/streaming_mlp.cu:11-41, backends/triton/core.py:9-17):
+//   w      = fp16( q * scale[c/128] ),  q = signed low-nibble-first INT4
+//   gate   = sum_c w_gate(c) x(c)   up = sum_c w_up(c) x(c)          (fp32)
+//   h      = fp16( fp16(silu(fp16(gate))) * fp16(up) )
+//   partial[dest][c] = sum_n h_n w_down(n, c)                         (fp32)
+//   y[c]   = fp16( sum_{slot = 0..U-1} partial[slot][c] )             (fp32, slot order)
+//
+// Work decomposition (MI355X-specific): every descriptor ("unit", one group of G
+// neurons) is cut into S items. Item j computes gate/up for neurons
+// [j*G/S, (j+1)*G/S) and the down projection for columns [j*d/S, (j+1)*d/S).
+// The down half of an item needs h of all G neurons of its unit, so items of
+// one unit meet at a per-unit counter. Items are spread over a persistent grid
+// sized to the chip, so a 58-group layer occupies every CU.
+//
+// Exactness: dequantisation is exact. The nibble is biased (x ^ 8) and OR-ed into
+// an fp16 magic constant (0x6400 = 1024 for low nibbles, 0x5400 = 64 with a 4-bit
+// mantissa offset for high nibbles); subtracting 1032 / 72 yields q exactly, and a
+// packed fp16 multiply rounds q*scale once (round-to-nearest-even), which is the
+// reference's fp16_rn(float(q)*float(scale)). Products w*x are exact in fp32;
+// only the fp32 summation order differs from the reference.
+//
+// Cross-workgroup data (h, partials, counters) uses agent-scope relaxed atomics,
+// which compile to sc1 loads/stores that are coherent across the eight XCD L2s,
+// with an explicit vmcnt(0) wait before each signalling atomic. No acquire or
+// release fence is issued inside a spin loop (those expand to whole-L2
+// invalidate / write-back). Every wait is bounded by a wall-clock limit; on
+// expiry the status word records a timeout and every worker leaves.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "mlp_args.h"
+#include "mlp_launch.h"
+
+namespace lsamd {
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxRows = 16;         // down-projection rows per thread held in registers
+constexpr int kRedFloats = 2048;     // LDS scratch for the cross-thread column reduction
+
+// ---------------------------------------------------------------------------------
+// memory helpers
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ldf_agent(const float* p) {
+    return __uint_as_float(ld_agent(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ void stf_agent(float* p, float v) {
+    st_agent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+__device__ __forceinline__ uint32_t ld_sys(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint64_t ld_sys64(const uint32_t* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+__device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// All of this thread's earlier memory operations have completed at their point of
+// coherence (stores acknowledged, loads returned).
+__device__ __forceinline__ void drain_vmem() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
+
+__device__ __forceinline__ u32x4 ld_stream16(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ uint32_t ld_stream4(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+}
+
+__device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+__device__ __forceinline__ _Float16 half_bits(uint16_t v) { return __builtin_bit_cast(_Float16, v); }
+__device__ __forceinline__ float round_half(float v) { return (float)(_Float16)v; }
+
+// Exact dequantisation of eight signed nibbles (one 32-bit word) into four fp16
+// pairs: out[k] = (w(col k), w(col k+4)) when the word holds one row, or
+// (row a, row b) of one column when the halves of the word come from two rows.
+__device__ __forceinline__ void dequant8(uint32_t word, h2 s, h2 out[4]) {
+    const uint32_t m = word ^ 0x88888888u;      // two's complement -> offset binary
+    const uint32_t m8 = m >> 8;
+    const h2 lo_bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    const h2 hi_bias = {(_Float16)-72.0f, (_Float16)-72.0f};
+    out[0] = (as_h2((m & 0x000F000Fu) | 0x64006400u) + lo_bias) * s;
+    out[1] = (as_h2((m & 0x00F000F0u) | 0x54005400u) + hi_bias) * s;
+    out[2] = (as_h2((m8 & 0x000F000Fu) | 0x64006400u) + lo_bias) * s;
+    out[3] = (as_h2((m8 & 0x00F000F0u) | 0x54005400u) + hi_bias) * s;
+}
+
+__device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// ---------------------------------------------------------------------------------
+// bounded waiting
+// ---------------------------------------------------------------------------------
+struct Waiter {
+    uint64_t start, limit;
+    __device__ Waiter(uint64_t lim) : start(now_ticks()), limit(lim) {}
+    __device__ bool expired() const { return now_ticks() - start > limit; }
+};
+
+__device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, uint32_t bit) {
+    __hip_atomic_fetch_or(a.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    st_agent(slot + kSyncAbort, 1u);
+}
+
+// ---------------------------------------------------------------------------------
+// Geometry of the gate/up half of an item, specialised on width D and neurons per item NS.
+// ---------------------------------------------------------------------------------
+template <int D, int NS>
+struct GuGeom {
+    static constexpr int CPR = D / 32;                 // 16-byte chunks per projection row
+    static constexpr int LPR = CPR < 64 ? CPR : 64;    // lanes sharing one row
+    static constexpr int CPL = CPR / LPR;              // chunks per lane per row
+    static constexpr int NPW = 64 / LPR;               // neurons per wave per pass
+    static constexpr int NPP = 4 * NPW;                // neurons per workgroup per pass
+    static constexpr int PASSES = (NS + NPP - 1) / NPP;
+    static constexpr int BLOCKS = D / 128;             // scale blocks per row
+    static_assert(D % 256 == 0 && CPR >= 8, "width must be a multiple of 256");
+};
+
+// x for this lane's chunks, rearranged into (k, k+4) pairs to match dequant8.
+template <int D, int NS>
+struct XRegs {
+    h2 p[GuGeom<D, NS>::CPL][16];
+};
+
+template <int D, int NS>
+__device__ __forceinline__ void load_x(const uint16_t* x, XRegs<D, NS>& xr) {
+    using Gm = GuGeom<D, NS>;
+    const int lane = threadIdx.x & 63;
+    const int r = lane % Gm::LPR;
+#pragma unroll
+    for (int k = 0; k < Gm::CPL; ++k) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(x + 32 * (r + Gm::LPR * k));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            // halves 8g..8g+7 live in words 4g..4g+3 as (0,1)(2,3)(4,5)(6,7)
+            const uint32_t w0 = src[4 * g + 0], w1 = src[4 * g + 1], w2 = src[4 * g + 2], w3 = src[4 * g + 3];
+            xr.p[k][4 * g + 0] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x05040100u));  // (x0, x4)
+            xr.p[k][4 * g + 1] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x07060302u));  // (x1, x5)
+            xr.p[k][4 * g + 2] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x05040100u));  // (x2, x6)
+            xr.p[k][4 * g + 3] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x07060302u));  // (x3, x7)
+        }
+    }
+}
+
+template <int D, int NS>
+struct GuLoads {
+    u32x4 w[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];
+    uint16_t s[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];
+};
+
+// Issue every gate/up load of one item. grp points at the unit's packed bytes,
+// sc at the unit's scale rows, n0 is the first neuron of the item.
+template <int D, int NS>
+__device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, GuLoads<D, NS>& L) {
+    using Gm = GuGeom<D, NS>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+#pragma unroll
+    for (int p = 0; p < Gm::PASSES; ++p) {
+        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;   // neuron within the item
+        const bool ok = nu < NS;
+        const int n = n0 + (ok ? nu : 0);
+        const uint8_t* row = grp + (size_t)n * (3 * D / 2);
+        const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
+#pragma unroll
+        for (int k = 0; k < Gm::CPL; ++k) {
+            const int chunk = r + Gm::LPR * k;
+            if (ok) {
+                L.w[p][0][k] = ld_stream16(row + 16 * chunk);
+                L.w[p][1][k] = ld_stream16(row + D / 2 + 16 * chunk);
+                L.s[p][0][k] = srow[chunk >> 2];
+                L.s[p][1][k] = srow[Gm::BLOCKS + (chunk >> 2)];
+            } else {
+                L.w[p][0][k] = u32x4{0, 0, 0, 0};
+                L.w[p][1][k] = u32x4{0, 0, 0, 0};
+                L.s[p][0][k] = 0;
+                L.s[p][1][k] = 0;
+            }
+        }
+    }
+}
+
+// Finish gate/up for the item: dot products, row reductions, activation.
+// Writes h (fp32, fp16-exact) for neurons n0..n0+NS-1 of unit row `hrow`.
+template <int D, int NS>
+__device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<D, NS>& xr, float* hrow, int n0) {
+    using Gm = GuGeom<D, NS>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+#pragma unroll
+    for (int p = 0; p < Gm::PASSES; ++p) {
+        float acc[2] = {0.f, 0.f};
+#pragma unroll
+        for (int proj = 0; proj < 2; ++proj) {
+#pragma unroll
+            for (int k = 0; k < Gm::CPL; ++k) {
+                const _Float16 sv = half_bits(L.s[p][proj][k]);
+                const h2 s2 = {sv, sv};
+                const u32x4 v = L.w[p][proj][k];
+                const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    h2 w[4];
+                    dequant8(words[g], s2, w);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], xr.p[k][4 * g + q], acc[proj]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 1; m < Gm::LPR; m <<= 1) {
+            acc[0] += __shfl_xor(acc[0], m, 64);
+            acc[1] += __shfl_xor(acc[1], m, 64);
+        }
+        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;
+        if (r == 0 && nu < NS) {
+            const float g = round_half(acc[0]);
+            const float u = round_half(acc[1]);
+            const float s = round_half(g / (1.0f + __expf(-g)));
+            const float h = round_half(s * u);
+            stf_agent(hrow + n0 + nu, h);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Down projection of one column tile of one unit (all G neurons), tc columns.
+// Thread t owns 8 columns (one packed word per row) and rows r0, r0+rpp, ...
+// ---------------------------------------------------------------------------------
+struct DnLoads {
+    uint32_t w[kMaxRows];
+    uint16_t s[kMaxRows];
+};
+
+struct DnGeom {
+    int dwr, rpp, dc, r0, nrows;
+    __device__ DnGeom(int G, int tc) {
+        dwr = tc >> 3;                 // packed words per row in the tile
+        rpp = kThreads / dwr;          // rows covered per pass of the workgroup
+        dc = threadIdx.x % dwr;
+        r0 = threadIdx.x / dwr;
+        nrows = r0 < G ? (G - r0 + rpp - 1) / rpp : 0;
+    }
+};
+
+template <int D>
+__device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc, const DnGeom& gm, int c0, DnLoads& L) {
+    constexpr int BLOCKS = D / 128;
+    const int col = c0 + 8 * gm.dc;
+#pragma unroll
+    for (int i = 0; i < kMaxRows; ++i) {
+        if (i < gm.nrows) {
+            const int n = gm.r0 + gm.rpp * i;
+            L.w[i] = ld_stream4(grp + (size_t)n * (3 * D / 2) + D + (col >> 1));
+            L.s[i] = sc[(size_t)n * 3 * BLOCKS + 2 * BLOCKS + (col >> 7)];
+        } else {
+            L.w[i] = 0;
+            L.s[i] = 0;
+        }
+    }
+}
+
+// Sums the tile into red[] (fp32 [tc]) in a fixed order: per thread over its rows
+// in increasing order (pairs via dot2), then across row groups r0 = 0..rpp-1.
+__device__ __forceinline__ void dn_compute(const DnLoads& L, const DnGeom& gm, const float* hs, float* red, int tc) {
+    float acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxRows; i += 2) {
+        if (i < gm.nrows) {
+            const bool pair = i + 1 < gm.nrows;
+            const int na = gm.r0 + gm.rpp * i;
+            const int nb = pair ? na + gm.rpp : na;
+            const uint32_t wa = L.w[i], wb = pair ? L.w[i + 1] : L.w[i];
+            const h2 hab = {(_Float16)hs[na], pair ? (_Float16)hs[nb] : (_Float16)0.0f};
+            const h2 sab = {half_bits(L.s[i]), half_bits(pair ? L.s[i + 1] : L.s[i])};
+            h2 w[4];
+            dequant8(__builtin_amdgcn_perm(wb, wa, 0x05040100u), sab, w);   // columns 0..3
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[c] = dot2(w[c], hab, acc[c]);
+            dequant8(__builtin_amdgcn_perm(wb, wa, 0x07060302u), sab, w);   // columns 4..7
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[4 + c] = dot2(w[c], hab, acc[4 + c]);
+        }
+    }
+    __syncthreads();  // red[] may still be read by a previous tile's reducer
+    if (gm.nrows > 0) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = acc[c];
+    } else if (gm.r0 < gm.rpp) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = 0.f;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < tc; c += kThreads) {
+        float v = 0.f;
+        for (int r = 0; r < gm.rpp; ++r) v += red[r * tc + c];
+        red[kRedFloats + c] = v;   // reduced tile (second half of the scratch)
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------
+// descriptor access and validation
+// ---------------------------------------------------------------------------------
+struct Unit {
+    const uint8_t* grp;     // packed bytes of the group
+    const uint16_t* sc;     // scale rows of the group
+    uint32_t dest;
+    bool ok;
+};
+
+__device__ __forceinline__ Unit resolve(const MlpArgs& a, const Bounds& b, ExecDesc d, int D) {
+    Unit u;
+    const bool staging = d.source_kind == leanstream::runtime::SourceKind::Staging;
+    const uint32_t slots = staging ? b.staging_groups : b.cache_groups;
+    u.ok = d.source_slot < slots && d.physical_group < b.physical_groups && d.dest_slot < a.slot_capacity &&
+           (uint32_t)d.source_kind <= 1u;
+    const size_t group_bytes = (size_t)a.group_size * 3 * D / 2;
+    u.grp = (staging ? a.staging : a.cache) + (u.ok ? (size_t)d.source_slot * group_bytes : 0);
+    u.sc = a.scales + (u.ok ? (size_t)d.physical_group * a.group_size * 3 * (D / 128) : 0);
+    u.dest = u.ok ? d.dest_slot : 0;
+    return u;
+}
+
+__device__ __forceinline__ ExecDesc load_core(const MlpArgs& a, uint32_t i) { return a.core[i]; }
+
+// Queue descriptors live in host-coherent memory and are read at system scope
+// after the position has been observed published.
+__device__ __forceinline__ ExecDesc load_queue(const MlpArgs& a, uint32_t pos) {
+    const uint32_t idx = ld_sys(a.ready + pos);
+    ExecDesc d;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(a.qdesc + (idx < a.capacity ? idx : 0));
+    d.logical_group = ld_sys(p + 0);
+    d.physical_group = ld_sys(p + 1);
+    d.source_slot = ld_sys(p + 2);
+    d.dest_slot = ld_sys(p + 3);
+    d.source_kind = (leanstream::runtime::SourceKind)ld_sys(p + 4);
+    if (idx >= a.capacity) d.dest_slot = 0xffffffffu;  // forces validation failure
+    return d;
+}
+
+// ---------------------------------------------------------------------------------
+// Shared workgroup state
+// ---------------------------------------------------------------------------------
+struct Shared {
+    float red[2 * kRedFloats];
+    float hs[256];
+    uint32_t word[8];
+    uint32_t desc[5];
+    // queue state learnt once per launch: known, ok, total, path
+    uint32_t ep_known, ep_ok, ep_total, ep_path;
+};
+
+__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t pre);
+
+// Thread 0 reads the published descriptor once (two dependent system-scope reads) and
+// shares it with the workgroup.
+__device__ ExecDesc load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t pos) {
+    __syncthreads();  // previous readers of sh.desc are done
+    if (threadIdx.x == 0) {
+        const ExecDesc d = load_queue(a, pos);
+        sh.desc[0] = d.logical_group;
+        sh.desc[1] = d.physical_group;
+        sh.desc[2] = d.source_slot;
+        sh.desc[3] = d.dest_slot;
+        sh.desc[4] = (uint32_t)d.source_kind;
+    }
+    __syncthreads();
+    ExecDesc d;
+    d.logical_group = sh.desc[0];
+    d.physical_group = sh.desc[1];
+    d.source_slot = sh.desc[2];
+    d.dest_slot = sh.desc[3];
+    d.source_kind = (leanstream::runtime::SourceKind)sh.desc[4];
+    return d;
+}
+
+// Reduce one column tile over destination rows 0..U-1 in slot order.
+template <int D>
+__device__ void reduce_tile(const MlpArgs& a, int c0, int tc, uint32_t U) {
+    for (int c = threadIdx.x; c < tc; c += kThreads) {
+        const int col = c0 + c;
+        float v = 0.f;
+        uint32_t i = 0;
+        for (; i + 4 <= U; i += 4) {
+            const float p0 = ldf_agent(a.partial + (size_t)(i + 0) * D + col);
+            const float p1 = ldf_agent(a.partial + (size_t)(i + 1) * D + col);
+            const float p2 = ldf_agent(a.partial + (size_t)(i + 2) * D + col);
+            const float p3 = ldf_agent(a.partial + (size_t)(i + 3) * D + col);
+            v += p0; v += p1; v += p2; v += p3;
+        }
+        for (; i < U; ++i) v += ldf_agent(a.partial + (size_t)i * D + col);
+        if (a.y32) a.y32[col] = v;
+        a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// One cooperative item: gate/up for slice j of unit `unit`, then (after all S
+// slices of the unit published h) the down projection of column tile j.
+// FUSED: also count the tile and let the last writer reduce it.
+// ---------------------------------------------------------------------------------
+template <int D, int NS, bool FUSED>
+__device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Unit& u,
+                         uint32_t unit, uint32_t j, bool cooperative, uint64_t pre) {
+    const int G = a.group_size;
+    const int S = a.slices;
+    const int tc = D / S;
+    const int c0 = j * tc;
+    if (j == 0 && threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
+    GuLoads<D, NS> gl;
+    gu_issue<D, NS>(u.grp, u.sc, j * NS, gl);
+    DnGeom gm(G, tc);
+    DnLoads dl;
+    dn_issue<D>(u.grp, u.sc, gm, c0, dl);
+    float* hrow = a.hbuf + (size_t)u.dest * G;
+    gu_compute<D, NS>(gl, xr, hrow, j * NS);
+    drain_vmem();
+    __syncthreads();
+    if (cooperative) {
+        if (threadIdx.x == 0) {
+            add_agent(slot + kSyncUnits + unit, 1u);
+            Waiter wt(a.spin_limit);
+            uint32_t ok = 1;
+            while (ld_agent(slot + kSyncUnits + unit) < (uint32_t)S) {
+                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+                if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            sh.word[0] = ok;
+        }
+        __syncthreads();
+        if (!sh.word[0]) return;
+    }
+    for (int n = threadIdx.x; n < G; n += kThreads) sh.hs[n] = ldf_agent(hrow + n);
+    __syncthreads();
+    dn_compute(dl, gm, sh.hs, sh.red, tc);
+    float* prow = a.partial + (size_t)u.dest * D + c0;
+    for (int c = threadIdx.x; c < tc; c += kThreads) stf_agent(prow + c, sh.red[kRedFloats + c]);
+    drain_vmem();
+    __syncthreads();
+    // The tile counter target is U = core + queue total, final once the epoch is seen.
+    if (FUSED && !await_epoch(a, sh, slot, pre)) return;
+    const uint32_t U = a.core_count + sh.ep_total;
+    if (threadIdx.x == 0) {
+        uint32_t last = 0;
+        if (a.executions) {
+            if (add_agent(slot + kSyncUnits + a.units_cap + unit, 1u) == (uint32_t)S - 1)
+                __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        if (FUSED) last = add_agent(slot + kSyncTiles + j, 1u) + 1 == U;
+        sh.word[1] = last;
+    }
+    __syncthreads();
+    if (FUSED && sh.word[1]) reduce_tile<D>(a, c0, tc, U);
+}
+
+// Process a whole unit inside one workgroup (claim path): no cross-workgroup wait.
+template <int D, int NS, bool FUSED>
+__device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Unit& u,
+                              uint32_t unit, uint32_t U) {
+    const int S = a.slices;
+    // gate/up for every slice first so that the whole h row exists, then the tiles.
+    for (int j = 0; j < S; ++j) {
+        if (j == 0 && threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
+        GuLoads<D, NS> gl;
+        gu_issue<D, NS>(u.grp, u.sc, j * NS, gl);
+        gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * a.group_size, j * NS);
+    }
+    drain_vmem();
+    __syncthreads();
+    const int G = a.group_size;
+    const int tc = D / S;
+    DnGeom gm(G, tc);
+    float* hrow = a.hbuf + (size_t)u.dest * G;
+    for (int n = threadIdx.x; n < G; n += kThreads) sh.hs[n] = ldf_agent(hrow + n);
+    __syncthreads();
+    for (int j = 0; j < S; ++j) {
+        const int c0 = j * tc;
+        DnLoads dl;
+        dn_issue<D>(u.grp, u.sc, gm, c0, dl);
+        dn_compute(dl, gm, sh.hs, sh.red, tc);
+        float* prow = a.partial + (size_t)u.dest * D + c0;
+        for (int c = threadIdx.x; c < tc; c += kThreads) stf_agent(prow + c, sh.red[kRedFloats + c]);
+        drain_vmem();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t last = 0;
+            if (FUSED) last = add_agent(slot + kSyncTiles + j, 1u) + 1 == U;
+            sh.word[1] = last;
+        }
+        __syncthreads();
+        if (FUSED && sh.word[1]) reduce_tile<D>(a, c0, tc, U);
+    }
+    if (threadIdx.x == 0 && a.executions)
+        __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// ---------------------------------------------------------------------------------
+// Queue protocol (LeanStream kernels/streaming_mlp.cu:47-79, backends/triton/persistent.py:32-92):
+// wait for the layer epoch (or an error), optionally for batch publication, then
+// decide once per launch between the all-ready fast path and the claim path.
+// Returns false when the worker must leave (error / abort / timeout).
+// ---------------------------------------------------------------------------------
+// `pre` is thread 0's early 64-bit snapshot of (total_count, epoch): the two words
+// are adjacent (byte offsets 8 and 12), so one load returns a consistent pair and
+// its PCIe latency overlaps the first item's work.
+__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t pre) {
+    // Every thread reads the flag before thread 0 may write it (barrier in between),
+    // so the whole workgroup takes the same branch.
+    const uint32_t known = sh.ep_known;
+    __syncthreads();
+    if (known) return sh.ep_ok != 0;
+    if (threadIdx.x == 0) {
+        uint32_t ok = 1;
+        uint64_t te = pre;
+        Waiter wt(a.spin_limit);
+        for (;;) {
+            if ((uint32_t)(te >> 32) == a.epoch) break;
+            if (ld_sys(&a.control->error)) { ok = 0; break; }
+            if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+            __builtin_amdgcn_s_sleep(8);
+            te = ld_sys64(&a.control->total_count);
+        }
+        uint32_t total = ok ? (uint32_t)te : 0;
+        if (ok && (total > a.capacity || a.core_count + total > a.slot_capacity)) {
+            raise_status(a, slot, kStatusBadDescriptor);
+            ok = 0;
+        }
+        if (ok && total && a.batch_mode) {
+            Waiter wb(a.spin_limit);
+            for (;;) {
+                if (ld_sys(&a.control->batch_epoch) == a.epoch) break;
+                if (ld_sys(&a.control->error)) { ok = 0; break; }
+                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+                if (wb.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        uint32_t path = 0;
+        if (ok && total) {
+            const uint32_t proposed = ld_sys(&a.control->ready_count) == total ? 2u : 1u;
+            uint32_t expected = 0;
+            __hip_atomic_compare_exchange_strong(slot + kSyncPath, &expected, proposed, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            path = ld_agent(slot + kSyncPath);
+        }
+        sh.ep_ok = ok;
+        sh.ep_total = total;
+        sh.ep_path = path;
+        sh.ep_known = 1;
+    }
+    __syncthreads();
+    return sh.ep_ok != 0;
+}
+
+__device__ __forceinline__ void init_shared(Shared& sh) {
+    if (threadIdx.x == 0) { sh.ep_known = 0; sh.ep_ok = 0; sh.ep_total = 0; sh.ep_path = 0; }
+    __syncthreads();
+}
+
+// Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86).
+// Returns the number of claimed positions (0 = leave) and the head in sh.word[5].
+__device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total) {
+    if (threadIdx.x == 0) {
+        uint32_t got = 0, head = 0;
+        Waiter wt(a.spin_limit);
+        for (;;) {
+            if (ld_agent(slot + kSyncAbort)) break;
+            const uint32_t ready = ld_sys(&a.control->ready_count);
+            head = ld_agent(slot + kSyncClaimHead);
+            if (head >= total) break;
+            if (head < ready) {
+                const uint32_t end = min(head + 2u, min(ready, total));
+                uint32_t expected = head;
+                if (__hip_atomic_compare_exchange_strong(slot + kSyncClaimHead, &expected, end, __ATOMIC_RELAXED,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                    got = end - head;
+                    const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
+                    if (a.claim_log && seq < a.claim_log_cap) a.claim_log[seq] = head | (got << 24);
+                    break;
+                }
+                continue;
+            }
+            if (ld_sys(&a.control->error)) { st_agent(slot + kSyncAbort, 1u); break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); break; }
+            __builtin_amdgcn_s_sleep(4);
+        }
+        sh.word[5] = head;
+        sh.word[6] = got;
+    }
+    __syncthreads();
+    return sh.word[6];
+}
+
+template <int D, int NS, bool FUSED>
+__device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Bounds& b,
+                              uint32_t W, uint32_t w, uint32_t first_item, uint64_t pre) {
+    if (!await_epoch(a, sh, slot, pre)) return;
+    const uint32_t total = sh.ep_total;
+    const uint32_t path = sh.ep_path;
+    if (!total) return;
+    const uint32_t U = a.core_count + total;
+    const uint32_t S = a.slices;
+    if (path == 2) {
+        (void)U;
+        // all ready: static stripes of (position, slice) items, continuing the
+        // round-robin after the core items so every worker gets an equal share.
+        const uint32_t n_items = total * S;
+        for (uint32_t i = (w + W - (first_item % W)) % W; i < n_items; i += W) {
+            const uint32_t pos = i / S, j = i % S;
+            const Unit u = resolve(a, b, load_queue_wg(a, sh, pos), D);
+            if (!u.ok) {
+                if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+                return;
+            }
+            if (threadIdx.x == 0 && j == 0 && a.claim_log && (pos & 1) == 0 && pos / 2 < a.claim_log_cap)
+                a.claim_log[pos / 2] = pos | (min(2u, total - pos) << 24);
+            run_item<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + pos, j, true, pre);
+        }
+        return;
+    }
+    for (;;) {
+        const uint32_t got = claim_pair(a, sh, slot, total);
+        if (!got) return;
+        const uint32_t head = sh.word[5];
+        for (uint32_t k = 0; k < got; ++k) {
+            const Unit u = resolve(a, b, load_queue_wg(a, sh, head + k), D);
+            if (!u.ok) {
+                if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+                return;
+            }
+            run_unit_solo<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + head + k, U);
+        }
+    }
+}
+
+// Last worker of a launch: clear the other ring slot for the next launch and, for an
+// empty layer (no rows at all), write the zero output the reduction would produce.
+template <int D>
+__device__ void finish_launch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t W, bool fused) {
+    __syncthreads();
+    if (threadIdx.x == 0) sh.word[7] = add_agent(slot + kSyncExit, 1u) + 1 == W;
+    __syncthreads();
+    if (!sh.word[7]) return;
+    uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
+    for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
+    if (fused && a.core_count == 0 && !ld_agent(slot + kSyncAbort)) {
+        // U == 0 only if the queue turned out empty; the queue total is final here.
+        const uint32_t total = ld_sys(&a.control->total_count);
+        if (total == 0 && ld_sys(&a.control->epoch) == a.epoch)
+            for (int c = threadIdx.x; c < D; c += kThreads) {
+                if (a.y32) a.y32[c] = 0.f;
+                a.y[c] = 0;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------------
+// Kernels
+// ---------------------------------------------------------------------------------
+
+// Fused layer: core items (stage A role), queue consumption (stage B role) and the
+// compact reduction (last writer of each column tile), one persistent launch.
+template <int D, int NS>
+__global__ __launch_bounds__(kThreads) void fused_layer_kernel(MlpArgs a, Bounds b) {
+    __shared__ Shared sh;
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+    init_shared(sh);
+    const uint32_t W = gridDim.x, w = blockIdx.x;
+    XRegs<D, NS> xr;
+    load_x<D, NS>(a.x, xr);
+    const uint32_t S = a.slices;
+    const uint32_t n_core = a.core_count * S;
+    for (uint32_t i = w; i < n_core; i += W) {
+        const uint32_t unit = i / S, j = i % S;
+        const Unit u = resolve(a, b, load_core(a, unit), D);
+        if (!u.ok) {
+            if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+            break;
+        }
+        run_item<D, NS, true>(a, sh, slot, xr, u, unit, j, true, pre);
+    }
+    consume_queue<D, NS, true>(a, sh, slot, xr, b, W, w, n_core, pre);
+    finish_launch<D>(a, sh, slot, W, true);
+}
+
+// Split path, stage A: core items only (no queue, no reduction).
+template <int D, int NS>
+__global__ __launch_bounds__(kThreads) void stage_a_kernel(MlpArgs a, Bounds b) {
+    __shared__ Shared sh;
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    init_shared(sh);
+    XRegs<D, NS> xr;
+    load_x<D, NS>(a.x, xr);
+    const uint32_t S = a.slices;
+    const uint32_t n_core = a.core_count * S;
+    for (uint32_t i = blockIdx.x; i < n_core; i += gridDim.x) {
+        const uint32_t unit = i / S, j = i % S;
+        const Unit u = resolve(a, b, load_core(a, unit), D);
+        if (!u.ok) {
+            if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+            return;
+        }
+        run_item<D, NS, false>(a, sh, slot, xr, u, unit, j, true, 0);
+    }
+}
+
+// Split path, stage B: persistent ready-queue consumer.
+template <int D, int NS>
+__global__ __launch_bounds__(kThreads) void stage_b_kernel(MlpArgs a, Bounds b) {
+    __shared__ Shared sh;
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+    init_shared(sh);
+    XRegs<D, NS> xr;
+    load_x<D, NS>(a.x, xr);
+    consume_queue<D, NS, false>(a, sh, slot, xr, b, gridDim.x, blockIdx.x, 0, pre);
+}
+
+// Split path, compact reduction over rows 0..core+total-1 (streaming_mlp.cu:80-84).
+// Block 0 also clears the other ring slot for the next launch.
+template <int D>
+__global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
+    const uint32_t total = ld_sys(&a.control->total_count);
+    uint32_t U = a.core_count + (total <= a.capacity ? total : 0);
+    if (U > a.slot_capacity) U = a.slot_capacity;
+    const int c0 = blockIdx.x * kThreads;
+    reduce_tile<D>(a, c0, kThreads, U);
+    if (blockIdx.x == 0) {
+        uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
+        for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
+    }
+}
+
+// Clears both ring slots (bind time, or after a partially failed enqueue).
+__global__ void clear_sync_kernel(uint32_t* sync, uint32_t words) {
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
+        st_agent(sync + i, 0u);
+}
+
+
+// ---------------------------------------------------------------------------------
+// Host-side launch dispatch over the compiled (width, neurons-per-item) variants.
+// ---------------------------------------------------------------------------------
+namespace {
+
+struct Variant {
+    int width, ns;
+    const void* fused;
+    const void* stage_a;
+    const void* stage_b;
+    const void* reduce;
+};
+
+template <int D, int NS>
+Variant make_variant() {
+    return {D, NS, reinterpret_cast<const void*>(&fused_layer_kernel<D, NS>),
+            reinterpret_cast<const void*>(&stage_a_kernel<D, NS>), reinterpret_cast<const void*>(&stage_b_kernel<D, NS>),
+            reinterpret_cast<const void*>(&reduce_kernel<D>)};
+}
+
+#define LS_VARIANTS_FOR(D) make_variant<D, 1>(), make_variant<D, 2>(), make_variant<D, 4>(), make_variant<D, 8>()
+
+const Variant* find_variant(int width, int ns) {
+    static const Variant table[] = {LS_VARIANTS_FOR(256),  LS_VARIANTS_FOR(512),  LS_VARIANTS_FOR(1024),
+                                    LS_VARIANTS_FOR(2048), LS_VARIANTS_FOR(4096), LS_VARIANTS_FOR(8192)};
+    for (const Variant& v : table)
+        if (v.width == width && v.ns == ns) return &v;
+    return nullptr;
+}
+
+}  // namespace
+
+bool variant_available(int width, int ns) { return find_variant(width, ns) != nullptr; }
+
+hipError_t resident_workers(int width, int ns, int entry_point, int* per_cu) {
+    const Variant* v = find_variant(width, ns);
+    if (!v) return hipErrorInvalidValue;
+    const void* k = entry_point == kEntryFused ? v->fused : v->stage_b;
+    int n = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kThreads, 0);
+    if (e == hipSuccess && entry_point != kEntryFused) {
+        int na = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&na, v->stage_a, kThreads, 0);
+        if (na < n) n = na;
+    }
+    *per_cu = n;
+    return e;
+}
+
+hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& bounds, hipStream_t stream) {
+    const Variant* v = find_variant(p.width, p.ns);
+    if (!v) return hipErrorInvalidValue;
+    MlpArgs a = args;
+    Bounds b = bounds;
+    void* kargs[] = {&a, &b};
+    if (p.entry_point == kEntryFused)
+        return hipLaunchKernel(v->fused, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+    hipError_t e = hipSuccess;
+    const uint32_t core_items = a.core_count * a.slices;
+    if (core_items) {
+        const uint32_t grid = core_items < (uint32_t)p.workers ? core_items : (uint32_t)p.workers;
+        e = hipLaunchKernel(v->stage_a, dim3(grid), dim3(kThreads), kargs, 0, stream);
+        if (e != hipSuccess) return e;
+    }
+    e = hipLaunchKernel(v->stage_b, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+    if (e != hipSuccess) return e;
+    void* rargs[] = {&a};
+    return hipLaunchKernel(v->reduce, dim3(p.width / kThreads), dim3(kThreads), rargs, 0, stream);
+}
+
+hipError_t clear_sync(uint32_t* sync, uint32_t words, hipStream_t stream) {
+    uint32_t grid = (words + kThreads - 1) / kThreads;
+    if (grid > 1024) grid = 1024;
+    if (!grid) grid = 1;
+    void* kargs[] = {&sync, &words};
+    return hipLaunchKernel(reinterpret_cast<const void*>(&clear_sync_kernel), dim3(grid), dim3(kThreads), kargs, 0,
+                           stream);
+}
+
+}  // namespace lsamd

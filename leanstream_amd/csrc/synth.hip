@@ -1,0 +1,111 @@
+// Synthetic workload generation on the device.
+//
+// Counter-based splitmix64 (S. Vigna's public-domain mixer): value(seed, i) =
+// mix(seed + (i + 1) * 0x9E3779B97F4A7C15). Element i of every stream depends only
+// on (seed, i), so a host mirror (leanstream_amd/synth.py) produces the same bytes.
+//   bytes:    little-endian bytes of value(seed, i) for word i (uniform INT4 nibbles)
+//   uniform:  lo + (hi - lo) * u, u = (value >> 11) * 2^-53, rounded double -> fp16 (RNE)
+//   normal:   Irwin-Hall: sum of 12 uniforms (sequential double adds) - 6 -> fp16 (RNE)
+// The double -> fp16 rounding is done in integer arithmetic (no double rounding).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <cerrno>
+#include "leanstream_hip.h"
+
+namespace lsamd {
+
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ inline uint64_t stream_value(uint64_t seed, uint64_t i) {
+    return mix64(seed + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+__host__ __device__ inline double stream_unit(uint64_t seed, uint64_t i) {
+    return (double)(stream_value(seed, i) >> 11) * 0x1.0p-53;
+}
+
+// Round-to-nearest-even conversion of a double to IEEE binary16 bits.
+__host__ __device__ inline uint16_t f64_to_f16_bits(double d) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, d);
+    const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    const int exp = (int)((b >> 52) & 0x7ff);
+    const uint64_t mant = b & 0xFFFFFFFFFFFFFull;
+    if (exp == 0x7ff) return sign | 0x7c00u | (mant ? 0x200u : 0u);
+    const int e = exp - 1023 + 15;
+    if (e >= 31) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint64_t m = mant | (1ull << 52);
+        const int shift = 42 + (1 - e);
+        uint64_t hm = m >> shift;
+        const uint64_t rem = m & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1))) ++hm;
+        return (uint16_t)(sign | hm);
+    }
+    uint32_t h = ((uint32_t)e << 10) | (uint32_t)(mant >> 42);
+    const uint64_t rem = mant & ((1ull << 42) - 1), half = 1ull << 41;
+    if (rem > half || (rem == half && (h & 1))) ++h;
+    return (uint16_t)(sign | h);
+}
+
+__global__ void synth_bytes_kernel(uint8_t* dst, uint64_t bytes, uint64_t seed) {
+    const uint64_t words = (bytes + 7) / 8;
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < words; i += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t v = stream_value(seed, i);
+        if (8 * i + 8 <= bytes) {
+            reinterpret_cast<uint64_t*>(dst)[i] = v;
+        } else {
+            for (uint64_t k = 0; 8 * i + k < bytes; ++k) dst[8 * i + k] = (uint8_t)(v >> (8 * k));
+        }
+    }
+}
+
+__global__ void synth_uniform_kernel(uint16_t* dst, uint64_t count, uint64_t seed, double lo, double hi) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = f64_to_f16_bits(lo + (hi - lo) * stream_unit(seed, i));
+}
+
+__global__ void synth_normal_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+        double acc = 0.0;
+        for (int k = 0; k < 12; ++k) acc += stream_unit(seed, 12 * i + k);
+        dst[i] = f64_to_f16_bits(acc - 6.0);
+    }
+}
+
+static unsigned grid_for(uint64_t n) {
+    uint64_t g = (n + 255) / 256;
+    return (unsigned)(g > 65536 ? 65536 : (g ? g : 1));
+}
+
+}  // namespace lsamd
+
+extern "C" {
+
+int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream) {
+    if (!dst && bytes) return EINVAL;
+    if (!bytes) return 0;
+    hipLaunchKernelGGL(lsamd::synth_bytes_kernel, dim3(lsamd::grid_for((bytes + 7) / 8)), dim3(256), 0,
+                       (hipStream_t)stream, (uint8_t*)dst, bytes, seed);
+    return (int)hipPeekAtLastError();
+}
+
+int ls_synth_uniform_f16(void* dst, uint64_t count, uint64_t seed, double lo, double hi, void* stream) {
+    if (!dst && count) return EINVAL;
+    if (!count) return 0;
+    hipLaunchKernelGGL(lsamd::synth_uniform_kernel, dim3(lsamd::grid_for(count)), dim3(256), 0, (hipStream_t)stream,
+                       (uint16_t*)dst, count, seed, lo, hi);
+    return (int)hipPeekAtLastError();
+}
+
+int ls_synth_normal_f16(void* dst, uint64_t count, uint64_t seed, void* stream) {
+    if (!dst && count) return EINVAL;
+    if (!count) return 0;
+    hipLaunchKernelGGL(lsamd::synth_normal_kernel, dim3(lsamd::grid_for(count)), dim3(256), 0, (hipStream_t)stream,
+                       (uint16_t*)dst, count, seed);
+    return (int)hipPeekAtLastError();
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+"""Synthetic sparse-MLP workloads (host mirror of the device generator in csrc/synth.hip).
+
+Element i of every stream is mix64(seed + (i + 1) * 0x9E3779B97F4A7C15) (splitmix64),
+so host (numpy) and device generation produce identical bytes:
+  * packed INT4 weights: the little-endian bytes of the stream (uniform nibbles in [-8, 7]);
+  * fp16 scales: lo + (hi - lo) * u, u = (value >> 11) * 2^-53, rounded to fp16;
+  * fp16 activations: Irwin-Hall normal, sum of 12 uniforms - 6, rounded to fp16;
+  * group scores: the same normal in fp32.
+
+Workloads named here are the layer shapes this library is measured on (d_model, d_ffn,
+64-neuron groups, active fraction k = floor(frac * groups + 0.5)).
+"""
+from dataclasses import dataclass, field
+
+import numpy as np
+
+GAMMA = np.uint64(0x9E3779B97F4A7C15)
+_M1 = np.uint64(0xBF58476D1CE4E5B9)
+_M2 = np.uint64(0x94D049BB133111EB)
+
+SEED_X, SEED_W, SEED_S, SEED_SCORE, SEED_ORDER = 1, 2, 3, 4, 5
+
+
+def stream(seed, index):
+    index = np.asarray(index, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed) + (index + np.uint64(1)) * GAMMA
+        z = (z ^ (z >> np.uint64(30))) * _M1
+        z = (z ^ (z >> np.uint64(27))) * _M2
+        return z ^ (z >> np.uint64(31))
+
+
+def unit(seed, index):
+    return (stream(seed, index) >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
+
+
+def fill_bytes(n, seed):
+    words = stream(seed, np.arange((n + 7) // 8, dtype=np.uint64))
+    return words.astype("<u8").view(np.uint8)[:n].copy()
+
+
+def uniform_f16(n, seed, lo, hi):
+    return (lo + (hi - lo) * unit(seed, np.arange(n, dtype=np.uint64))).astype(np.float16)
+
+
+def normal_f64(n, seed):
+    base = np.arange(n, dtype=np.uint64) * np.uint64(12)
+    acc = np.zeros(n, dtype=np.float64)
+    for k in range(12):
+        acc += unit(seed, base + np.uint64(k))
+    return acc - 6.0
+
+
+def normal_f16(n, seed):
+    return normal_f64(n, seed).astype(np.float16)
+
+
+def permutation(n, seed):
+    """Fisher-Yates driven by the stream: j = value(i) mod (i + 1), i from n-1 down."""
+    perm = np.arange(n, dtype=np.int64)
+    vals = stream(seed, np.arange(n, dtype=np.uint64))
+    for i in range(n - 1, 0, -1):
+        j = int(vals[i] % np.uint64(i + 1))
+        perm[i], perm[j] = perm[j], perm[i]
+    return perm
+
+
+def rank_top_k(scores, k):
+    """Top-k ids by (score descending, id ascending) (predictor_cpu.cpp:192-201)."""
+    scores = np.asarray(scores, dtype=np.float32)
+    order = np.lexsort((np.arange(len(scores)), -scores.astype(np.float64)))
+    return order[:k].astype(np.int64)
+
+
+@dataclass(frozen=True)
+class LayerConfig:
+    name: str
+    width: int               # d_model
+    ffn: int                 # d_ffn
+    active_frac: float
+    group_size: int = 64
+    batch: int = 1
+    scale_lo: float = 0.005
+    scale_hi: float = 0.02
+    selection: str = "ranking"   # "ranking" (N(0,1) scores, top-k) | "permutation" | "all"
+    seed: int = 0x1EA5_5EED
+
+    @property
+    def groups(self):
+        return self.ffn // self.group_size
+
+    @property
+    def active(self):
+        return int(np.floor(self.active_frac * self.groups + 0.5))
+
+    @property
+    def group_bytes(self):
+        return self.group_size * 3 * self.width // 2
+
+    @property
+    def scale_words(self):
+        """fp16 scales per group: G neurons x 3 projections x d/128 blocks."""
+        return self.group_size * 3 * (self.width // 128)
+
+    def sub_seed(self, tag):
+        return (self.seed * 0x100000001B3 + tag) & 0xFFFFFFFFFFFFFFFF
+
+    def algorithmic_bytes(self):
+        """INT4 weights + fp16 scales of the active groups + x in + y out."""
+        k, G, d = self.active, self.group_size, self.width
+        return k * G * (3 * d // 2) + k * G * 3 * (d // 128) * 2 + 2 * self.batch * d * 2
+
+
+CONFIGS = {
+    "c1": LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25", 1024, 4096, 0.25, selection="permutation",
+                      seed=0xC1),
+    "c2": LayerConfig("ministral8b_sparse_int4_mlp_d4096_f12288_a30_b1", 4096, 12288, 0.30, seed=0xC2),
+    "c4": LayerConfig("llama70b_sparse_int4_mlp_d8192_f28672_a20_b1", 8192, 28672, 0.20, scale_lo=0.003,
+                      scale_hi=0.015, seed=0xC4),
+}
+
+
+def physical_of(logical, groups):
+    """Fixed bijection logical -> physical (storage order differs from predictor ids)."""
+    return (np.asarray(logical, dtype=np.int64) * 37 + 11) % groups
+
+
+def active_groups(cfg):
+    """Logical ids of the active groups, in execution (rank / publication) order."""
+    if cfg.selection == "all":
+        return np.arange(cfg.groups, dtype=np.int64)
+    if cfg.selection == "permutation":
+        return permutation(cfg.groups, cfg.sub_seed(SEED_SCORE))[: cfg.active]
+    scores = normal_f64(cfg.groups, cfg.sub_seed(SEED_SCORE)).astype(np.float32)
+    return rank_top_k(scores, cfg.active)
+
+
+def group_scores(cfg):
+    return normal_f64(cfg.groups, cfg.sub_seed(SEED_SCORE)).astype(np.float32)
+
+
+def ready_order(count, cfg):
+    """Publication order of queue descriptors (a seeded permutation of 0..count-1)."""
+    return permutation(count, cfg.sub_seed(SEED_ORDER))
+
+
+@dataclass
+class HostLayer:
+    """A whole layer in host memory: cache arena in physical order, scales, x."""
+
+    cfg: LayerConfig
+    cache: np.ndarray = field(repr=False)    # uint8 [groups * group_bytes]
+    scales: np.ndarray = field(repr=False)   # float16 [groups * scale_words]
+    x: np.ndarray = field(repr=False)        # float16 [batch * width]
+
+
+def host_layer(cfg):
+    cache = fill_bytes(cfg.groups * cfg.group_bytes, cfg.sub_seed(SEED_W))
+    scales = uniform_f16(cfg.groups * cfg.scale_words, cfg.sub_seed(SEED_S), cfg.scale_lo, cfg.scale_hi)
+    x = normal_f16(cfg.batch * cfg.width, cfg.sub_seed(SEED_X))
+    return HostLayer(cfg, cache, scales, x)
+
+
+def descriptors(cfg, logical, source_kind=0, dest_base=0):
+    """ExecDesc rows (uint32 [n, 5]) for the given logical ids: source slot and scale
+    row are the physical group; destinations are dest_base + position."""
+    logical = np.asarray(logical, dtype=np.int64)
+    phys = physical_of(logical, cfg.groups)
+    out = np.zeros((len(logical), 5), dtype=np.uint32)
+    out[:, 0] = logical
+    out[:, 1] = phys
+    out[:, 2] = phys
+    out[:, 3] = dest_base + np.arange(len(logical))
+    out[:, 4] = source_kind
+    return out

@@ -1,0 +1,90 @@
+"""Device-resident sparse INT4 MLP layers for tests and benchmarks.
+
+Weights, scales and activations are generated on the GPU by the library's own
+generator kernels (identical to leanstream_amd.synth on the host). A layer can be
+replicated into several independent copies (different seeds, disjoint memory) so
+that a benchmark rotating over them reads HBM rather than the 256 MB Infinity Cache.
+"""
+import numpy as np
+
+from . import _native, synth
+from .backend import MODE_PROGRESSIVE, NativeBackend, ReadyQueue
+
+
+def _check(rc, what):
+    if rc:
+        raise RuntimeError(f"{what} failed: {rc}")
+
+
+class DeviceLayer:
+    def __init__(self, cfg, copies=1, logical=None, with_y32=True, diagnostics=True, queue_capacity=None,
+                 offline_table=None):
+        import torch
+
+        self.torch = torch
+        self.cfg = cfg
+        self.copies = copies
+        lib = _native.library()
+        dev = torch.device("cuda")
+        G, d, n = cfg.group_size, cfg.width, cfg.groups
+        stream = torch.cuda.current_stream().cuda_stream
+        self.cache = torch.empty(copies * n * cfg.group_bytes, dtype=torch.uint8, device=dev)
+        self.scales = torch.empty(copies * n * cfg.scale_words, dtype=torch.float16, device=dev)
+        self.x = torch.empty(cfg.batch * d, dtype=torch.float16, device=dev)
+        for c in range(copies):
+            _check(lib.ls_synth_bytes(self.cache.data_ptr() + c * n * cfg.group_bytes, n * cfg.group_bytes,
+                                      cfg.sub_seed(synth.SEED_W) + c * 0x1000, stream), "synth bytes")
+            _check(lib.ls_synth_uniform_f16(self.scales.data_ptr() + 2 * c * n * cfg.scale_words, n * cfg.scale_words,
+                                            cfg.sub_seed(synth.SEED_S) + c * 0x1000, cfg.scale_lo, cfg.scale_hi,
+                                            stream), "synth scales")
+        _check(lib.ls_synth_normal_f16(self.x.data_ptr(), cfg.batch * d, cfg.sub_seed(synth.SEED_X), stream),
+               "synth x")
+        self.logical = synth.active_groups(cfg) if logical is None else np.asarray(logical, dtype=np.int64)
+        k = len(self.logical)
+        self.k = k
+        rows = []
+        for c in range(copies):
+            r = synth.descriptors(cfg, self.logical)
+            r[:, 1] += c * n   # scale rows of copy c
+            r[:, 2] += c * n   # cache slots of copy c
+            rows.append(r)
+        self.core_rows = np.stack(rows)                     # [copies, k, 5]
+        self.core = torch.from_numpy(self.core_rows.reshape(-1).astype(np.int32)).to(dev)
+        self.slot_capacity = max(1, k)
+        self.y = torch.empty(cfg.batch * d, dtype=torch.float16, device=dev)
+        self.y32 = torch.empty(cfg.batch * d, dtype=torch.float32, device=dev) if with_y32 else None
+        self.hidden = torch.zeros(self.slot_capacity * G, dtype=torch.float32, device=dev)
+        self.partial = torch.zeros(self.slot_capacity * d, dtype=torch.float32, device=dev)
+        self.executions = torch.zeros(self.slot_capacity, dtype=torch.int32, device=dev) if diagnostics else None
+        self.queue = ReadyQueue(queue_capacity if queue_capacity else max(1, k))
+        self.backend = NativeBackend(offline_table)
+        self.backend.bind(d, G, self.slot_capacity, self.cache, self.scales, physical_groups=copies * n,
+                          cache_groups=copies * n, staging=self.cache, staging_groups=copies * n,
+                          queue_capacity=self.queue.capacity, hidden=self.hidden, partial=self.partial, y32=self.y32,
+                          executions=self.executions, batch=cfg.batch)
+        torch.cuda.synchronize()
+
+    def core_ptr(self, copy):
+        return self.core.data_ptr() + copy * self.k * 20
+
+    def seal_empty_queue(self, epoch):
+        self.queue.reset(epoch)
+        self.queue.seal(0)
+
+    def run_core(self, copy=0, epoch=1, layer=0, bucket=0, stream=None, mode=MODE_PROGRESSIVE):
+        """Enqueue one layer whose active groups are all resident core descriptors."""
+        torch = self.torch
+        s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        self.backend.enqueue(layer, bucket, epoch, self.x, self.y, s, self.core_ptr(copy), self.k, self.queue, mode)
+
+    def host_copy(self):
+        """Host (numpy) copies of copy 0: cache, scales, x."""
+        n = self.cfg.groups
+        cache = self.cache[: n * self.cfg.group_bytes].cpu().numpy()
+        scales = self.scales[: n * self.cfg.scale_words].cpu().numpy()
+        return cache, scales, self.x.cpu().numpy()
+
+    def close(self):
+        self.torch.cuda.synchronize()
+        self.backend.close()
+        self.queue.close()
