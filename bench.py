@@ -1,0 +1,207 @@
+#!/usr/bin/env python3
+"""Benchmark: microseconds per sparse INT4 MLP layer and achieved HBM bandwidth on one MI355X.
+
+Workload (one GPU, batch 1): Ministral-8B-shaped sparse MLP layer, d_model 4096,
+d_ffn 12288 = 192 groups of 64 neurons, 58 active groups (30%, seeded ranking), INT4 g128
+weights with fp16 scales U(0.005, 0.02), fp16 x ~ N(0, 1), all weights HBM-resident and
+every group ready before launch (resident core descriptors).
+
+A "step" is one enqueue of the layer (fused persistent kernel: gate/up, SiLU, down
+projection, compact reduction). Steps rotate over independent copies of the layer whose
+active bytes total more than the 256 MB Infinity Cache, so every step reads HBM.
+
+Printed: one JSON line (rank 0). value = microseconds per layer in the back-to-back
+pipeline (HIP events on the launch stream around the timed steps, divided by steps).
+roofline.achieved = algorithmic bytes per layer / that per-layer time.
+"""
+import argparse
+import json
+import math
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "µs per sparse INT4 MLP layer + achieved HBM GB/s (% roofline), batch 1, 8B shape"
+HBM_PEAK_GBS = 8000.0
+MALL_BYTES = 256 * 2 ** 20
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4"])
+    ap.add_argument("--candidate", type=int, default=None, help="force a kernel candidate id (offline LUT of one entry)")
+    ap.add_argument("--copies", type=int, default=0, help="layer copies to rotate over (0: enough to exceed 256 MB)")
+    ap.add_argument("--isolated", type=int, default=100, help="isolated launches timed one by one")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def percentile(v, q):
+    v = sorted(v)
+    if not v:
+        return None
+    k = (len(v) - 1) * q
+    lo, hi = math.floor(k), math.ceil(k)
+    return v[lo] + (v[hi] - v[lo]) * (k - lo)
+
+
+def traffic_from_profiles(workload_name):
+    """HBM bytes per launch measured with rocprofv3 PMC counters (committed summary)."""
+    f = ROOT / "profiles" / f"traffic_{workload_name}.txt"
+    if not f.is_file():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return int(float(line.split(":", 1)[1].strip()))
+            except ValueError:
+                return None
+    return None
+
+
+def cpu_baseline(cfg, budget_s):
+    """The oracle (CPU restatement of the reference arithmetic) timed on the host cores."""
+    import numpy as np
+
+    if not (ROOT / "oracle" / "liboracle.so").is_file():
+        subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+    import oracle
+    from leanstream_amd import synth
+
+    hl = synth.host_layer(cfg)
+    rows = synth.descriptors(cfg, synth.active_groups(cfg))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    out = {}
+    for label, nthreads, share in (("all", threads, 0.7), ("one", 1, 0.3)):
+        t_end = time.perf_counter() + budget_s * share
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            oracle.layer(rows, len(rows), hl.cache, hl.scales, hl.x, cfg.width, cfg.group_size, threads=nthreads)
+            n += 1
+            if time.perf_counter() >= t_end:
+                break
+        out[label] = ((time.perf_counter() - t0) / n * 1e6, n, nthreads)
+    us_all, n_all, t_all = out["all"]
+    us_one, n_one, _ = out["one"]
+    return {
+        "value": round(us_all, 1),
+        "unit": "us/layer",
+        "cores": t_all,
+        "kind": "port",
+        "sample": f"{n_all} full layers ({cfg.name}) with {t_all} OpenMP threads; single thread: {us_one:.0f} us/layer "
+                  f"over {n_one} layers",
+        "gbs": round(cfg.algorithmic_bytes() / us_all / 1e3, 2),
+        "single_thread_us": round(us_one, 1),
+    }
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        sys.exit(2)
+    import torch
+
+    from leanstream_amd import synth
+    from leanstream_amd.workload import DeviceLayer
+
+    cfg = synth.CONFIGS[a.workload]
+    active_bytes = cfg.active * cfg.group_bytes + cfg.active * cfg.scale_words * 2
+    copies = a.copies or max(2, math.ceil(1.5 * MALL_BYTES / active_bytes))
+    table = None if a.candidate is None else [[a.candidate]]
+    print(f"[bench] workload {cfg.name}: k={cfg.active} B_alg={cfg.algorithmic_bytes()} copies={copies}",
+          file=sys.stderr, flush=True)
+    layer = DeviceLayer(cfg, copies=copies, with_y32=False, diagnostics=False, offline_table=table)
+    layer.seal_empty_queue(1)
+    stream = torch.cuda.current_stream()
+    for i in range(a.warmup):
+        layer.run_core(copy=i % copies, epoch=1)
+    torch.cuda.synchronize()
+    assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
+    print(f"[bench] warmup done, timing {a.steps} steps", file=sys.stderr, flush=True)
+
+    # back-to-back pipeline: events on the launch stream around the timed steps
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(a.steps):
+        layer.run_core(copy=i % copies, epoch=1)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    ms_total = start.elapsed_time(stop)
+    us_per_layer = ms_total * 1000.0 / a.steps
+
+    # isolated layers: one event pair per launch, idle GPU between launches
+    iso = []
+    for i in range(a.isolated):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        layer.run_core(copy=i % copies, epoch=1)
+        e1.record(stream)
+        e1.synchronize()
+        iso.append(e0.elapsed_time(e1) * 1000.0)
+    status = layer.backend.status()
+    candidate = layer.backend.last_candidate()
+    workers = layer.backend.max_workers
+    layer.close()
+    assert status == 0, f"device status {status}"
+
+    balg = cfg.algorithmic_bytes()
+    achieved = balg / us_per_layer / 1e3  # GB/s
+    traffic = traffic_from_profiles(cfg.name)
+    result = {
+        "metric": METRIC,
+        "value": round(us_per_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_total / a.steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16-f32acc",
+        "data": "synthetic (seeded splitmix64 INT4 weights, U(lo,hi) fp16 scales, N(0,1) fp16 x)",
+        "config": {
+            "workload": cfg.name,
+            "d_model": cfg.width,
+            "d_ffn": cfg.ffn,
+            "group_size": cfg.group_size,
+            "active_groups": cfg.active,
+            "batch": cfg.batch,
+            "algorithmic_bytes": balg,
+            "rotation_copies": copies,
+            "rotation_active_bytes": copies * active_bytes,
+            "candidate": candidate,
+            "resident_workers": workers,
+            "isolated_us_p10_p50_p90": [round(percentile(iso, q), 3) for q in (0.1, 0.5, 0.9)],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+    }
+    if not a.no_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds)
+        except Exception as exc:  # the GPU figure stands on its own
+            result["cpu_baseline"] = {"value": None, "error": str(exc)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

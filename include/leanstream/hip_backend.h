@@ -52,6 +52,7 @@ struct HipLayerBuffers {
     uint32_t* executions = nullptr;     // optional per-destination execution counts
     uint64_t* first_compute = nullptr;  // optional per-destination start stamps
     uint32_t* claim_log = nullptr;      // optional claim log (queue positions)
+    uint64_t* stamps = nullptr;         // optional per-worker phase stamps [max workers][32]
 };
 
 class HipBackend {

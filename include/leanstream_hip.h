@@ -56,6 +56,7 @@ typedef struct ls_hip_layer_buffers {
     uint32_t* executions;
     uint64_t* first_compute;
     uint32_t* claim_log;
+    uint64_t* stamps;
 } ls_hip_layer_buffers;
 
 /* Consumer modes (leanstream::runtime::ConsumerMode). */

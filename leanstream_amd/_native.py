@@ -34,7 +34,7 @@ class LayerBuffers(C.Structure):
     _fields_ = [("width", u32), ("group_size", u32), ("batch", u32), ("slot_capacity", u32),
                 ("cache_groups", u32), ("staging_groups", u32), ("physical_groups", u32), ("queue_capacity", u32),
                 ("cache", p), ("staging", p), ("scales", p), ("hidden", p), ("partial", p), ("y32", p),
-                ("executions", p), ("first_compute", p), ("claim_log", p)]
+                ("executions", p), ("first_compute", p), ("claim_log", p), ("stamps", p)]
 
 
 _SIGNATURES = [

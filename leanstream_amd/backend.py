@@ -157,14 +157,14 @@ class NativeBackend:
 
     def bind(self, width, group_size, slot_capacity, cache, scales, physical_groups, cache_groups, staging=None,
              staging_groups=0, queue_capacity=0, hidden=None, partial=None, y32=None, executions=None,
-             first_compute=None, claim_log=None, batch=1):
+             first_compute=None, claim_log=None, batch=1, stamps=None):
         b = LayerBuffers(width, group_size, batch, slot_capacity, cache_groups, staging_groups, physical_groups,
                          queue_capacity, _ptr(cache), _ptr(staging), _ptr(scales), _ptr(hidden), _ptr(partial),
-                         _ptr(y32), _ptr(executions), _ptr(first_compute), _ptr(claim_log))
+                         _ptr(y32), _ptr(executions), _ptr(first_compute), _ptr(claim_log), _ptr(stamps))
         rc = self.lib.ls_hip_bind(self.context, C.byref(b))
         if rc:
             raise RuntimeError(f"Native bind failed: {rc}")
-        self._bound = (b, cache, scales, staging, hidden, partial, y32, executions, first_compute, claim_log)
+        self._bound = (b, cache, scales, staging, hidden, partial, y32, executions, first_compute, claim_log, stamps)
 
     def enqueue(self, layer, io_bucket, epoch, x, y, stream, core, core_count, queue, mode=MODE_PROGRESSIVE):
         rc = self.lib.ls_hip_enqueue(self.context, layer, io_bucket, epoch, _ptr(x), _ptr(y), stream, _ptr(core),

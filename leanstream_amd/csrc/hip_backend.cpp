@@ -16,6 +16,7 @@ struct HipBackend::Impl {
     lsamd::MlpArgs base{};
     lsamd::Bounds bounds{};
     uint32_t* sync = nullptr;
+    uint32_t* qmirror = nullptr;  // device copy of published queue descriptors
     uint32_t slot_words = 0;
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
@@ -29,11 +30,13 @@ struct HipBackend::Impl {
 
     void release() {
         if (sync) (void)hipFree(sync);
+        if (qmirror) (void)hipFree(qmirror);
         if (owned_hidden) (void)hipFree(owned_hidden);
         if (owned_partial) (void)hipFree(owned_partial);
         if (status) (void)hipHostFree(status);
         if (done) (void)hipEventDestroy(done);
         sync = nullptr;
+        qmirror = nullptr;
         owned_hidden = owned_partial = nullptr;
         status = nullptr;
         done = nullptr;
@@ -80,6 +83,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     const uint32_t units_cap = b.slot_capacity + b.queue_capacity;
     p.slot_words = lsamd::sync_slot_words(units_cap);
     hipError_t e = hipMalloc(&p.sync, sizeof(uint32_t) * 2 * p.slot_words);
+    if (e == hipSuccess) e = hipMalloc(&p.qmirror, sizeof(uint32_t) * 5 * std::max<uint32_t>(1, b.queue_capacity));
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
     if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(float) * b.slot_capacity * b.group_size);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
@@ -109,7 +113,9 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.first_compute = b.first_compute;
     a.claim_log = b.claim_log;
     a.claim_log_cap = b.claim_log ? b.queue_capacity : 0;
+    a.stamps = b.stamps;
     a.sync = p.sync;
+    a.qmirror = p.qmirror;
     a.status = p.status;
     a.group_size = b.group_size;
     a.slices = S;
@@ -119,7 +125,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
     slices_ = S;
     ns_ = ns;
-    max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused);
+    max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused) - 1;
     p.needs_clear = false;
     p.recorded = false;
     p.bound = true;
@@ -134,8 +140,9 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     const KernelCandidate c = selector_.candidate(selector_.select(s));
     const int entry = c.entry_point == lsamd::kEntrySplit ? lsamd::kEntrySplit : lsamd::kEntryFused;
     const int per_cu = entry == lsamd::kEntryFused ? p.per_cu_fused : p.per_cu_split;
-    // Persistent workers must be co-resident: items of one unit wait for each other.
-    const uint32_t resident = static_cast<uint32_t>(p.cus * per_cu);
+    // Persistent workers (plus the mirror workgroup) must be co-resident: items of one
+    // unit wait for each other.
+    const uint32_t resident = static_cast<uint32_t>(p.cus * per_cu) - 1;
     const uint32_t workers = std::max<uint32_t>(1, std::min<uint32_t>(c.workers ? c.workers : resident, resident));
     lsamd::MlpArgs a = p.base;
     a.core = core.data;

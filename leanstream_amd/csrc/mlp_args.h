@@ -18,12 +18,22 @@ enum SyncWord : uint32_t {
     kSyncClaimHead = 2,  // next unclaimed ready position (claim path)
     kSyncAbort = 3,      // set on queue error or spin timeout: every worker leaves
     kSyncClaims = 4,     // number of successful claims (claim path)
+    kSyncEpochState = 5, // mirror: 0 not yet seen, 1 epoch published, 2 leave (error / abort / timeout)
+    kSyncTotal = 6,      // mirror: final queue total_count
+    kSyncReady = 7,      // mirror: published positions copied into qmirror
     kSyncTiles = 16,     // [kMaxSlices] completed down-projection tiles per column tile
 };
 constexpr uint32_t kMaxSlices = 64;
 constexpr uint32_t kSyncUnits = kSyncTiles + kMaxSlices;  // [units] gate/up slices done per unit
 // then [units] down tiles done per unit, then [units] claim log entries
 inline uint32_t sync_slot_words(uint32_t units) { return kSyncUnits + 3 * units; }
+
+// Phase stamps written by thread 0 of each worker when MlpArgs::stamps is set.
+constexpr uint32_t kStampSlots = 32;
+enum StampPhase : uint32_t {
+    kStampEntry = 0, kStampXLoaded = 1, kStampFinish = 30, kStampExit = 31,
+    kStampItemBase = 2,  // + 7 * item (items 0..3): start, gu done, siblings, dn done, stored, counted, reduced
+};
 
 // Status word bits (host-coherent, sticky until cleared by the host).
 enum StatusBit : uint32_t { kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u };
@@ -39,6 +49,7 @@ struct MlpArgs {
     uint32_t core_count;
     const ExecDesc* qdesc;        // queue descriptors (final order)
     const uint32_t* ready;        // ready_indices (publication order)
+    uint32_t* qmirror;            // device copy of published descriptors, in publication order [capacity][5]
     QueueControl* control;        // host-coherent control block
     uint32_t capacity;
     // data
@@ -56,6 +67,7 @@ struct MlpArgs {
     uint32_t* status;             // host-coherent sticky status word
     uint32_t* claim_log;          // optional: per-claim (head | (len << 24)), in claim order
     uint32_t claim_log_cap;       // entries in claim_log
+    uint64_t* stamps;             // optional: per-worker phase stamps [workers][kStampSlots] (100 MHz clock)
     // geometry / control
     uint32_t group_size;          // G
     uint32_t slices;              // S: work items per unit (G/S neurons, d/S columns each)

@@ -110,6 +110,10 @@ struct Waiter {
     __device__ bool expired() const { return now_ticks() - start > limit; }
 };
 
+__device__ __forceinline__ void stamp(const MlpArgs& a, uint32_t k) {
+    if (a.stamps && threadIdx.x == 0 && k < kStampSlots) a.stamps[blockIdx.x * kStampSlots + k] = now_ticks();
+}
+
 __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, uint32_t bit) {
     __hip_atomic_fetch_or(a.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     st_agent(slot + kSyncAbort, 1u);
@@ -367,47 +371,39 @@ struct Shared {
     uint32_t ep_known, ep_ok, ep_total, ep_path;
 };
 
-__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t pre);
+__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t);
 
-// Thread 0 reads the published descriptor once (two dependent system-scope reads) and
-// shares it with the workgroup.
-__device__ ExecDesc load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t pos) {
-    __syncthreads();  // previous readers of sh.desc are done
-    if (threadIdx.x == 0) {
-        const ExecDesc d = load_queue(a, pos);
-        sh.desc[0] = d.logical_group;
-        sh.desc[1] = d.physical_group;
-        sh.desc[2] = d.source_slot;
-        sh.desc[3] = d.dest_slot;
-        sh.desc[4] = (uint32_t)d.source_kind;
-    }
-    __syncthreads();
-    ExecDesc d;
-    d.logical_group = sh.desc[0];
-    d.physical_group = sh.desc[1];
-    d.source_slot = sh.desc[2];
-    d.dest_slot = sh.desc[3];
-    d.source_kind = (leanstream::runtime::SourceKind)sh.desc[4];
-    return d;
+// Reduce one column tile over destination rows 0..U-1 in slot order. Each thread owns
+// two adjacent columns and keeps 16 rows of loads in flight before adding them in order.
+__device__ __forceinline__ uint64_t ld_agent64(const float* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Reduce one column tile over destination rows 0..U-1 in slot order.
 template <int D>
 __device__ void reduce_tile(const MlpArgs& a, int c0, int tc, uint32_t U) {
-    for (int c = threadIdx.x; c < tc; c += kThreads) {
+    constexpr uint32_t kBatch = 16;
+    for (int c = 2 * threadIdx.x; c < tc; c += 2 * kThreads) {
         const int col = c0 + c;
-        float v = 0.f;
-        uint32_t i = 0;
-        for (; i + 4 <= U; i += 4) {
-            const float p0 = ldf_agent(a.partial + (size_t)(i + 0) * D + col);
-            const float p1 = ldf_agent(a.partial + (size_t)(i + 1) * D + col);
-            const float p2 = ldf_agent(a.partial + (size_t)(i + 2) * D + col);
-            const float p3 = ldf_agent(a.partial + (size_t)(i + 3) * D + col);
-            v += p0; v += p1; v += p2; v += p3;
+        float v0 = 0.f, v1 = 0.f;
+        for (uint32_t i0 = 0; i0 < U; i0 += kBatch) {
+            uint64_t buf[kBatch];
+#pragma unroll
+            for (uint32_t r = 0; r < kBatch; ++r)
+                buf[r] = i0 + r < U ? ld_agent64(a.partial + (size_t)(i0 + r) * D + col) : 0ull;
+#pragma unroll
+            for (uint32_t r = 0; r < kBatch; ++r) {
+                if (i0 + r < U) {
+                    v0 += __uint_as_float((uint32_t)buf[r]);
+                    v1 += __uint_as_float((uint32_t)(buf[r] >> 32));
+                }
+            }
         }
-        for (; i < U; ++i) v += ldf_agent(a.partial + (size_t)i * D + col);
-        if (a.y32) a.y32[col] = v;
-        a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+        if (a.y32) {
+            a.y32[col] = v0;
+            a.y32[col + 1] = v1;
+        }
+        a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+        a.y[col + 1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
     }
 }
 
@@ -418,7 +414,9 @@ __device__ void reduce_tile(const MlpArgs& a, int c0, int tc, uint32_t U) {
 // ---------------------------------------------------------------------------------
 template <int D, int NS, bool FUSED>
 __device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Unit& u,
-                         uint32_t unit, uint32_t j, bool cooperative, uint64_t pre) {
+                         uint32_t unit, uint32_t j, bool cooperative, uint64_t pre, uint32_t it) {
+    const uint32_t sb = kStampItemBase + 7 * (it < 4 ? it : 4);
+    stamp(a, sb + 0);
     const int G = a.group_size;
     const int S = a.slices;
     const int tc = D / S;
@@ -433,6 +431,7 @@ __device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRe
     gu_compute<D, NS>(gl, xr, hrow, j * NS);
     drain_vmem();
     __syncthreads();
+    stamp(a, sb + 1);
     if (cooperative) {
         if (threadIdx.x == 0) {
             add_agent(slot + kSyncUnits + unit, 1u);
@@ -448,13 +447,16 @@ __device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRe
         __syncthreads();
         if (!sh.word[0]) return;
     }
+    stamp(a, sb + 2);
     for (int n = threadIdx.x; n < G; n += kThreads) sh.hs[n] = ldf_agent(hrow + n);
     __syncthreads();
     dn_compute(dl, gm, sh.hs, sh.red, tc);
+    stamp(a, sb + 3);
     float* prow = a.partial + (size_t)u.dest * D + c0;
     for (int c = threadIdx.x; c < tc; c += kThreads) stf_agent(prow + c, sh.red[kRedFloats + c]);
     drain_vmem();
     __syncthreads();
+    stamp(a, sb + 4);
     // The tile counter target is U = core + queue total, final once the epoch is seen.
     if (FUSED && !await_epoch(a, sh, slot, pre)) return;
     const uint32_t U = a.core_count + sh.ep_total;
@@ -468,7 +470,9 @@ __device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRe
         sh.word[1] = last;
     }
     __syncthreads();
+    stamp(a, sb + 5);
     if (FUSED && sh.word[1]) reduce_tile<D>(a, c0, tc, U);
+    stamp(a, sb + 6);
 }
 
 // Process a whole unit inside one workgroup (claim path): no cross-workgroup wait.
@@ -514,57 +518,124 @@ __device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
 
 // ---------------------------------------------------------------------------------
 // Queue protocol (LeanStream kernels/streaming_mlp.cu:47-79, backends/triton/persistent.py:32-92):
-// wait for the layer epoch (or an error), optionally for batch publication, then
-// decide once per launch between the all-ready fast path and the claim path.
-// Returns false when the worker must leave (error / abort / timeout).
+// wait for the layer epoch (or an error), optionally for batch publication, decide once
+// per launch between the all-ready fast path and the claim path, then consume published
+// positions in order.
+//
+// On MI355X the queue lives in host memory behind PCIe, where concurrent reads from
+// hundreds of workgroups are served one after another. So exactly one workgroup of
+// each launch (the mirror, the last block) reads host memory: it publishes
+// (epoch state, total, path) into the device ring slot, copies every newly published
+// position's descriptor into a device-side table in publication order (64 positions
+// per round trip, one per lane) and advances a device-side ready count. Workers only
+// poll device memory.
 // ---------------------------------------------------------------------------------
-// `pre` is thread 0's early 64-bit snapshot of (total_count, epoch): the two words
-// are adjacent (byte offsets 8 and 12), so one load returns a consistent pair and
-// its PCIe latency overlaps the first item's work.
-__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t pre) {
+__device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __shfl(v, 0, 64); }
+
+// Runs on wave 0 of the mirror workgroup. `pre` is lane 0's early 64-bit load of
+// (total_count, epoch): adjacent words (byte offsets 8 and 12), read as one pair.
+__device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t state = 0, total = 0;
+    if (lane == 0) {
+        Waiter wt(a.spin_limit);
+        uint64_t te = pre;
+        for (;;) {
+            if ((uint32_t)(te >> 32) == a.epoch) { state = 1; break; }
+            if (ld_sys(&a.control->error)) { state = 2; st_agent(slot + kSyncAbort, 1u); break; }
+            if (ld_agent(slot + kSyncAbort)) { state = 2; break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); state = 2; break; }
+            __builtin_amdgcn_s_sleep(8);
+            te = ld_sys64(&a.control->total_count);
+        }
+        total = state == 1 ? (uint32_t)te : 0;
+        if (state == 1 && (total > a.capacity || a.core_count + total > a.slot_capacity)) {
+            raise_status(a, slot, kStatusBadDescriptor);
+            state = 2;
+        }
+        if (state == 1 && total && a.batch_mode) {
+            Waiter wb(a.spin_limit);
+            for (;;) {
+                if (ld_sys(&a.control->batch_epoch) == a.epoch) break;
+                if (ld_sys(&a.control->error)) { state = 2; st_agent(slot + kSyncAbort, 1u); break; }
+                if (ld_agent(slot + kSyncAbort)) { state = 2; break; }
+                if (wb.expired()) { raise_status(a, slot, kStatusTimeout); state = 2; break; }
+                __builtin_amdgcn_s_sleep(8);
+            }
+        }
+        uint32_t path = 0;
+        if (state == 1 && total) path = ld_sys(&a.control->ready_count) >= total ? 2u : 1u;
+        st_agent(slot + kSyncTotal, state == 1 ? total : 0u);
+        st_agent(slot + kSyncPath, path);
+        drain_vmem();
+        st_agent(slot + kSyncEpochState, state);
+    }
+    state = wave_bcast(state);
+    total = wave_bcast(total);
+    if (state != 1) return;
+    uint32_t mirrored = 0;
+    Waiter wt(a.spin_limit);
+    while (mirrored < total) {
+        uint32_t ready = 0, stop = 0;
+        if (lane == 0) {
+            ready = min(ld_sys(&a.control->ready_count), total);
+            if (ld_sys(&a.control->error)) {
+                st_agent(slot + kSyncAbort, 1u);
+                stop = 1;
+            } else if (ld_agent(slot + kSyncAbort)) {
+                stop = 1;
+            }
+        }
+        ready = wave_bcast(ready);
+        if (wave_bcast(stop)) return;
+        if (ready > mirrored) {
+            for (uint32_t base = mirrored; base < ready; base += 64) {
+                const uint32_t pos = base + lane;
+                if (pos < ready) {
+                    const uint32_t idx = ld_sys(a.ready + pos);
+                    const uint32_t* d = reinterpret_cast<const uint32_t*>(a.qdesc + (idx < a.capacity ? idx : 0));
+                    uint32_t w[5];
+#pragma unroll
+                    for (int k = 0; k < 5; ++k) w[k] = ld_sys(d + k);
+                    if (idx >= a.capacity) w[3] = 0xffffffffu;  // fails validation on the consumer side
+#pragma unroll
+                    for (int k = 0; k < 5; ++k) st_agent(a.qmirror + 5 * pos + k, w[k]);
+                }
+            }
+            drain_vmem();  // the whole wave's copies are complete before the count moves
+            if (lane == 0) st_agent(slot + kSyncReady, ready);
+            mirrored = ready;
+            wt = Waiter(a.spin_limit);  // the bound applies to waiting without progress
+        } else {
+            if (wt.expired()) {
+                if (lane == 0) raise_status(a, slot, kStatusTimeout);
+                return;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+}
+
+// Worker side: (ok, total, path) from the ring slot, learnt once per workgroup.
+__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t) {
     // Every thread reads the flag before thread 0 may write it (barrier in between),
     // so the whole workgroup takes the same branch.
     const uint32_t known = sh.ep_known;
     __syncthreads();
     if (known) return sh.ep_ok != 0;
     if (threadIdx.x == 0) {
-        uint32_t ok = 1;
-        uint64_t te = pre;
         Waiter wt(a.spin_limit);
+        uint32_t state = 0;
         for (;;) {
-            if ((uint32_t)(te >> 32) == a.epoch) break;
-            if (ld_sys(&a.control->error)) { ok = 0; break; }
-            if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
-            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
-            __builtin_amdgcn_s_sleep(8);
-            te = ld_sys64(&a.control->total_count);
+            state = ld_agent(slot + kSyncEpochState);
+            if (state) break;
+            if (ld_agent(slot + kSyncAbort)) { state = 2; break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); state = 2; break; }
+            __builtin_amdgcn_s_sleep(2);
         }
-        uint32_t total = ok ? (uint32_t)te : 0;
-        if (ok && (total > a.capacity || a.core_count + total > a.slot_capacity)) {
-            raise_status(a, slot, kStatusBadDescriptor);
-            ok = 0;
-        }
-        if (ok && total && a.batch_mode) {
-            Waiter wb(a.spin_limit);
-            for (;;) {
-                if (ld_sys(&a.control->batch_epoch) == a.epoch) break;
-                if (ld_sys(&a.control->error)) { ok = 0; break; }
-                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
-                if (wb.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
-                __builtin_amdgcn_s_sleep(8);
-            }
-        }
-        uint32_t path = 0;
-        if (ok && total) {
-            const uint32_t proposed = ld_sys(&a.control->ready_count) == total ? 2u : 1u;
-            uint32_t expected = 0;
-            __hip_atomic_compare_exchange_strong(slot + kSyncPath, &expected, proposed, __ATOMIC_RELAXED,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            path = ld_agent(slot + kSyncPath);
-        }
-        sh.ep_ok = ok;
-        sh.ep_total = total;
-        sh.ep_path = path;
+        sh.ep_ok = state == 1;
+        sh.ep_total = state == 1 ? ld_agent(slot + kSyncTotal) : 0u;
+        sh.ep_path = state == 1 ? ld_agent(slot + kSyncPath) : 0u;
         sh.ep_known = 1;
     }
     __syncthreads();
@@ -576,15 +647,41 @@ __device__ __forceinline__ void init_shared(Shared& sh) {
     __syncthreads();
 }
 
-// Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86).
-// Returns the number of claimed positions (0 = leave) and the head in sh.word[5].
+// Descriptor of published position `pos` from the device-side table; false when the
+// worker must leave (abort or timeout) before the position is mirrored.
+__device__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out) {
+    __syncthreads();  // previous readers of sh.desc / sh.word[2] are done
+    if (threadIdx.x == 0) {
+        uint32_t ok = 1;
+        Waiter wt(a.spin_limit);
+        while (ld_agent(slot + kSyncReady) <= pos) {
+            if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (ok)
+            for (int k = 0; k < 5; ++k) sh.desc[k] = ld_agent(a.qmirror + 5 * pos + k);
+        sh.word[2] = ok;
+    }
+    __syncthreads();
+    out->logical_group = sh.desc[0];
+    out->physical_group = sh.desc[1];
+    out->source_slot = sh.desc[2];
+    out->dest_slot = sh.desc[3];
+    out->source_kind = (leanstream::runtime::SourceKind)sh.desc[4];
+    return sh.word[2] != 0;
+}
+
+// Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86),
+// against the mirrored ready count. Returns the number of claimed positions (0 = leave).
 __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total) {
+    __syncthreads();  // previous readers of sh.word[5..6] are done
     if (threadIdx.x == 0) {
         uint32_t got = 0, head = 0;
         Waiter wt(a.spin_limit);
         for (;;) {
             if (ld_agent(slot + kSyncAbort)) break;
-            const uint32_t ready = ld_sys(&a.control->ready_count);
+            const uint32_t ready = ld_agent(slot + kSyncReady);
             head = ld_agent(slot + kSyncClaimHead);
             if (head >= total) break;
             if (head < ready) {
@@ -595,13 +692,13 @@ __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uin
                     got = end - head;
                     const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
                     if (a.claim_log && seq < a.claim_log_cap) a.claim_log[seq] = head | (got << 24);
+                    wt = Waiter(a.spin_limit);
                     break;
                 }
                 continue;
             }
-            if (ld_sys(&a.control->error)) { st_agent(slot + kSyncAbort, 1u); break; }
             if (wt.expired()) { raise_status(a, slot, kStatusTimeout); break; }
-            __builtin_amdgcn_s_sleep(4);
+            __builtin_amdgcn_s_sleep(2);
         }
         sh.word[5] = head;
         sh.word[6] = got;
@@ -612,28 +709,29 @@ __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uin
 
 template <int D, int NS, bool FUSED>
 __device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Bounds& b,
-                              uint32_t W, uint32_t w, uint32_t first_item, uint64_t pre) {
-    if (!await_epoch(a, sh, slot, pre)) return;
+                              uint32_t W, uint32_t w, uint32_t first_item, uint32_t it) {
+    if (!await_epoch(a, sh, slot, 0)) return;
     const uint32_t total = sh.ep_total;
     const uint32_t path = sh.ep_path;
     if (!total) return;
     const uint32_t U = a.core_count + total;
     const uint32_t S = a.slices;
     if (path == 2) {
-        (void)U;
         // all ready: static stripes of (position, slice) items, continuing the
         // round-robin after the core items so every worker gets an equal share.
         const uint32_t n_items = total * S;
         for (uint32_t i = (w + W - (first_item % W)) % W; i < n_items; i += W) {
             const uint32_t pos = i / S, j = i % S;
-            const Unit u = resolve(a, b, load_queue_wg(a, sh, pos), D);
+            ExecDesc d;
+            if (!load_queue_wg(a, sh, slot, pos, &d)) return;
+            const Unit u = resolve(a, b, d, D);
             if (!u.ok) {
                 if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
                 return;
             }
             if (threadIdx.x == 0 && j == 0 && a.claim_log && (pos & 1) == 0 && pos / 2 < a.claim_log_cap)
                 a.claim_log[pos / 2] = pos | (min(2u, total - pos) << 24);
-            run_item<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + pos, j, true, pre);
+            run_item<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + pos, j, true, 0, it++);
         }
         return;
     }
@@ -642,7 +740,9 @@ __device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
         if (!got) return;
         const uint32_t head = sh.word[5];
         for (uint32_t k = 0; k < got; ++k) {
-            const Unit u = resolve(a, b, load_queue_wg(a, sh, head + k), D);
+            ExecDesc d;
+            if (!load_queue_wg(a, sh, slot, head + k, &d)) return;
+            const Unit u = resolve(a, b, d, D);
             if (!u.ok) {
                 if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
                 return;
@@ -652,29 +752,33 @@ __device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
     }
 }
 
-// Last worker of a launch: clear the other ring slot for the next launch and, for an
+// Last workgroup of a launch: clear the other ring slot for the next launch and, for an
 // empty layer (no rows at all), write the zero output the reduction would produce.
 template <int D>
-__device__ void finish_launch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t W, bool fused) {
+__device__ void finish_launch(const MlpArgs& a, Shared& sh, uint32_t* slot, bool fused) {
     __syncthreads();
-    if (threadIdx.x == 0) sh.word[7] = add_agent(slot + kSyncExit, 1u) + 1 == W;
+    if (threadIdx.x == 0) sh.word[7] = add_agent(slot + kSyncExit, 1u) + 1 == gridDim.x;
     __syncthreads();
     if (!sh.word[7]) return;
     uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
     for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
-    if (fused && a.core_count == 0 && !ld_agent(slot + kSyncAbort)) {
-        // U == 0 only if the queue turned out empty; the queue total is final here.
-        const uint32_t total = ld_sys(&a.control->total_count);
-        if (total == 0 && ld_sys(&a.control->epoch) == a.epoch)
-            for (int c = threadIdx.x; c < D; c += kThreads) {
-                if (a.y32) a.y32[c] = 0.f;
-                a.y[c] = 0;
-            }
-    }
+    // Every other workgroup (the mirror included) has finished: the slot words are final.
+    if (fused && a.core_count == 0 && ld_agent(slot + kSyncEpochState) == 1 && ld_agent(slot + kSyncTotal) == 0 &&
+        !ld_agent(slot + kSyncAbort))
+        for (int c = threadIdx.x; c < D; c += kThreads) {
+            if (a.y32) a.y32[c] = 0.f;
+            a.y[c] = 0;
+        }
+}
+
+// The mirror workgroup: wave 0 mirrors, the other waves wait at the barrier.
+__device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
+    if (threadIdx.x < 64) mirror_queue(a, slot, pre);
+    __syncthreads();
 }
 
 // ---------------------------------------------------------------------------------
-// Kernels
+// Kernels. Persistent launches have gridDim.x = workers + 1; the last block mirrors.
 // ---------------------------------------------------------------------------------
 
 // Fused layer: core items (stage A role), queue consumption (stage B role) and the
@@ -683,13 +787,21 @@ template <int D, int NS>
 __global__ __launch_bounds__(kThreads) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+    const uint32_t W = gridDim.x - 1, w = blockIdx.x;
+    if (w == W) {
+        const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+        run_mirror(a, slot, pre);
+        finish_launch<D>(a, sh, slot, true);
+        return;
+    }
+    stamp(a, kStampEntry);
     init_shared(sh);
-    const uint32_t W = gridDim.x, w = blockIdx.x;
     XRegs<D, NS> xr;
     load_x<D, NS>(a.x, xr);
     const uint32_t S = a.slices;
     const uint32_t n_core = a.core_count * S;
+    stamp(a, kStampXLoaded);
+    uint32_t it = 0;
     for (uint32_t i = w; i < n_core; i += W) {
         const uint32_t unit = i / S, j = i % S;
         const Unit u = resolve(a, b, load_core(a, unit), D);
@@ -697,10 +809,12 @@ __global__ __launch_bounds__(kThreads) void fused_layer_kernel(MlpArgs a, Bounds
             if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
             break;
         }
-        run_item<D, NS, true>(a, sh, slot, xr, u, unit, j, true, pre);
+        run_item<D, NS, true>(a, sh, slot, xr, u, unit, j, true, 0, it++);
     }
-    consume_queue<D, NS, true>(a, sh, slot, xr, b, W, w, n_core, pre);
-    finish_launch<D>(a, sh, slot, W, true);
+    consume_queue<D, NS, true>(a, sh, slot, xr, b, W, w, n_core, it);
+    stamp(a, kStampFinish);
+    finish_launch<D>(a, sh, slot, true);
+    stamp(a, kStampExit);
 }
 
 // Split path, stage A: core items only (no queue, no reduction).
@@ -720,28 +834,34 @@ __global__ __launch_bounds__(kThreads) void stage_a_kernel(MlpArgs a, Bounds b) 
             if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
             return;
         }
-        run_item<D, NS, false>(a, sh, slot, xr, u, unit, j, true, 0);
+        run_item<D, NS, false>(a, sh, slot, xr, u, unit, j, true, 0, 0);
     }
 }
 
-// Split path, stage B: persistent ready-queue consumer.
+// Split path, stage B: persistent ready-queue consumer (last block mirrors).
 template <int D, int NS>
 __global__ __launch_bounds__(kThreads) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+    const uint32_t W = gridDim.x - 1;
+    if (blockIdx.x == W) {
+        const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
+        run_mirror(a, slot, pre);
+        return;
+    }
     init_shared(sh);
     XRegs<D, NS> xr;
     load_x<D, NS>(a.x, xr);
-    consume_queue<D, NS, false>(a, sh, slot, xr, b, gridDim.x, blockIdx.x, 0, pre);
+    consume_queue<D, NS, false>(a, sh, slot, xr, b, W, blockIdx.x, 0, 0);
 }
 
-// Split path, compact reduction over rows 0..core+total-1 (streaming_mlp.cu:80-84).
-// Block 0 also clears the other ring slot for the next launch.
+// Split path, compact reduction over rows 0..core+total-1 (streaming_mlp.cu:80-84), with
+// the total mirrored by stage B. Block 0 also clears the other ring slot.
 template <int D>
 __global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
-    const uint32_t total = ld_sys(&a.control->total_count);
-    uint32_t U = a.core_count + (total <= a.capacity ? total : 0);
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    const uint32_t state = ld_agent(slot + kSyncEpochState);
+    uint32_t U = a.core_count + (state == 1 ? ld_agent(slot + kSyncTotal) : 0u);
     if (U > a.slot_capacity) U = a.slot_capacity;
     const int c0 = blockIdx.x * kThreads;
     reduce_tile<D>(a, c0, kThreads, U);
@@ -814,7 +934,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     Bounds b = bounds;
     void* kargs[] = {&a, &b};
     if (p.entry_point == kEntryFused)
-        return hipLaunchKernel(v->fused, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+        return hipLaunchKernel(v->fused, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     hipError_t e = hipSuccess;
     const uint32_t core_items = a.core_count * a.slices;
     if (core_items) {
@@ -822,7 +942,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
         e = hipLaunchKernel(v->stage_a, dim3(grid), dim3(kThreads), kargs, 0, stream);
         if (e != hipSuccess) return e;
     }
-    e = hipLaunchKernel(v->stage_b, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+    e = hipLaunchKernel(v->stage_b, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
     return hipLaunchKernel(v->reduce, dim3(p.width / kThreads), dim3(kThreads), rargs, 0, stream);
