@@ -26,7 +26,7 @@ inline constexpr KernelCandidate kHipCandidates[] = {
     {4, 512, "hip_split_w512", 512, 0, 0, 0, 1},
 };
 inline constexpr uint32_t kHipCandidateCount = 5;
-inline constexpr KernelCandidate kHipDefault = kHipCandidates[0];
+inline constexpr KernelCandidate kHipDefault = kHipCandidates[1];
 inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexcept {
     return KernelSelector(offline_table, {kHipCandidates, kHipCandidateCount}, kHipDefault);
 }
@@ -46,8 +46,8 @@ struct HipLayerBuffers {
     const void* cache = nullptr;   // packed groups [cache_groups][G][3][d/2]
     const void* staging = nullptr; // packed groups [staging_groups][G][3][d/2]
     const void* scales = nullptr;  // fp16 [physical_groups*G][3][d/128]
-    void* hidden = nullptr;        // fp32 [slot_capacity][G]
-    void* partial = nullptr;       // fp32 [slot_capacity][d]
+    void* hidden = nullptr;        // u64 [slot_capacity][G]: fp32 bits of h | launch sequence << 32
+    void* partial = nullptr;       // reserved (the reduction accumulates in backend-owned fixed point)
     void* y32 = nullptr;           // optional fp32 [d] pre-rounding output
     uint32_t* executions = nullptr;     // optional per-destination execution counts
     uint64_t* first_compute = nullptr;  // optional per-destination start stamps

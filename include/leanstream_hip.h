@@ -62,7 +62,7 @@ typedef struct ls_hip_layer_buffers {
 /* Consumer modes (leanstream::runtime::ConsumerMode). */
 enum { LS_MODE_BATCH_COMPAT = 0, LS_MODE_PROGRESSIVE = 1, LS_MODE_AUTO = 2 };
 /* Device status bits returned by ls_hip_status. */
-enum { LS_STATUS_TIMEOUT = 1, LS_STATUS_QUEUE_ERROR = 2, LS_STATUS_BAD_DESCRIPTOR = 4 };
+enum { LS_STATUS_TIMEOUT = 1, LS_STATUS_QUEUE_ERROR = 2, LS_STATUS_BAD_DESCRIPTOR = 4, LS_STATUS_RANGE = 8 };
 
 /* ---- backend ---- */
 void* ls_hip_create(void);

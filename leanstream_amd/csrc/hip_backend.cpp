@@ -17,6 +17,7 @@ struct HipBackend::Impl {
     lsamd::Bounds bounds{};
     uint32_t* sync = nullptr;
     uint32_t* qmirror = nullptr;  // device copy of published queue descriptors
+    unsigned long long* yacc = nullptr;  // packed fixed-point column accumulators [2][d]
     uint32_t slot_words = 0;
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
@@ -31,12 +32,14 @@ struct HipBackend::Impl {
     void release() {
         if (sync) (void)hipFree(sync);
         if (qmirror) (void)hipFree(qmirror);
+        if (yacc) (void)hipFree(yacc);
         if (owned_hidden) (void)hipFree(owned_hidden);
         if (owned_partial) (void)hipFree(owned_partial);
         if (status) (void)hipHostFree(status);
         if (done) (void)hipEventDestroy(done);
         sync = nullptr;
         qmirror = nullptr;
+        yacc = nullptr;
         owned_hidden = owned_partial = nullptr;
         status = nullptr;
         done = nullptr;
@@ -77,6 +80,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
         !b.scales || (b.cache_groups && !b.cache) || (b.staging_groups && !b.staging))
         return EINVAL;
     if (b.batch != 1) return ENOTSUP;
+    if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
     uint32_t S = 0, ns = 0;
     if (!choose_slices(b.group_size, b.width, &S, &ns)) return ENOTSUP;
     p.buf = b;
@@ -84,8 +88,9 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     p.slot_words = lsamd::sync_slot_words(units_cap);
     hipError_t e = hipMalloc(&p.sync, sizeof(uint32_t) * 2 * p.slot_words);
     if (e == hipSuccess) e = hipMalloc(&p.qmirror, sizeof(uint32_t) * 5 * std::max<uint32_t>(1, b.queue_capacity));
+    if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * b.batch);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
-    if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(float) * b.slot_capacity * b.group_size);
+    if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * b.group_size);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p.done, hipEventDisableTiming);
     int dev = 0;
@@ -94,7 +99,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntryFused, &p.per_cu_fused);
     if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntrySplit, &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1)) e = hipErrorInvalidConfiguration;
-    if (e == hipSuccess) e = lsamd::clear_sync(p.sync, 2 * p.slot_words, nullptr);
+    if (e == hipSuccess) e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * b.batch, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         p.release();
@@ -106,7 +111,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.cache = static_cast<const uint8_t*>(b.cache);
     a.staging = static_cast<const uint8_t*>(b.staging);
     a.scales = static_cast<const uint16_t*>(b.scales);
-    a.hbuf = static_cast<float*>(b.hidden ? b.hidden : p.owned_hidden);
+    a.hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
     a.partial = static_cast<float*>(b.partial ? b.partial : p.owned_partial);
     a.y32 = static_cast<float*>(b.y32);
     a.executions = b.executions;
@@ -116,7 +121,9 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.stamps = b.stamps;
     a.sync = p.sync;
     a.qmirror = p.qmirror;
+    a.yacc = p.yacc;
     a.status = p.status;
+    a.width = b.width;
     a.group_size = b.group_size;
     a.slices = S;
     a.slot_words = p.slot_words;
@@ -159,12 +166,13 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     auto hs = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
     if (p.needs_clear) {
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, hs);
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * p.buf.batch, hs);
         if (e != hipSuccess) return static_cast<int>(e);
         p.needs_clear = false;
         p.seq = 0;
     }
-    a.seq = ++p.seq;
+    if (++p.seq == 0) p.seq = 1;  // 0 never tags a stored h
+    a.seq = p.seq;
     const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(ns_), static_cast<int>(workers), entry};
     e = lsamd::launch_layer(plan, a, p.bounds, hs);
     last_candidate_ = static_cast<int>(c.id);

@@ -9,24 +9,42 @@ namespace lsamd {
 using leanstream::runtime::ExecDesc;
 using leanstream::runtime::QueueControl;
 
-// Per-launch device synchronisation block ("ring slot"). Two slots alternate
-// between consecutive launches of one backend; the last worker of launch n
-// clears the slot that launch n+1 will use (the one launch n-1 dirtied).
+// Per-launch device synchronisation block ("ring slot"). Two slots alternate between
+// consecutive launches of one backend; launch n clears the slot launch n+1 will use
+// (the one launch n-1 dirtied) while it runs. Every polled or contended word sits on
+// its own 128-byte line.
+constexpr uint32_t kLine = 32;  // 32-bit words per 128-byte line
 enum SyncWord : uint32_t {
-    kSyncExit = 0,       // workers that have finished
-    kSyncPath = 1,       // 0 undecided, 1 claim path, 2 all-ready fast path
-    kSyncClaimHead = 2,  // next unclaimed ready position (claim path)
-    kSyncAbort = 3,      // set on queue error or spin timeout: every worker leaves
-    kSyncClaims = 4,     // number of successful claims (claim path)
-    kSyncEpochState = 5, // mirror: 0 not yet seen, 1 epoch published, 2 leave (error / abort / timeout)
-    kSyncTotal = 6,      // mirror: final queue total_count
-    kSyncReady = 7,      // mirror: published positions copied into qmirror
-    kSyncTiles = 16,     // [kMaxSlices] completed down-projection tiles per column tile
+    kSyncExit = 0 * kLine,        // workgroups that have finished
+    kSyncEpoch = 1 * kLine,       // mirror: state | path << 2 | total << 4 (state 0 unseen, 1 ok, 2 leave)
+    kSyncReady = 2 * kLine,       // mirror: published positions copied into qmirror
+    kSyncClaimHead = 3 * kLine,   // next unclaimed ready position (claim path)
+    kSyncAbort = 4 * kLine,       // set on queue error or spin timeout: every worker leaves
+    kSyncClaims = 5 * kLine,      // number of successful claims (claim path)
 };
+constexpr uint32_t kSyncTiles = 8 * kLine;
 constexpr uint32_t kMaxSlices = 64;
-constexpr uint32_t kSyncUnits = kSyncTiles + kMaxSlices;  // [units] gate/up slices done per unit
-// then [units] down tiles done per unit, then [units] claim log entries
-inline uint32_t sync_slot_words(uint32_t units) { return kSyncUnits + 3 * units; }
+constexpr uint32_t kSyncUnits = kSyncTiles + kMaxSlices * kLine;  // + u * kLine + 1: down tiles of unit u done
+// (counted only for the optional execution counters)
+inline uint32_t sync_slot_words(uint32_t units) { return kSyncUnits + units * kLine; }
+
+// Deterministic compact reduction. Every (unit, column tile) contribution v is added
+// atomically into one 64-bit word per output column:
+//     word += (round(v * 2^20) + 2^39) + 2^52
+// bits 0..51 hold the biased fixed-point sum, bits 52..63 count the contributions.
+// Integer addition is associative, so the final word -- and the fp32 / fp16 output
+// decoded from it -- does not depend on the order in which units finish. The atomic
+// that brings a column's count to U (the number of destination rows) returns the
+// complete sum, so that lane writes the output column directly.
+// Bounds: |v| < 2^19 per contribution, U < 4096 rows; resolution 2^-20.
+constexpr float kAccScale = 1048576.0f;                 // 2^20
+constexpr double kAccInv = 1.0 / 1048576.0;
+constexpr long long kAccBias = 1ll << 39;
+constexpr unsigned long long kAccOne = 1ull << 52;
+constexpr unsigned long long kAccValueMask = kAccOne - 1;
+constexpr uint32_t kMaxRowsReduced = 4095;
+
+constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
 // Phase stamps written by thread 0 of each worker when MlpArgs::stamps is set.
 constexpr uint32_t kStampSlots = 32;
@@ -36,7 +54,7 @@ enum StampPhase : uint32_t {
 };
 
 // Status word bits (host-coherent, sticky until cleared by the host).
-enum StatusBit : uint32_t { kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u };
+enum StatusBit : uint32_t { kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u, kStatusRange = 8u };
 
 // Arena extents used to validate descriptors on the device before any access.
 struct Bounds {
@@ -57,8 +75,9 @@ struct MlpArgs {
     const uint8_t* cache;         // packed groups, slot-major
     const uint8_t* staging;
     const uint16_t* scales;       // fp16 [(physical*G + n)*3 + proj][d/128]
-    float* hbuf;                  // fp32 [slot][G] intermediate silu(g)*u
-    float* partial;               // fp32 [slot][d]
+    uint64_t* hbuf;               // [slot][G] h = fp16(silu(g)*u) as fp32 bits | launch seq << 32
+    float* partial;               // unused by the fixed-point reduction (kept in the buffer block)
+    unsigned long long* yacc;     // [2][d] packed accumulators (see kAccOne), buffer (seq & 1) per launch
     uint16_t* y;                  // fp16 [d]
     float* y32;                   // optional fp32 [d] pre-rounding output
     uint32_t* executions;         // optional per-destination execution counters
@@ -69,6 +88,7 @@ struct MlpArgs {
     uint32_t claim_log_cap;       // entries in claim_log
     uint64_t* stamps;             // optional: per-worker phase stamps [workers][kStampSlots] (100 MHz clock)
     // geometry / control
+    uint32_t width;               // d
     uint32_t group_size;          // G
     uint32_t slices;              // S: work items per unit (G/S neurons, d/S columns each)
     uint32_t slot_words;          // words per ring slot

@@ -19,6 +19,6 @@ bool variant_available(int width, int ns);
 hipError_t resident_workers(int width, int ns, int entry_point, int* per_cu);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
 hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
-hipError_t clear_sync(uint32_t* sync, uint32_t words, hipStream_t);
+hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, hipStream_t);
 
 }  // namespace lsamd

@@ -5,7 +5,7 @@
 //   gate   = sum_c w_gate(c) x(c)   up = sum_c w_up(c) x(c)          (fp32)
 //   h      = fp16( fp16(silu(fp16(gate))) * fp16(up) )
 //   partial[dest][c] = sum_n h_n w_down(n, c)                         (fp32)
-//   y[c]   = fp16( sum_{slot = 0..U-1} partial[slot][c] )             (fp32, slot order)
+//   y[c]   = fp16( sum over the U destination rows of partial[.][c] )
 //
 // Work decomposition (MI355X-specific): every descriptor ("unit", one group of G
 // neurons) is cut into S items. Item j computes gate/up for neurons
@@ -21,7 +21,13 @@
 // reference's fp16_rn(float(q)*float(scale)). Products w*x are exact in fp32;
 // only the fp32 summation order differs from the reference.
 //
-// Cross-workgroup data (h, partials, counters) uses agent-scope relaxed atomics,
+// Reduction: each unit's tile is added into int64 fixed-point column accumulators
+// (round(v * 2^24)); integer addition is associative, so y does not depend on the order
+// in which units finish -- the output is bit-identical across consumer modes,
+// publication orders and entry points. The U-th contributor of a column tile converts
+// it to fp32 / fp16 and clears it.
+//
+// Cross-workgroup data (h, accumulators, counters) uses agent-scope relaxed atomics,
 // which compile to sc1 loads/stores that are coherent across the eight XCD L2s,
 // with an explicit vmcnt(0) wait before each signalling atomic. No acquire or
 // release fence is issued inside a spin loop (those expand to whole-L2
@@ -201,7 +207,8 @@ __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc,
 // Finish gate/up for the item: dot products, row reductions, activation.
 // Writes h (fp32, fp16-exact) for neurons n0..n0+NS-1 of unit row `hrow`.
 template <int D, int NS>
-__device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<D, NS>& xr, float* hrow, int n0) {
+__device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<D, NS>& xr, uint64_t* hrow, int n0,
+                                           uint32_t seq) {
     using Gm = GuGeom<D, NS>;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
@@ -236,7 +243,9 @@ __device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<
             const float u = round_half(acc[1]);
             const float s = round_half(g / (1.0f + __expf(-g)));
             const float h = round_half(s * u);
-            stf_agent(hrow + n0 + nu, h);
+            // h tagged with the launch sequence: the word is its own ready flag.
+            __hip_atomic_store(hrow + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -278,20 +287,56 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
     }
 }
 
-// Sums the tile into red[] (fp32 [tc]) in a fixed order: per thread over its rows
-// in increasing order (pairs via dot2), then across row groups r0 = 0..rpp-1.
-__device__ __forceinline__ void dn_compute(const DnLoads& L, const DnGeom& gm, const float* hs, float* red, int tc) {
+__device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __shfl(v, 0, 64); }
+
+// Down projection of the tile, consuming h as the unit's items publish it. Each lane
+// needs h only for its own rows; row pairs are processed in a fixed order, and a wave
+// waits (polling the tagged words) only when the next pair's h has not arrived yet,
+// so the down-projection arithmetic overlaps the wait for slower sibling items.
+// The tile is summed into red[kRedFloats + c] (c < tc): per thread over its rows in
+// increasing order (pairs via dot2), then across row groups r0 = 0..rpp-1.
+// Returns false (for the whole workgroup) when the wait was abandoned.
+__device__ bool dn_compute(const MlpArgs& a, uint32_t* slot, const DnLoads& L, const DnGeom& gm, const uint64_t* hrow,
+                           float* red, uint32_t* stop_flag, int tc) {
+    const uint64_t want = (uint64_t)a.seq;
+    uint64_t hv[kMaxRows];
+#pragma unroll
+    for (int i = 0; i < kMaxRows; ++i) hv[i] = i < gm.nrows ? ld_agent_u64(hrow + gm.r0 + gm.rpp * i) : (want << 32);
     float acc[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+    uint32_t stop = 0;
+    Waiter wt(a.spin_limit);
 #pragma unroll
     for (int i = 0; i < kMaxRows; i += 2) {
+        for (;;) {
+            const int ok = (hv[i] >> 32) == want && (hv[i + 1] >> 32) == want;
+            if (__all(ok) || stop) break;
+            uint32_t s = 0;
+            if ((threadIdx.x & 63) == 0) {
+                if (ld_agent(slot + kSyncAbort)) {
+                    s = 1;
+                } else if (wt.expired()) {
+                    raise_status(a, slot, kStatusTimeout);
+                    s = 1;
+                }
+            }
+            stop = wave_bcast(s);
+            if (stop) break;
+            __builtin_amdgcn_s_sleep(1);
+            if ((hv[i] >> 32) != want) hv[i] = ld_agent_u64(hrow + gm.r0 + gm.rpp * i);
+            if ((hv[i + 1] >> 32) != want) hv[i + 1] = ld_agent_u64(hrow + gm.r0 + gm.rpp * (i + 1));
+        }
+        if (stop) break;
         if (i < gm.nrows) {
             const bool pair = i + 1 < gm.nrows;
-            const int na = gm.r0 + gm.rpp * i;
-            const int nb = pair ? na + gm.rpp : na;
             const uint32_t wa = L.w[i], wb = pair ? L.w[i + 1] : L.w[i];
-            const h2 hab = {(_Float16)hs[na], pair ? (_Float16)hs[nb] : (_Float16)0.0f};
+            const _Float16 ha = (_Float16)__uint_as_float((uint32_t)hv[i]);
+            const _Float16 hb = pair ? (_Float16)__uint_as_float((uint32_t)hv[i + 1]) : (_Float16)0.0f;
+            const h2 hab = {ha, hb};
             const h2 sab = {half_bits(L.s[i]), half_bits(pair ? L.s[i + 1] : L.s[i])};
             h2 w[4];
             dequant8(__builtin_amdgcn_perm(wb, wa, 0x05040100u), sab, w);   // columns 0..3
@@ -302,21 +347,27 @@ __device__ __forceinline__ void dn_compute(const DnLoads& L, const DnGeom& gm, c
             for (int c = 0; c < 4; ++c) acc[4 + c] = dot2(w[c], hab, acc[4 + c]);
         }
     }
-    __syncthreads();  // red[] may still be read by a previous tile's reducer
-    if (gm.nrows > 0) {
+    if (stop && (threadIdx.x & 63) == 0) *stop_flag = 1;
+    __syncthreads();  // red[] may still be read by a previous tile; stop flags are set
+    const bool leave = *stop_flag != 0;
+    if (!leave) {
+        if (gm.nrows > 0) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = acc[c];
-    } else if (gm.r0 < gm.rpp) {
+            for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = acc[c];
+        } else if (gm.r0 < gm.rpp) {
 #pragma unroll
-        for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = 0.f;
+            for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = 0.f;
+        }
     }
     __syncthreads();
+    if (leave) return false;
     for (int c = threadIdx.x; c < tc; c += kThreads) {
         float v = 0.f;
         for (int r = 0; r < gm.rpp; ++r) v += red[r * tc + c];
         red[kRedFloats + c] = v;   // reduced tile (second half of the scratch)
     }
     __syncthreads();
+    return true;
 }
 
 // ---------------------------------------------------------------------------------
@@ -344,21 +395,6 @@ __device__ __forceinline__ Unit resolve(const MlpArgs& a, const Bounds& b, ExecD
 
 __device__ __forceinline__ ExecDesc load_core(const MlpArgs& a, uint32_t i) { return a.core[i]; }
 
-// Queue descriptors live in host-coherent memory and are read at system scope
-// after the position has been observed published.
-__device__ __forceinline__ ExecDesc load_queue(const MlpArgs& a, uint32_t pos) {
-    const uint32_t idx = ld_sys(a.ready + pos);
-    ExecDesc d;
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(a.qdesc + (idx < a.capacity ? idx : 0));
-    d.logical_group = ld_sys(p + 0);
-    d.physical_group = ld_sys(p + 1);
-    d.source_slot = ld_sys(p + 2);
-    d.dest_slot = ld_sys(p + 3);
-    d.source_kind = (leanstream::runtime::SourceKind)ld_sys(p + 4);
-    if (idx >= a.capacity) d.dest_slot = 0xffffffffu;  // forces validation failure
-    return d;
-}
-
 // ---------------------------------------------------------------------------------
 // Shared workgroup state
 // ---------------------------------------------------------------------------------
@@ -371,52 +407,91 @@ struct Shared {
     uint32_t ep_known, ep_ok, ep_total, ep_path;
 };
 
-__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t);
-
-// Reduce one column tile over destination rows 0..U-1 in slot order. Each thread owns
-// two adjacent columns and keeps 16 rows of loads in flight before adding them in order.
-__device__ __forceinline__ uint64_t ld_agent64(const float* p) {
-    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void init_shared(Shared& sh) {
+    if (threadIdx.x == 0) { sh.ep_known = 0; sh.ep_ok = 0; sh.ep_total = 0; sh.ep_path = 0; }
+    __syncthreads();
 }
 
-template <int D>
-__device__ void reduce_tile(const MlpArgs& a, int c0, int tc, uint32_t U) {
-    constexpr uint32_t kBatch = 16;
-    for (int c = 2 * threadIdx.x; c < tc; c += 2 * kThreads) {
-        const int col = c0 + c;
-        float v0 = 0.f, v1 = 0.f;
-        for (uint32_t i0 = 0; i0 < U; i0 += kBatch) {
-            uint64_t buf[kBatch];
-#pragma unroll
-            for (uint32_t r = 0; r < kBatch; ++r)
-                buf[r] = i0 + r < U ? ld_agent64(a.partial + (size_t)(i0 + r) * D + col) : 0ull;
-#pragma unroll
-            for (uint32_t r = 0; r < kBatch; ++r) {
-                if (i0 + r < U) {
-                    v0 += __uint_as_float((uint32_t)buf[r]);
-                    v1 += __uint_as_float((uint32_t)(buf[r] >> 32));
-                }
-            }
+// Thread 0's early, non-blocking look at the mirrored epoch word (0 = not yet known).
+__device__ __forceinline__ uint32_t epoch_peek(const Shared& sh, const uint32_t* slot) {
+    return threadIdx.x == 0 && !sh.ep_known ? ld_agent(slot + kSyncEpoch) : 0u;
+}
+
+// (ok, total, path) of the queue, learnt once per workgroup from the word the mirror
+// workgroup publishes. `early` is thread 0's epoch_peek taken before the item's loads.
+__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t early) {
+    // Every thread reads the flag before thread 0 may write it (barrier in between),
+    // so the whole workgroup takes the same branch.
+    const uint32_t known = sh.ep_known;
+    __syncthreads();
+    if (known) return sh.ep_ok != 0;
+    if (threadIdx.x == 0) {
+        uint32_t word = early;
+        Waiter wt(a.spin_limit);
+        while (!(word & 3u)) {
+            if (ld_agent(slot + kSyncAbort)) { word = 2; break; }
+            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); word = 2; break; }
+            __builtin_amdgcn_s_sleep(2);
+            word = ld_agent(slot + kSyncEpoch);
         }
-        if (a.y32) {
-            a.y32[col] = v0;
-            a.y32[col + 1] = v1;
-        }
-        a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-        a.y[col + 1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+        const bool ok = (word & 3u) == 1u;
+        sh.ep_ok = ok;
+        sh.ep_path = ok ? (word >> 2) & 3u : 0u;
+        sh.ep_total = ok ? word >> 4 : 0u;
+        sh.ep_known = 1;
     }
+    __syncthreads();
+    return sh.ep_ok != 0;
 }
 
 // ---------------------------------------------------------------------------------
-// One cooperative item: gate/up for slice j of unit `unit`, then (after all S
-// slices of the unit published h) the down projection of column tile j.
-// FUSED: also count the tile and let the last writer reduce it.
+// Compact reduction by deterministic fixed-point accumulation (kAccOne in mlp_args.h).
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ void st_agent_u64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned long long word, uint32_t rows) {
+    const long long sum = (long long)(word & kAccValueMask) - (long long)rows * kAccBias;
+    const float v = (float)((double)sum * kAccInv);
+    if (a.y32) a.y32[col] = v;
+    a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Adds the reduced tile (tile[c], c < tc) into the column words; with U > 0 (fused
+// launch) the contribution that completes a column writes its output.
+__device__ __forceinline__ void accumulate_tile(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc,
+                                                const float* tile, int c0, int tc, uint32_t U) {
+    bool clipped = false;
+    for (int c = threadIdx.x; c < tc; c += kThreads) {
+        float v = tile[c] * kAccScale;
+        if (!(fabsf(v) < (float)(kAccBias - 1))) {  // out of range or NaN: clip and report
+            clipped = true;
+            v = v > 0.f ? (float)(kAccBias - 1) : -(float)(kAccBias - 1);
+        }
+        const unsigned long long add = (unsigned long long)(__float2ll_rn(v) + kAccBias) + kAccOne;
+        if (U) {
+            const unsigned long long now =
+                __hip_atomic_fetch_add(yacc + c0 + c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+            if ((uint32_t)(now >> 52) == U) write_output(a, c0 + c, now, U);
+        } else {
+            __hip_atomic_fetch_add(yacc + c0 + c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (clipped) raise_status(a, slot, kStatusRange);
+}
+
+// ---------------------------------------------------------------------------------
+// One cooperative item: gate/up for slice j of unit `unit`, then (once all S slices of
+// the unit stored h) the down projection of column tile j into the accumulators.
+// FUSED: also count the tile; the U-th contributor converts it.
 // ---------------------------------------------------------------------------------
 template <int D, int NS, bool FUSED>
-__device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Unit& u,
-                         uint32_t unit, uint32_t j, bool cooperative, uint64_t pre, uint32_t it) {
+__device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc, const XRegs<D, NS>& xr,
+                         const Unit& u, uint32_t unit, uint32_t j, uint32_t it) {
     const uint32_t sb = kStampItemBase + 7 * (it < 4 ? it : 4);
     stamp(a, sb + 0);
+    const uint32_t early = FUSED ? epoch_peek(sh, slot) : 0u;
     const int G = a.group_size;
     const int S = a.slices;
     const int tc = D / S;
@@ -427,93 +502,55 @@ __device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRe
     DnGeom gm(G, tc);
     DnLoads dl;
     dn_issue<D>(u.grp, u.sc, gm, c0, dl);
-    float* hrow = a.hbuf + (size_t)u.dest * G;
-    gu_compute<D, NS>(gl, xr, hrow, j * NS);
-    drain_vmem();
-    __syncthreads();
+    gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * G, j * NS, a.seq);
     stamp(a, sb + 1);
-    if (cooperative) {
-        if (threadIdx.x == 0) {
-            add_agent(slot + kSyncUnits + unit, 1u);
-            Waiter wt(a.spin_limit);
-            uint32_t ok = 1;
-            while (ld_agent(slot + kSyncUnits + unit) < (uint32_t)S) {
-                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
-                if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
-                __builtin_amdgcn_s_sleep(1);
-            }
-            sh.word[0] = ok;
-        }
-        __syncthreads();
-        if (!sh.word[0]) return;
-    }
-    stamp(a, sb + 2);
-    for (int n = threadIdx.x; n < G; n += kThreads) sh.hs[n] = ldf_agent(hrow + n);
+    if (threadIdx.x == 0) sh.word[3] = 0;
     __syncthreads();
-    dn_compute(dl, gm, sh.hs, sh.red, tc);
+    if (!dn_compute(a, slot, dl, gm, a.hbuf + (size_t)u.dest * G, sh.red, &sh.word[3], tc)) return;
     stamp(a, sb + 3);
-    float* prow = a.partial + (size_t)u.dest * D + c0;
-    for (int c = threadIdx.x; c < tc; c += kThreads) stf_agent(prow + c, sh.red[kRedFloats + c]);
-    drain_vmem();
-    __syncthreads();
+    if (FUSED && !await_epoch(a, sh, slot, early)) return;
+    accumulate_tile(a, slot, yacc, sh.red + kRedFloats, c0, tc, FUSED ? a.core_count + sh.ep_total : 0u);
     stamp(a, sb + 4);
-    // The tile counter target is U = core + queue total, final once the epoch is seen.
-    if (FUSED && !await_epoch(a, sh, slot, pre)) return;
-    const uint32_t U = a.core_count + sh.ep_total;
-    if (threadIdx.x == 0) {
-        uint32_t last = 0;
-        if (a.executions) {
-            if (add_agent(slot + kSyncUnits + a.units_cap + unit, 1u) == (uint32_t)S - 1)
-                __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        }
-        if (FUSED) last = add_agent(slot + kSyncTiles + j, 1u) + 1 == U;
-        sh.word[1] = last;
+    if (a.executions) {
+        drain_vmem();
+        __syncthreads();
+        if (threadIdx.x == 0 && add_agent(slot + kSyncUnits + unit * kLine + 1, 1u) == (uint32_t)S - 1)
+            __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    __syncthreads();
-    stamp(a, sb + 5);
-    if (FUSED && sh.word[1]) reduce_tile<D>(a, c0, tc, U);
     stamp(a, sb + 6);
 }
 
 // Process a whole unit inside one workgroup (claim path): no cross-workgroup wait.
 template <int D, int NS, bool FUSED>
-__device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Unit& u,
-                              uint32_t unit, uint32_t U) {
+__device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
+                              const XRegs<D, NS>& xr, const Unit& u) {
     const int S = a.slices;
+    const int G = a.group_size;
     // gate/up for every slice first so that the whole h row exists, then the tiles.
     for (int j = 0; j < S; ++j) {
         if (j == 0 && threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
         GuLoads<D, NS> gl;
         gu_issue<D, NS>(u.grp, u.sc, j * NS, gl);
-        gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * a.group_size, j * NS);
+        gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * G, j * NS, a.seq);
     }
-    drain_vmem();
-    __syncthreads();
-    const int G = a.group_size;
     const int tc = D / S;
     DnGeom gm(G, tc);
-    float* hrow = a.hbuf + (size_t)u.dest * G;
-    for (int n = threadIdx.x; n < G; n += kThreads) sh.hs[n] = ldf_agent(hrow + n);
-    __syncthreads();
+    const uint32_t U = FUSED ? a.core_count + sh.ep_total : 0u;
     for (int j = 0; j < S; ++j) {
         const int c0 = j * tc;
         DnLoads dl;
         dn_issue<D>(u.grp, u.sc, gm, c0, dl);
-        dn_compute(dl, gm, sh.hs, sh.red, tc);
-        float* prow = a.partial + (size_t)u.dest * D + c0;
-        for (int c = threadIdx.x; c < tc; c += kThreads) stf_agent(prow + c, sh.red[kRedFloats + c]);
+        if (threadIdx.x == 0) sh.word[3] = 0;
+        __syncthreads();
+        if (!dn_compute(a, slot, dl, gm, a.hbuf + (size_t)u.dest * G, sh.red, &sh.word[3], tc)) return;
+        accumulate_tile(a, slot, yacc, sh.red + kRedFloats, c0, tc, U);
+    }
+    if (a.executions) {
         drain_vmem();
         __syncthreads();
-        if (threadIdx.x == 0) {
-            uint32_t last = 0;
-            if (FUSED) last = add_agent(slot + kSyncTiles + j, 1u) + 1 == U;
-            sh.word[1] = last;
-        }
-        __syncthreads();
-        if (FUSED && sh.word[1]) reduce_tile<D>(a, c0, tc, U);
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    if (threadIdx.x == 0 && a.executions)
-        __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 // ---------------------------------------------------------------------------------
@@ -524,14 +561,12 @@ __device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
 //
 // On MI355X the queue lives in host memory behind PCIe, where concurrent reads from
 // hundreds of workgroups are served one after another. So exactly one workgroup of
-// each launch (the mirror, the last block) reads host memory: it publishes
-// (epoch state, total, path) into the device ring slot, copies every newly published
+// each launch (the mirror, the last block) reads host memory: it publishes the packed
+// (state, path, total) word into the device ring slot, copies every newly published
 // position's descriptor into a device-side table in publication order (64 positions
 // per round trip, one per lane) and advances a device-side ready count. Workers only
 // poll device memory.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __shfl(v, 0, 64); }
-
 // Runs on wave 0 of the mirror workgroup. `pre` is lane 0's early 64-bit load of
 // (total_count, epoch): adjacent words (byte offsets 8 and 12), read as one pair.
 __device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
@@ -565,14 +600,19 @@ __device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
         }
         uint32_t path = 0;
         if (state == 1 && total) path = ld_sys(&a.control->ready_count) >= total ? 2u : 1u;
-        st_agent(slot + kSyncTotal, state == 1 ? total : 0u);
-        st_agent(slot + kSyncPath, path);
-        drain_vmem();
-        st_agent(slot + kSyncEpochState, state);
+        st_agent(slot + kSyncEpoch, pack_epoch(state, path, state == 1 ? total : 0u));
     }
     state = wave_bcast(state);
     total = wave_bcast(total);
     if (state != 1) return;
+    if (total == 0 && a.core_count == 0) {
+        // no rows at all: the reduction of nothing is zero
+        for (uint32_t c = lane; c < a.width; c += 64) {
+            if (a.y32) a.y32[c] = 0.f;
+            a.y[c] = 0;
+        }
+        return;
+    }
     uint32_t mirrored = 0;
     Waiter wt(a.spin_limit);
     while (mirrored < total) {
@@ -614,37 +654,6 @@ __device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
             __builtin_amdgcn_s_sleep(2);
         }
     }
-}
-
-// Worker side: (ok, total, path) from the ring slot, learnt once per workgroup.
-__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint64_t) {
-    // Every thread reads the flag before thread 0 may write it (barrier in between),
-    // so the whole workgroup takes the same branch.
-    const uint32_t known = sh.ep_known;
-    __syncthreads();
-    if (known) return sh.ep_ok != 0;
-    if (threadIdx.x == 0) {
-        Waiter wt(a.spin_limit);
-        uint32_t state = 0;
-        for (;;) {
-            state = ld_agent(slot + kSyncEpochState);
-            if (state) break;
-            if (ld_agent(slot + kSyncAbort)) { state = 2; break; }
-            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); state = 2; break; }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        sh.ep_ok = state == 1;
-        sh.ep_total = state == 1 ? ld_agent(slot + kSyncTotal) : 0u;
-        sh.ep_path = state == 1 ? ld_agent(slot + kSyncPath) : 0u;
-        sh.ep_known = 1;
-    }
-    __syncthreads();
-    return sh.ep_ok != 0;
-}
-
-__device__ __forceinline__ void init_shared(Shared& sh) {
-    if (threadIdx.x == 0) { sh.ep_known = 0; sh.ep_ok = 0; sh.ep_total = 0; sh.ep_path = 0; }
-    __syncthreads();
 }
 
 // Descriptor of published position `pos` from the device-side table; false when the
@@ -692,7 +701,6 @@ __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uin
                     got = end - head;
                     const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
                     if (a.claim_log && seq < a.claim_log_cap) a.claim_log[seq] = head | (got << 24);
-                    wt = Waiter(a.spin_limit);
                     break;
                 }
                 continue;
@@ -708,13 +716,12 @@ __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uin
 }
 
 template <int D, int NS, bool FUSED>
-__device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, const XRegs<D, NS>& xr, const Bounds& b,
-                              uint32_t W, uint32_t w, uint32_t first_item, uint32_t it) {
-    if (!await_epoch(a, sh, slot, 0)) return;
+__device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc, const XRegs<D, NS>& xr,
+                              const Bounds& b, uint32_t W, uint32_t w, uint32_t first_item, uint32_t it) {
+    if (!await_epoch(a, sh, slot, epoch_peek(sh, slot))) return;
     const uint32_t total = sh.ep_total;
     const uint32_t path = sh.ep_path;
     if (!total) return;
-    const uint32_t U = a.core_count + total;
     const uint32_t S = a.slices;
     if (path == 2) {
         // all ready: static stripes of (position, slice) items, continuing the
@@ -731,7 +738,7 @@ __device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
             }
             if (threadIdx.x == 0 && j == 0 && a.claim_log && (pos & 1) == 0 && pos / 2 < a.claim_log_cap)
                 a.claim_log[pos / 2] = pos | (min(2u, total - pos) << 24);
-            run_item<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + pos, j, true, 0, it++);
+            run_item<D, NS, FUSED>(a, sh, slot, yacc, xr, u, a.core_count + pos, j, it++);
         }
         return;
     }
@@ -747,81 +754,75 @@ __device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, cons
                 if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
                 return;
             }
-            run_unit_solo<D, NS, FUSED>(a, sh, slot, xr, u, a.core_count + head + k, U);
+            run_unit_solo<D, NS, FUSED>(a, sh, slot, yacc, xr, u);
         }
     }
 }
 
-// Last workgroup of a launch: clear the other ring slot for the next launch and, for an
-// empty layer (no rows at all), write the zero output the reduction would produce.
-template <int D>
-__device__ void finish_launch(const MlpArgs& a, Shared& sh, uint32_t* slot, bool fused) {
-    __syncthreads();
-    if (threadIdx.x == 0) sh.word[7] = add_agent(slot + kSyncExit, 1u) + 1 == gridDim.x;
-    __syncthreads();
-    if (!sh.word[7]) return;
+// The mirror workgroup: wave 0 mirrors the queue while waves 1..3 clear what the next
+// launch will use -- the other ring slot and the other accumulator buffer, both last
+// used by the previous launch (finished, by stream order).
+__device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
+    if (threadIdx.x < 64) {
+        mirror_queue(a, slot, pre);
+        return;
+    }
+    const uint32_t t = threadIdx.x - 64, n = kThreads - 64;
     uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-    for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
-    // Every other workgroup (the mirror included) has finished: the slot words are final.
-    if (fused && a.core_count == 0 && ld_agent(slot + kSyncEpochState) == 1 && ld_agent(slot + kSyncTotal) == 0 &&
-        !ld_agent(slot + kSyncAbort))
-        for (int c = threadIdx.x; c < D; c += kThreads) {
-            if (a.y32) a.y32[c] = 0.f;
-            a.y[c] = 0;
-        }
+    for (uint32_t i = t; i < a.slot_words; i += n) st_agent(other + i, 0u);
+    unsigned long long* other_acc = a.yacc + ((a.seq + 1) & 1) * a.width;
+    for (uint32_t i = t; i < a.width; i += n) st_agent_u64(other_acc + i, 0ull);
 }
 
-// The mirror workgroup: wave 0 mirrors, the other waves wait at the barrier.
-__device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
-    if (threadIdx.x < 64) mirror_queue(a, slot, pre);
-    __syncthreads();
-}
+__device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { return a.yacc + (a.seq & 1) * a.width; }
 
 // ---------------------------------------------------------------------------------
 // Kernels. Persistent launches have gridDim.x = workers + 1; the last block mirrors.
 // ---------------------------------------------------------------------------------
 
 // Fused layer: core items (stage A role), queue consumption (stage B role) and the
-// compact reduction (last writer of each column tile), one persistent launch.
+// compact reduction (U-th contributor of each column tile), one persistent launch.
 template <int D, int NS>
-__global__ __launch_bounds__(kThreads) void fused_layer_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, 2) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     const uint32_t W = gridDim.x - 1, w = blockIdx.x;
     if (w == W) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
-        finish_launch<D>(a, sh, slot, true);
         return;
     }
     stamp(a, kStampEntry);
+    unsigned long long* yacc = launch_acc(a);
+    const uint32_t S = a.slices;
+    const uint32_t n_core = a.core_count * S;
+    // the first core descriptor is read before anything else: every later load waits
+    // behind it in the in-order return queue
+    ExecDesc d0 = w < n_core ? load_core(a, w / S) : ExecDesc{};
     init_shared(sh);
     XRegs<D, NS> xr;
     load_x<D, NS>(a.x, xr);
-    const uint32_t S = a.slices;
-    const uint32_t n_core = a.core_count * S;
     stamp(a, kStampXLoaded);
     uint32_t it = 0;
     for (uint32_t i = w; i < n_core; i += W) {
         const uint32_t unit = i / S, j = i % S;
-        const Unit u = resolve(a, b, load_core(a, unit), D);
+        const Unit u = resolve(a, b, i == w ? d0 : load_core(a, unit), D);
         if (!u.ok) {
             if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
             break;
         }
-        run_item<D, NS, true>(a, sh, slot, xr, u, unit, j, true, 0, it++);
+        run_item<D, NS, true>(a, sh, slot, yacc, xr, u, unit, j, it++);
     }
-    consume_queue<D, NS, true>(a, sh, slot, xr, b, W, w, n_core, it);
-    stamp(a, kStampFinish);
-    finish_launch<D>(a, sh, slot, true);
+    consume_queue<D, NS, true>(a, sh, slot, yacc, xr, b, W, w, n_core, it);
     stamp(a, kStampExit);
 }
 
-// Split path, stage A: core items only (no queue, no reduction).
+// Split path, stage A: core items only (no queue, no conversion).
 template <int D, int NS>
-__global__ __launch_bounds__(kThreads) void stage_a_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, 2) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    unsigned long long* yacc = launch_acc(a);
     init_shared(sh);
     XRegs<D, NS> xr;
     load_x<D, NS>(a.x, xr);
@@ -834,13 +835,13 @@ __global__ __launch_bounds__(kThreads) void stage_a_kernel(MlpArgs a, Bounds b) 
             if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
             return;
         }
-        run_item<D, NS, false>(a, sh, slot, xr, u, unit, j, true, 0, 0);
+        run_item<D, NS, false>(a, sh, slot, yacc, xr, u, unit, j, 0);
     }
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
 template <int D, int NS>
-__global__ __launch_bounds__(kThreads) void stage_b_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, 2) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     const uint32_t W = gridDim.x - 1;
@@ -852,31 +853,26 @@ __global__ __launch_bounds__(kThreads) void stage_b_kernel(MlpArgs a, Bounds b) 
     init_shared(sh);
     XRegs<D, NS> xr;
     load_x<D, NS>(a.x, xr);
-    consume_queue<D, NS, false>(a, sh, slot, xr, b, W, blockIdx.x, 0, 0);
+    consume_queue<D, NS, false>(a, sh, slot, launch_acc(a), xr, b, W, blockIdx.x, 0, 0);
 }
 
-// Split path, compact reduction over rows 0..core+total-1 (streaming_mlp.cu:80-84), with
-// the total mirrored by stage B. Block 0 also clears the other ring slot.
+// Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
+// accumulator to y32 / y. 256 columns per block.
 template <int D>
 __global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
-    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    const uint32_t state = ld_agent(slot + kSyncEpochState);
-    uint32_t U = a.core_count + (state == 1 ? ld_agent(slot + kSyncTotal) : 0u);
-    if (U > a.slot_capacity) U = a.slot_capacity;
-    const int c0 = blockIdx.x * kThreads;
-    reduce_tile<D>(a, c0, kThreads, U);
-    if (blockIdx.x == 0) {
-        uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-        for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
-    }
+    const int col = blockIdx.x * kThreads + threadIdx.x;
+    const unsigned long long w = __hip_atomic_load(launch_acc(a) + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    write_output(a, col, w, (uint32_t)(w >> 52));
 }
 
-// Clears both ring slots (bind time, or after a partially failed enqueue).
-__global__ void clear_sync_kernel(uint32_t* sync, uint32_t words) {
+// Clears both ring slots and the accumulators (bind time, or after a failed enqueue).
+__global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns) {
+    // `columns` covers both accumulator buffers
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
         st_agent(sync + i, 0u);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < columns; i += gridDim.x * blockDim.x)
+        st_agent_u64(yacc + i, 0ull);
 }
-
 
 // ---------------------------------------------------------------------------------
 // Host-side launch dispatch over the compiled (width, neurons-per-item) variants.
@@ -948,11 +944,11 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     return hipLaunchKernel(v->reduce, dim3(p.width / kThreads), dim3(kThreads), rargs, 0, stream);
 }
 
-hipError_t clear_sync(uint32_t* sync, uint32_t words, hipStream_t stream) {
+hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, hipStream_t stream) {
     uint32_t grid = (words + kThreads - 1) / kThreads;
     if (grid > 1024) grid = 1024;
     if (!grid) grid = 1;
-    void* kargs[] = {&sync, &words};
+    void* kargs[] = {&sync, &words, &yacc, &columns};
     return hipLaunchKernel(reinterpret_cast<const void*>(&clear_sync_kernel), dim3(grid), dim3(kThreads), kargs, 0,
                            stream);
 }

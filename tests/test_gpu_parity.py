@@ -86,7 +86,7 @@ def test_core_layer_matches_oracle(torch_gpu, key):
     log(f"  fp16 output: max {ulps.max()} ulp, {np.mean(ulps > 0) * 100:.2f}% differ")
     # the fp16 output is the round-to-nearest of y32
     assert np.array_equal(layer.y.cpu().numpy().view(np.uint16), y32.astype(np.float16).view(np.uint16))
-    h = layer.hidden.cpu().numpy().reshape(layer.slot_capacity, cfg.group_size)
+    h = layer.hidden_h()
     hdiff = np.abs(h - ref["h"]) > 0
     log(f"  h: {hdiff.mean() * 100:.3f}% of neurons differ (fp16 rounding-boundary flips)")
     assert hdiff.mean() < 0.01
