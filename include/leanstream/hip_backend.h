@@ -15,15 +15,19 @@
 
 namespace leanstream::runtime {
 
-// CDNA4 candidate catalog. `workers` = persistent workgroups (256 threads each);
-// entry_point 0 = one fused launch (core + ready queue + compact reduction),
-// entry_point 1 = split launches (stage A -> stage B -> reduction kernel).
+// CDNA4 candidate catalog. `workers` = persistent workgroups (256 threads each),
+// clamped to the co-resident count minus one for the queue-mirror workgroup
+// (kAllResident asks for exactly that; the selector rejects 0 workers); every worker
+// takes a share of both the gate/up and the down-projection work; entry_point 0 = one
+// fused launch (core + ready queue + compact reduction), entry_point 1 = split launches
+// (stage A -> stage B -> reduction kernel).
+inline constexpr uint32_t kAllResident = 1u << 16;
 inline constexpr KernelCandidate kHipCandidates[] = {
-    {0, 256, "hip_fused_w256", 256, 0, 0, 0, 0},
-    {1, 512, "hip_fused_w512", 512, 0, 0, 0, 0},
-    {2, 1024, "hip_fused_w1024", 1024, 0, 0, 0, 0},
-    {3, 256, "hip_split_w256", 256, 0, 0, 0, 1},
-    {4, 512, "hip_split_w512", 512, 0, 0, 0, 1},
+    {0, 256, "hip_fused_w256", 0, 0, 0, 0, 0},
+    {1, kAllResident, "hip_fused_resident", 0, 0, 0, 0, 0},
+    {2, 1024, "hip_fused_w1024", 0, 0, 0, 0, 0},
+    {3, 256, "hip_split_w256", 0, 0, 0, 0, 1},
+    {4, kAllResident, "hip_split_resident", 0, 0, 0, 0, 1},
 };
 inline constexpr uint32_t kHipCandidateCount = 5;
 inline constexpr KernelCandidate kHipDefault = kHipCandidates[1];
@@ -81,6 +85,9 @@ public:
     void clear_status();
     void set_spin_limit_ticks(uint64_t ticks) { spin_limit_ = ticks; }
     uint32_t slices() const { return slices_; }
+    // Overrides the selected candidate's persistent worker count (0 = the candidate's
+    // own value); for tuning sweeps.
+    void set_workers(uint32_t workers) { workers_override_ = workers; }
     uint32_t selected(KernelRuntimeState s) const { return selector_.select(s); }
     int last_candidate() const { return last_candidate_; }
     uint32_t max_workers() const { return max_workers_; }
@@ -90,7 +97,8 @@ private:
     Impl* impl_ = nullptr;
     KernelSelector selector_;
     uint64_t spin_limit_ = 200000000ull;  // 2 s of the 100 MHz device clock
-    uint32_t slices_ = 0, ns_ = 0, max_workers_ = 0;
+    uint32_t slices_ = 0, dn_tile_ = 0, max_workers_ = 0;
+    uint32_t workers_override_ = 0;
     int last_candidate_ = -1;
     static int submit(void*, uint32_t, const void*, void*, void*, Span<ExecDesc>, DeviceExecQueue, uint32_t,
                       ConsumerMode);

@@ -78,7 +78,11 @@ int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t ou
 uint32_t ls_hip_status(void* backend);
 void ls_hip_clear_status(void* backend);
 void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
+/* Down-projection column tiles per unit (d / tile). */
 uint32_t ls_hip_slices(void* backend);
+/* Overrides the selected candidate's persistent worker count (0 = the candidate's own
+ * value). No reference counterpart: a tuning knob of the persistent launch. */
+void ls_hip_set_workers(void* backend, uint32_t workers);
 uint32_t ls_hip_select(void* backend, uint32_t layer, uint32_t bucket);
 int ls_hip_last_candidate(void* backend);
 uint32_t ls_hip_max_workers(void* backend);

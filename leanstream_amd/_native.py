@@ -49,6 +49,7 @@ _SIGNATURES = [
     ("ls_hip_clear_status", [p], None),
     ("ls_hip_set_spin_limit", [p, u64], None),
     ("ls_hip_slices", [p], u32),
+    ("ls_hip_set_workers", [p, u32], None),
     ("ls_hip_select", [p, u32, u32], u32),
     ("ls_hip_last_candidate", [p], C.c_int),
     ("ls_hip_max_workers", [p], u32),

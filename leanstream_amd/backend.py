@@ -188,6 +188,10 @@ class NativeBackend:
     def set_spin_limit(self, ticks):
         self.lib.ls_hip_set_spin_limit(self.context, int(ticks))
 
+    def set_workers(self, workers=0):
+        """Override the persistent worker count (0 = the selected candidate's)."""
+        self.lib.ls_hip_set_workers(self.context, int(workers))
+
     @property
     def slices(self):
         return int(self.lib.ls_hip_slices(self.context))

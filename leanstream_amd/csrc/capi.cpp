@@ -102,6 +102,9 @@ void ls_hip_set_spin_limit(void* p, uint64_t ticks) {
     if (p) backend(p)->set_spin_limit_ticks(ticks);
 }
 uint32_t ls_hip_slices(void* p) { return p ? backend(p)->slices() : 0; }
+void ls_hip_set_workers(void* p, uint32_t workers) {
+    if (p) backend(p)->set_workers(workers);
+}
 uint32_t ls_hip_select(void* p, uint32_t layer, uint32_t bucket) {
     return p ? backend(p)->selected({layer, bucket}) : kHipDefault.id;
 }

@@ -22,8 +22,8 @@ struct HipBackend::Impl {
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
     void* owned_partial = nullptr;
-    hipEvent_t done = nullptr;
-    bool recorded = false;
+    uint32_t* done = nullptr;    // host-coherent: sequence of the last finished launch
+    uint32_t last_seq = 0;       // sequence of the last enqueued launch (0: none)
     bool needs_clear = true;
     uint32_t seq = 0;
     int cus = 0, per_cu_fused = 0, per_cu_split = 0;
@@ -36,7 +36,7 @@ struct HipBackend::Impl {
         if (owned_hidden) (void)hipFree(owned_hidden);
         if (owned_partial) (void)hipFree(owned_partial);
         if (status) (void)hipHostFree(status);
-        if (done) (void)hipEventDestroy(done);
+        if (done) (void)hipHostFree(done);
         sync = nullptr;
         qmirror = nullptr;
         yacc = nullptr;
@@ -53,22 +53,13 @@ HipBackend::~HipBackend() { delete impl_; }
 
 namespace {
 
-// Items per unit: S = G / NS with NS in {8,4,2,1}, column tile d/S of whole packed
-// words, and at most 16 down-projection rows per thread (G * d/S <= 32768).
-bool choose_slices(uint32_t G, uint32_t d, uint32_t* slices, uint32_t* ns) {
-    for (uint32_t n : {8u, 4u, 2u, 1u}) {
-        if (G % n) continue;
-        const uint32_t S = G / n;
-        if (S == 0 || S > lsamd::kMaxSlices || d % S) continue;
-        const uint32_t tc = d / S, dwr = tc / 8;
-        if (tc % 8 || dwr == 0 || dwr > 256 || 256 % dwr) continue;
-        if (static_cast<uint64_t>(G) * tc > 32768) continue;
-        if (!lsamd::variant_available(static_cast<int>(d), static_cast<int>(n))) continue;
-        *slices = S;
-        *ns = n;
-        return true;
-    }
-    return false;
+// Columns per down-projection tile: a power of two in [64, 256] with at most
+// kMaxRowsPerThread rows per thread (G * tile <= 16 * 4 * 256: 16 columns of one row per
+// thread and load). G <= 256 always admits 64.
+uint32_t choose_dn_tile(uint32_t G, uint32_t d) {
+    for (uint32_t tc = 256; tc >= 64; tc >>= 1)
+        if (d % tc == 0 && static_cast<uint64_t>(G) * tc <= 16u * lsamd::kMaxRowsPerThread * 256u) return tc;
+    return 0;
 }
 
 }  // namespace
@@ -81,8 +72,8 @@ int HipBackend::bind(const HipLayerBuffers& b) {
         return EINVAL;
     if (b.batch != 1) return ENOTSUP;
     if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
-    uint32_t S = 0, ns = 0;
-    if (!choose_slices(b.group_size, b.width, &S, &ns)) return ENOTSUP;
+    const uint32_t tile = choose_dn_tile(b.group_size, b.width);
+    if (!tile || !lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
     p.buf = b;
     const uint32_t units_cap = b.slot_capacity + b.queue_capacity;
     p.slot_words = lsamd::sync_slot_words(units_cap);
@@ -92,14 +83,19 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
     if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * b.group_size);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&p.done, hipEventDisableTiming);
+    if (e == hipSuccess)
+        e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
     int dev = 0;
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntryFused, &p.per_cu_fused);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, ns, lsamd::kEntrySplit, &p.per_cu_split);
-    if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1)) e = hipErrorInvalidConfiguration;
-    if (e == hipSuccess) e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * b.batch, nullptr);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, &p.per_cu_fused);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, &p.per_cu_split);
+    if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
+        e = hipErrorInvalidConfiguration;
+    uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
+    if (e == hipSuccess)
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * b.batch, hbuf,
+                              b.slot_capacity * b.group_size, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         p.release();
@@ -125,16 +121,19 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.status = p.status;
     a.width = b.width;
     a.group_size = b.group_size;
-    a.slices = S;
+    a.slices = b.width / tile;
+    a.dn_tile = tile;
+    a.g_recip = ((1ull << 32) + b.group_size - 1) / b.group_size;
     a.slot_words = p.slot_words;
     a.units_cap = units_cap;
     a.slot_capacity = b.slot_capacity;
     p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
-    slices_ = S;
-    ns_ = ns;
+    slices_ = b.width / tile;
+    dn_tile_ = tile;
     max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused) - 1;
     p.needs_clear = false;
-    p.recorded = false;
+    p.last_seq = 0;
+    *p.done = 0;
     p.bound = true;
     return 0;
 }
@@ -147,10 +146,11 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     const KernelCandidate c = selector_.candidate(selector_.select(s));
     const int entry = c.entry_point == lsamd::kEntrySplit ? lsamd::kEntrySplit : lsamd::kEntryFused;
     const int per_cu = entry == lsamd::kEntryFused ? p.per_cu_fused : p.per_cu_split;
-    // Persistent workers (plus the mirror workgroup) must be co-resident: items of one
-    // unit wait for each other.
+    // Persistent workers (plus the mirror workgroup) must be co-resident: a worker's
+    // down-projection share waits for h published by other workers.
     const uint32_t resident = static_cast<uint32_t>(p.cus * per_cu) - 1;
-    const uint32_t workers = std::max<uint32_t>(1, std::min<uint32_t>(c.workers ? c.workers : resident, resident));
+    const uint32_t want = workers_override_ ? workers_override_ : c.workers ? c.workers : resident;
+    const uint32_t workers = std::max<uint32_t>(1, std::min<uint32_t>(want, resident));
     lsamd::MlpArgs a = p.base;
     a.core = core.data;
     a.core_count = static_cast<uint32_t>(core.size);
@@ -165,25 +165,28 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     a.spin_limit = spin_limit_;
     auto hs = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
-    if (p.needs_clear) {
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * p.buf.batch, hs);
+    // h words are tagged with the launch sequence. A clear (after a failed launch, and
+    // before the sequence wraps) zeroes every tag, so no stored tag can match a later one.
+    if (p.needs_clear || p.seq == UINT32_MAX) {
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * p.buf.batch, a.hbuf,
+                              p.buf.slot_capacity * p.buf.group_size, hs);
         if (e != hipSuccess) return static_cast<int>(e);
         p.needs_clear = false;
-        p.seq = 0;
     }
-    if (++p.seq == 0) p.seq = 1;  // 0 never tags a stored h
+    // The sequence never takes the value 0 and only moves forward, so neither a tag
+    // from before the last clear nor a late completion word can match a newer launch.
+    p.seq = p.seq == UINT32_MAX ? 1u : p.seq + 1;
     a.seq = p.seq;
-    const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(ns_), static_cast<int>(workers), entry};
+    a.done = p.done;
+    const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(workers), entry};
     e = lsamd::launch_layer(plan, a, p.bounds, hs);
     last_candidate_ = static_cast<int>(c.id);
     if (e != hipSuccess) {
         p.needs_clear = true;  // a partial launch may have left a ring slot dirty
-        p.recorded = false;
         return static_cast<int>(e);
     }
-    e = hipEventRecord(p.done, hs);
-    p.recorded = e == hipSuccess;
-    return static_cast<int>(e);
+    p.last_seq = a.seq;
+    return 0;
 }
 
 uint32_t HipBackend::status() const { return impl_->status ? __atomic_load_n(impl_->status, __ATOMIC_ACQUIRE) : 0; }
@@ -202,8 +205,12 @@ int HipBackend::submit(void* ctx, uint32_t layer, const void* input, void* outpu
 bool HipBackend::complete(void* ctx, uint32_t layer) {
     auto& b = *static_cast<HipBackend*>(ctx);
     if (b.completed) return b.completed(b.lifecycle_context, layer);
-    if (!b.impl_->recorded) return true;
-    return hipEventQuery(b.impl_->done) == hipSuccess;
+    // The last workgroup of a launch to finish stores its sequence (see finish_launch in
+    // the kernel source): wrap-aware comparison against the last enqueued launch.
+    const Impl& p = *b.impl_;
+    if (!p.last_seq) return true;
+    const uint32_t done = __atomic_load_n(p.done, __ATOMIC_ACQUIRE);
+    return static_cast<int32_t>(done - p.last_seq) >= 0;
 }
 
 int HipBackend::commit(void* ctx, uint32_t layer, Span<GroupId> ids) {

@@ -15,16 +15,15 @@ using leanstream::runtime::QueueControl;
 // its own 128-byte line.
 constexpr uint32_t kLine = 32;  // 32-bit words per 128-byte line
 enum SyncWord : uint32_t {
-    kSyncExit = 0 * kLine,        // workgroups that have finished
+    kSyncExit = 0 * kLine,        // groups of workgroups (kSyncExitGroups) that have finished
     kSyncEpoch = 1 * kLine,       // mirror: state | path << 2 | total << 4 (state 0 unseen, 1 ok, 2 leave)
     kSyncReady = 2 * kLine,       // mirror: published positions copied into qmirror
     kSyncClaimHead = 3 * kLine,   // next unclaimed ready position (claim path)
     kSyncAbort = 4 * kLine,       // set on queue error or spin timeout: every worker leaves
     kSyncClaims = 5 * kLine,      // number of successful claims (claim path)
 };
-constexpr uint32_t kSyncTiles = 8 * kLine;
-constexpr uint32_t kMaxSlices = 64;
-constexpr uint32_t kSyncUnits = kSyncTiles + kMaxSlices * kLine;  // + u * kLine + 1: down tiles of unit u done
+constexpr uint32_t kSyncExitGroups = 8 * kLine;  // + g * kLine (g < 8): workgroups blk % 8 == g finished
+constexpr uint32_t kSyncUnits = 16 * kLine;      // + u * kLine: down tiles of unit u done
 // (counted only for the optional execution counters)
 inline uint32_t sync_slot_words(uint32_t units) { return kSyncUnits + units * kLine; }
 
@@ -43,14 +42,17 @@ constexpr long long kAccBias = 1ll << 39;
 constexpr unsigned long long kAccOne = 1ull << 52;
 constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
+constexpr uint32_t kMaxRowsPerThread = 4;  // down-projection rows per thread held in registers
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
 // Phase stamps written by thread 0 of each worker when MlpArgs::stamps is set.
 constexpr uint32_t kStampSlots = 32;
 enum StampPhase : uint32_t {
-    kStampEntry = 0, kStampXLoaded = 1, kStampFinish = 30, kStampExit = 31,
-    kStampItemBase = 2,  // + 7 * item (items 0..3): start, gu done, siblings, dn done, stored, counted, reduced
+    kStampEntry = 0, kStampXLoaded = 1, kStampCoreDone = 2, kStampEpoch = 3, kStampQueueDone = 4,
+    kStampFirstData = 5,  // first gate/up batch or down tile computed
+    kStampDnComputed = 8,  // first round of a down worker computed
+    kStampExit = 31,
 };
 
 // Status word bits (host-coherent, sticky until cleared by the host).
@@ -83,14 +85,17 @@ struct MlpArgs {
     uint32_t* executions;         // optional per-destination execution counters
     uint64_t* first_compute;      // optional per-destination start stamps (100 MHz clock)
     uint32_t* sync;               // base of the two ring slots
-    uint32_t* status;             // host-coherent sticky status word
+    uint32_t* status;
+    uint32_t* done;               // host-coherent: the last workgroup of a launch stores seq             // host-coherent sticky status word
     uint32_t* claim_log;          // optional: per-claim (head | (len << 24)), in claim order
     uint32_t claim_log_cap;       // entries in claim_log
     uint64_t* stamps;             // optional: per-worker phase stamps [workers][kStampSlots] (100 MHz clock)
     // geometry / control
     uint32_t width;               // d
     uint32_t group_size;          // G
-    uint32_t slices;              // S: work items per unit (G/S neurons, d/S columns each)
+    uint32_t slices;              // down-projection tiles per unit (d / dn_tile)
+    uint32_t dn_tile;             // columns per down-projection tile
+    uint64_t g_recip;             // ceil(2^32 / group_size): division by G as a multiply
     uint32_t slot_words;          // words per ring slot
     uint32_t units_cap;           // max units (core + queue) the ring slot covers
     uint32_t slot_capacity;       // rows in hbuf/partial

@@ -9,16 +9,17 @@ enum EntryPoint : int { kEntryFused = 0, kEntrySplit = 1 };
 
 struct LaunchPlan {
     int width;        // d
-    int ns;           // neurons per item (G / slices)
     int workers;      // persistent workgroups
     int entry_point;  // kEntryFused or kEntrySplit
 };
 
-bool variant_available(int width, int ns);
+bool variant_available(int width);
 // Maximum co-resident workgroups per CU for the kernels of an entry point.
-hipError_t resident_workers(int width, int ns, int entry_point, int* per_cu);
+hipError_t resident_workers(int width, int entry_point, int* per_cu);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
 hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
-hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, hipStream_t);
+// Zeroes both ring slots, both accumulator buffers and the tagged h rows.
+hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
+                      uint32_t hwords, hipStream_t);
 
 }  // namespace lsamd

@@ -42,10 +42,15 @@ namespace lsamd {
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kMaxRows = 16;         // down-projection rows per thread held in registers
-constexpr int kRedFloats = 2048;     // LDS scratch for the cross-thread column reduction
+constexpr int kMaxRows = kMaxRowsPerThread;   // down-projection rows per thread
+constexpr int kMaxDnTiles = 6;       // down-projection tiles prefetched per round by a down worker
+constexpr int kGuBuffers = 3;        // gate/up batches in flight per gate/up worker
+constexpr int kUnitChunk = 16;       // unit descriptors loaded per parallel descriptor fetch
+constexpr int kRedFloats = 4096;     // LDS scratch for the cross-thread column reduction (rpp * tile)
+constexpr int kTileScales = 256;     // LDS scale slots per down pair (G * scale blocks of the tile)
 
 // ---------------------------------------------------------------------------------
 // memory helpers
@@ -82,6 +87,9 @@ __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
 
 __device__ __forceinline__ u32x4 ld_stream16(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x2 ld_stream8(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
 __device__ __forceinline__ uint32_t ld_stream4(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
@@ -169,20 +177,21 @@ __device__ __forceinline__ void load_x(const uint16_t* x, XRegs<D, NS>& xr) {
 template <int D, int NS>
 struct GuLoads {
     u32x4 w[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];
-    uint16_t s[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];
+    uint32_t s[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];   // fp16 bits (32-bit registers)
 };
 
 // Issue every gate/up load of one item. grp points at the unit's packed bytes,
 // sc at the unit's scale rows, n0 is the first neuron of the item.
 template <int D, int NS>
-__device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, GuLoads<D, NS>& L) {
+__device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, int nvalid,
+                                         GuLoads<D, NS>& L) {
     using Gm = GuGeom<D, NS>;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
 #pragma unroll
     for (int p = 0; p < Gm::PASSES; ++p) {
-        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;   // neuron within the item
-        const bool ok = nu < NS;
+        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;   // neuron within the batch
+        const bool ok = nu < nvalid;
         const int n = n0 + (ok ? nu : 0);
         const uint8_t* row = grp + (size_t)n * (3 * D / 2);
         const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
@@ -204,11 +213,33 @@ __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc,
     }
 }
 
+// x + the value of another lane chosen by a DPP control (row_mask limits the rows
+// updated; rows outside it add 0).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Sum over each group of LPR consecutive lanes (LPR a power of two <= 64), valid in the
+// group's last lane: a butterfly inside 16-lane rows (quad_perm, row_half_mirror,
+// row_mirror), then row_bcast15 / row_bcast31 across rows. Fixed order, so the result
+// does not depend on timing.
+template <int LPR>
+__device__ __forceinline__ float group_sum(float x) {
+    if (LPR >= 2) x = dpp_add<0xB1>(x);          // quad_perm [1,0,3,2]
+    if (LPR >= 4) x = dpp_add<0x4E>(x);          // quad_perm [2,3,0,1]
+    if (LPR >= 8) x = dpp_add<0x141>(x);         // row_half_mirror
+    if (LPR >= 16) x = dpp_add<0x140>(x);        // row_mirror
+    if (LPR >= 32) x = dpp_add<0x142, 0xA>(x);   // row_bcast15 into rows 1 and 3
+    if (LPR >= 64) x = dpp_add<0x143, 0xC>(x);   // row_bcast31 into rows 2 and 3
+    return x;
+}
+
 // Finish gate/up for the item: dot products, row reductions, activation.
 // Writes h (fp32, fp16-exact) for neurons n0..n0+NS-1 of unit row `hrow`.
 template <int D, int NS>
 __device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<D, NS>& xr, uint64_t* hrow, int n0,
-                                           uint32_t seq) {
+                                           int nvalid, uint32_t seq) {
     using Gm = GuGeom<D, NS>;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
@@ -219,7 +250,7 @@ __device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<
         for (int proj = 0; proj < 2; ++proj) {
 #pragma unroll
             for (int k = 0; k < Gm::CPL; ++k) {
-                const _Float16 sv = half_bits(L.s[p][proj][k]);
+                const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
                 const h2 s2 = {sv, sv};
                 const u32x4 v = L.w[p][proj][k];
                 const uint32_t words[4] = {v.x, v.y, v.z, v.w};
@@ -232,13 +263,10 @@ __device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<
                 }
             }
         }
-#pragma unroll
-        for (int m = 1; m < Gm::LPR; m <<= 1) {
-            acc[0] += __shfl_xor(acc[0], m, 64);
-            acc[1] += __shfl_xor(acc[1], m, 64);
-        }
+        acc[0] = group_sum<Gm::LPR>(acc[0]);
+        acc[1] = group_sum<Gm::LPR>(acc[1]);
         const int nu = p * Gm::NPP + wave * Gm::NPW + sub;
-        if (r == 0 && nu < NS) {
+        if (r == Gm::LPR - 1 && nu < nvalid) {
             const float g = round_half(acc[0]);
             const float u = round_half(acc[1]);
             const float s = round_half(g / (1.0f + __expf(-g)));
@@ -251,40 +279,52 @@ __device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<
 }
 
 // ---------------------------------------------------------------------------------
-// Down projection of one column tile of one unit (all G neurons), tc columns.
-// Thread t owns 8 columns (one packed word per row) and rows r0, r0+rpp, ...
+// Down projection of one column tile (tc columns) of one unit, all G neurons.
+// Thread t covers 16 columns -- one 8-byte load of 16 nibbles per row -- of rows
+// r0, r0 + rpp, ...: lanes = tc / 16 threads share a row, rpp = 256 / lanes rows per
+// pass, at most kMaxRows rows per thread (G * tc <= 16384).
 // ---------------------------------------------------------------------------------
 struct DnLoads {
-    uint32_t w[kMaxRows];
-    uint16_t s[kMaxRows];
+    u32x2 w[kMaxRows];
 };
 
 struct DnGeom {
-    int dwr, rpp, dc, r0, nrows;
+    int lanes, rpp, rpp_shift, dc, r0, nrows, nbk, nbk_shift;
     __device__ DnGeom(int G, int tc) {
-        dwr = tc >> 3;                 // packed words per row in the tile
-        rpp = kThreads / dwr;          // rows covered per pass of the workgroup
-        dc = threadIdx.x % dwr;
-        r0 = threadIdx.x / dwr;
-        nrows = r0 < G ? (G - r0 + rpp - 1) / rpp : 0;
+        const int lanes_shift = __builtin_ctz((unsigned)tc) - 4;
+        lanes = 1 << lanes_shift;      // threads per row of the tile (tc is a power of two)
+        rpp_shift = 8 - lanes_shift;
+        rpp = 1 << rpp_shift;          // rows covered per pass of the workgroup
+        dc = threadIdx.x & (lanes - 1);
+        r0 = threadIdx.x >> lanes_shift;
+        nrows = r0 < G ? (G - r0 + rpp - 1) >> rpp_shift : 0;
+        nbk_shift = tc > 128 ? 1 : 0;
+        nbk = 1 << nbk_shift;          // 128-column scale blocks the tile spans
     }
 };
 
 template <int D>
-__device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc, const DnGeom& gm, int c0, DnLoads& L) {
-    constexpr int BLOCKS = D / 128;
-    const int col = c0 + 8 * gm.dc;
+__device__ __forceinline__ void dn_issue(const uint8_t* grp, const DnGeom& gm, int c0, DnLoads& L) {
+    const int col = c0 + 16 * gm.dc;
 #pragma unroll
     for (int i = 0; i < kMaxRows; ++i) {
         if (i < gm.nrows) {
             const int n = gm.r0 + gm.rpp * i;
-            L.w[i] = ld_stream4(grp + (size_t)n * (3 * D / 2) + D + (col >> 1));
-            L.s[i] = sc[(size_t)n * 3 * BLOCKS + 2 * BLOCKS + (col >> 7)];
+            L.w[i] = ld_stream8(grp + (size_t)n * (3 * D / 2) + D + (col >> 1));
         } else {
-            L.w[i] = 0;
-            L.s[i] = 0;
+            L.w[i] = u32x2{0, 0};
         }
     }
+}
+
+// This thread's share of the tile's down scales, staged in LDS by stage_round:
+// slot t < G * nbk holds row t / nbk, block t % nbk of the tile.
+template <int D>
+__device__ __forceinline__ uint32_t dn_scale_issue(const uint16_t* sc, const DnGeom& gm, int G, int c0) {
+    constexpr int BLOCKS = D / 128;
+    const int t = threadIdx.x;
+    if (t >= G * gm.nbk) return 0;
+    return sc[(size_t)(t >> gm.nbk_shift) * 3 * BLOCKS + 2 * BLOCKS + (c0 >> 7) + (t & (gm.nbk - 1))];
 }
 
 __device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
@@ -292,82 +332,76 @@ __device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
 }
 __device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __shfl(v, 0, 64); }
 
-// Down projection of the tile, consuming h as the unit's items publish it. Each lane
-// needs h only for its own rows; row pairs are processed in a fixed order, and a wave
-// waits (polling the tagged words) only when the next pair's h has not arrived yet,
-// so the down-projection arithmetic overlaps the wait for slower sibling items.
-// The tile is summed into red[kRedFloats + c] (c < tc): per thread over its rows in
-// increasing order (pairs via dot2), then across row groups r0 = 0..rpp-1.
-// Returns false (for the whole workgroup) when the wait was abandoned.
-__device__ bool dn_compute(const MlpArgs& a, uint32_t* slot, const DnLoads& L, const DnGeom& gm, const uint64_t* hrow,
-                           float* red, uint32_t* stop_flag, int tc) {
-    const uint64_t want = (uint64_t)a.seq;
-    uint64_t hv[kMaxRows];
+// Float offset of the 4-column chunk q of column group dc in a row of the reduction
+// scratch (see dn_compute).
+__device__ __forceinline__ int red_swizzle(int dc, int q) { return 16 * dc + 4 * ((q + (dc >> 1)) & 3); }
+
+// Down projection of the tile with the pair's h (hs) and scales (ss) staged in LDS.
+// Each thread sums its rows in increasing order, two rows per dot2 (v_perm pairs the
+// nibbles of rows (j, j+1) column by column), into 16 column partials; the partials
+// of the rpp row groups are then summed in LDS in row-group order into
+// red[kRedFloats + t], tile column t.
+__device__ __forceinline__ void dn_compute(const DnLoads& L, const DnGeom& gm, const uint16_t* hs, const uint16_t* ss,
+                                           float* red, int tc) {
+    static_assert(kMaxRows == 4, "two row pairs per thread");
+    const u32x2 hp = *reinterpret_cast<const u32x2*>(hs + gm.r0 * kMaxRows);  // h of rows (0,1) (2,3)
+    const uint32_t hw[2] = {hp.x, hp.y};
+    const int blk = gm.dc >> 3;   // 16 dc / 128: scale block within the tile
+    float acc[16];
 #pragma unroll
-    for (int i = 0; i < kMaxRows; ++i) hv[i] = i < gm.nrows ? ld_agent_u64(hrow + gm.r0 + gm.rpp * i) : (want << 32);
-    float acc[8];
-#pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = 0.f;
-    uint32_t stop = 0;
-    Waiter wt(a.spin_limit);
+    for (int c = 0; c < 16; ++c) acc[c] = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxRows; i += 2) {
-        for (;;) {
-            const int ok = (hv[i] >> 32) == want && (hv[i + 1] >> 32) == want;
-            if (__all(ok) || stop) break;
-            uint32_t s = 0;
-            if ((threadIdx.x & 63) == 0) {
-                if (ld_agent(slot + kSyncAbort)) {
-                    s = 1;
-                } else if (wt.expired()) {
-                    raise_status(a, slot, kStatusTimeout);
-                    s = 1;
-                }
-            }
-            stop = wave_bcast(s);
-            if (stop) break;
-            __builtin_amdgcn_s_sleep(1);
-            if ((hv[i] >> 32) != want) hv[i] = ld_agent_u64(hrow + gm.r0 + gm.rpp * i);
-            if ((hv[i + 1] >> 32) != want) hv[i + 1] = ld_agent_u64(hrow + gm.r0 + gm.rpp * (i + 1));
-        }
-        if (stop) break;
         if (i < gm.nrows) {
             const bool pair = i + 1 < gm.nrows;
-            const uint32_t wa = L.w[i], wb = pair ? L.w[i + 1] : L.w[i];
-            const _Float16 ha = (_Float16)__uint_as_float((uint32_t)hv[i]);
-            const _Float16 hb = pair ? (_Float16)__uint_as_float((uint32_t)hv[i + 1]) : (_Float16)0.0f;
-            const h2 hab = {ha, hb};
-            const h2 sab = {half_bits(L.s[i]), half_bits(pair ? L.s[i + 1] : L.s[i])};
-            h2 w[4];
-            dequant8(__builtin_amdgcn_perm(wb, wa, 0x05040100u), sab, w);   // columns 0..3
+            const u32x2 wa = L.w[i], wb = pair ? L.w[i + 1] : L.w[i];
+            const h2 hab = as_h2(hw[i / 2]);   // second half is zero when !pair
+            const int na = gm.r0 + gm.rpp * i, nb = pair ? na + gm.rpp : na;
+            const h2 sab = {half_bits(ss[na * gm.nbk + blk]), half_bits(ss[nb * gm.nbk + blk])};
+            const uint32_t xa[2] = {wa.x, wa.y}, xb[2] = {wb.x, wb.y};
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[c] = dot2(w[c], hab, acc[c]);
-            dequant8(__builtin_amdgcn_perm(wb, wa, 0x07060302u), sab, w);   // columns 4..7
+            for (int q = 0; q < 2; ++q) {
+                h2 w[4];
+                dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
 #pragma unroll
-            for (int c = 0; c < 4; ++c) acc[4 + c] = dot2(w[c], hab, acc[4 + c]);
+                for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
+                dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);   // columns 8q + 4..7
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
+            }
         }
     }
-    if (stop && (threadIdx.x & 63) == 0) *stop_flag = 1;
-    __syncthreads();  // red[] may still be read by a previous tile; stop flags are set
-    const bool leave = *stop_flag != 0;
-    if (!leave) {
-        if (gm.nrows > 0) {
+    // red's first half is free: the previous tile's column sums were read before the
+    // barrier that ended it. Row group r0's partial of tile column 16 dc + 4 q + e sits
+    // at r0 * tc + swz(dc, q) + e: each thread stores 4 x 16 bytes, and within any 8
+    // consecutive lanes the 16-byte chunks fall on distinct banks.
+    float* mine = red + gm.r0 * tc;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = acc[c];
-        } else if (gm.r0 < gm.rpp) {
-#pragma unroll
-            for (int c = 0; c < 8; ++c) red[gm.r0 * tc + 8 * gm.dc + c] = 0.f;
-        }
+    for (int q = 0; q < 4; ++q) {
+        const float4 v = gm.nrows > 0 ? float4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]}
+                                      : float4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<float4*>(mine + red_swizzle(gm.dc, q)) = v;
     }
-    __syncthreads();
-    if (leave) return false;
-    for (int c = threadIdx.x; c < tc; c += kThreads) {
+    __syncthreads();  // also: every thread is done with the previous tile's second half
+    for (int t = threadIdx.x; t < tc; t += kThreads) {
+        const int at = red_swizzle(t >> 4, (t >> 2) & 3) + (t & 3);
         float v = 0.f;
-        for (int r = 0; r < gm.rpp; ++r) v += red[r * tc + c];
-        red[kRedFloats + c] = v;   // reduced tile (second half of the scratch)
+        for (int r0 = 0; r0 < gm.rpp; r0 += 16) {   // rpp is 16, 32 or 64
+            float p[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = red[(r0 + r) * tc + at];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) v += p[r];
+        }
+        red[kRedFloats + t] = v;   // reduced tile, natural column order
     }
     __syncthreads();
-    return true;
+}
+
+// x / G for x < 2^16 (G <= 256) via the launch's reciprocal ceil(2^32 / G): exact, as
+// x * (ceil(2^32 / G) - 2^32 / G) < 2^32 / G.
+__device__ __forceinline__ uint32_t div_group(const MlpArgs& a, uint32_t x) {
+    return (uint32_t)(((uint64_t)x * a.g_recip) >> 32);
 }
 
 // ---------------------------------------------------------------------------------
@@ -399,8 +433,12 @@ __device__ __forceinline__ ExecDesc load_core(const MlpArgs& a, uint32_t i) { re
 // Shared workgroup state
 // ---------------------------------------------------------------------------------
 struct Shared {
-    float red[2 * kRedFloats];
-    float hs[256];
+    alignas(16) float red[kRedFloats + 256];
+    alignas(16) uint16_t hs[kMaxDnTiles * 64 * kMaxRows];   // staged h of a round (stage_round layout)
+    uint16_t ss[kMaxDnTiles * kTileScales];                  // staged down scales of a round
+    uint32_t pdest[kMaxDnTiles];                             // dest rows of the round's pairs
+    uint32_t ulist[kUnitChunk];                              // units of a descriptor fetch
+    uint32_t udesc[kUnitChunk][5];                           // their descriptor words
     uint32_t word[8];
     uint32_t desc[5];
     // queue state learnt once per launch: known, ok, total, path
@@ -409,6 +447,7 @@ struct Shared {
 
 __device__ __forceinline__ void init_shared(Shared& sh) {
     if (threadIdx.x == 0) { sh.ep_known = 0; sh.ep_ok = 0; sh.ep_total = 0; sh.ep_path = 0; }
+    for (int i = threadIdx.x; i < kMaxDnTiles * 64 * kMaxRows; i += kThreads) sh.hs[i] = 0;
     __syncthreads();
 }
 
@@ -419,7 +458,7 @@ __device__ __forceinline__ uint32_t epoch_peek(const Shared& sh, const uint32_t*
 
 // (ok, total, path) of the queue, learnt once per workgroup from the word the mirror
 // workgroup publishes. `early` is thread 0's epoch_peek taken before the item's loads.
-__device__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t early) {
+__device__ __forceinline__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t early) {
     // Every thread reads the flag before thread 0 may write it (barrier in between),
     // so the whole workgroup takes the same branch.
     const uint32_t known = sh.ep_known;
@@ -458,99 +497,503 @@ __device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned
     a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-// Adds the reduced tile (tile[c], c < tc) into the column words; with U > 0 (fused
-// launch) the contribution that completes a column writes its output.
-__device__ __forceinline__ void accumulate_tile(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc,
-                                                const float* tile, int c0, int tc, uint32_t U) {
-    bool clipped = false;
-    for (int c = threadIdx.x; c < tc; c += kThreads) {
-        float v = tile[c] * kAccScale;
-        if (!(fabsf(v) < (float)(kAccBias - 1))) {  // out of range or NaN: clip and report
-            clipped = true;
-            v = v > 0.f ? (float)(kAccBias - 1) : -(float)(kAccBias - 1);
+
+__device__ __forceinline__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out);
+
+// h and down scales of a round's pairs staged in LDS. h as the fp16 values each
+// down-projection thread multiplies: hs[i * stride + r0 * kMaxRows + j] = h_i[r0 + rpp * j]
+// for pair i (stride = rpp * kMaxRows; zero for rows >= G, written once at start).
+// Every thread polls its share of the tagged words (dest rows in sh.pdest) until each
+// tag carries the launch sequence, then converts (exactly: h is fp16-representable).
+// Scales: ss[i * kTileScales + t] = sv[i] (dn_scale_issue). Returns false for the whole
+// workgroup when the wait was abandoned.
+constexpr int kStageWords = 8;   // h words per thread per staging pass
+__device__ __forceinline__ bool stage_round(const MlpArgs& a, uint32_t* slot, Shared& sh, uint32_t npairs,
+                                            const DnGeom& gm, int G, const uint32_t (&sv)[kMaxDnTiles]) {
+    const uint32_t total = npairs * (uint32_t)G;
+    const uint32_t stride = (uint32_t)gm.rpp * kMaxRows;
+    const uint64_t want = (uint64_t)a.seq;
+    uint32_t* stop_flag = &sh.word[3];
+    if (threadIdx.x == 0) *stop_flag = 0;
+    __syncthreads();  // pdest written; earlier readers of hs / ss and the flag are done
+#pragma unroll
+    for (int i = 0; i < kMaxDnTiles; ++i)
+        if ((uint32_t)i < npairs && (int)threadIdx.x < G * gm.nbk) sh.ss[i * kTileScales + threadIdx.x] = (uint16_t)sv[i];
+    for (uint32_t f0 = 0; f0 < total; f0 += kStageWords * kThreads) {
+        uint64_t v[kStageWords];
+        const uint64_t* src[kStageWords];
+#pragma unroll
+        for (int q = 0; q < kStageWords; ++q) {
+            const uint32_t f = f0 + threadIdx.x + q * kThreads;
+            const uint32_t i = div_group(a, f), n = f - i * G;
+            src[q] = f < total ? a.hbuf + (size_t)sh.pdest[i] * G + n : nullptr;
+            v[q] = src[q] ? ld_agent_u64(src[q]) : (want << 32);
         }
-        const unsigned long long add = (unsigned long long)(__float2ll_rn(v) + kAccBias) + kAccOne;
-        if (U) {
-            const unsigned long long now =
-                __hip_atomic_fetch_add(yacc + c0 + c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
-            if ((uint32_t)(now >> 52) == U) write_output(a, c0 + c, now, U);
-        } else {
-            __hip_atomic_fetch_add(yacc + c0 + c, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t stop = 0;
+        Waiter wt(a.spin_limit);
+        for (;;) {
+            bool ok = true;
+#pragma unroll
+            for (int q = 0; q < kStageWords; ++q) ok = ok && (v[q] >> 32) == want;
+            if (__all(ok)) break;
+            uint32_t st = 0;
+            if ((threadIdx.x & 63) == 0) {
+                if (ld_agent(slot + kSyncAbort)) {
+                    st = 1;
+                } else if (wt.expired()) {
+                    raise_status(a, slot, kStatusTimeout);
+                    st = 1;
+                }
+            }
+            stop = wave_bcast(st);
+            if (stop) break;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int q = 0; q < kStageWords; ++q)
+                if ((v[q] >> 32) != want) v[q] = ld_agent_u64(src[q]);
+        }
+        if (stop) {
+            if ((threadIdx.x & 63) == 0) *stop_flag = 1;
+            break;
+        }
+#pragma unroll
+        for (int q = 0; q < kStageWords; ++q) {
+            const uint32_t f = f0 + threadIdx.x + q * kThreads;
+            if (f < total) {
+                const uint32_t i = div_group(a, f), n = f - i * G;
+                sh.hs[i * stride + (n & (gm.rpp - 1)) * kMaxRows + (n >> gm.rpp_shift)] =
+                    __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)v[q]));
+            }
         }
     }
-    if (clipped) raise_status(a, slot, kStatusRange);
-}
-
-// ---------------------------------------------------------------------------------
-// One cooperative item: gate/up for slice j of unit `unit`, then (once all S slices of
-// the unit stored h) the down projection of column tile j into the accumulators.
-// FUSED: also count the tile; the U-th contributor converts it.
-// ---------------------------------------------------------------------------------
-template <int D, int NS, bool FUSED>
-__device__ void run_item(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc, const XRegs<D, NS>& xr,
-                         const Unit& u, uint32_t unit, uint32_t j, uint32_t it) {
-    const uint32_t sb = kStampItemBase + 7 * (it < 4 ? it : 4);
-    stamp(a, sb + 0);
-    const uint32_t early = FUSED ? epoch_peek(sh, slot) : 0u;
-    const int G = a.group_size;
-    const int S = a.slices;
-    const int tc = D / S;
-    const int c0 = j * tc;
-    if (j == 0 && threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
-    GuLoads<D, NS> gl;
-    gu_issue<D, NS>(u.grp, u.sc, j * NS, gl);
-    DnGeom gm(G, tc);
-    DnLoads dl;
-    dn_issue<D>(u.grp, u.sc, gm, c0, dl);
-    gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * G, j * NS, a.seq);
-    stamp(a, sb + 1);
-    if (threadIdx.x == 0) sh.word[3] = 0;
     __syncthreads();
-    if (!dn_compute(a, slot, dl, gm, a.hbuf + (size_t)u.dest * G, sh.red, &sh.word[3], tc)) return;
-    stamp(a, sb + 3);
-    if (FUSED && !await_epoch(a, sh, slot, early)) return;
-    accumulate_tile(a, slot, yacc, sh.red + kRedFloats, c0, tc, FUSED ? a.core_count + sh.ep_total : 0u);
-    stamp(a, sb + 4);
-    if (a.executions) {
-        drain_vmem();
-        __syncthreads();
-        if (threadIdx.x == 0 && add_agent(slot + kSyncUnits + unit * kLine + 1, 1u) == (uint32_t)S - 1)
-            __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
-    stamp(a, sb + 6);
+    return *stop_flag == 0;
 }
 
-// Process a whole unit inside one workgroup (claim path): no cross-workgroup wait.
-template <int D, int NS, bool FUSED>
-__device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
-                              const XRegs<D, NS>& xr, const Unit& u) {
-    const int S = a.slices;
+// Gate/up batch size of the width-D variant: one pass of the workgroup (4 waves).
+template <int D>
+struct Batch {
+    static constexpr int N = GuGeom<D, 1>::NPP;
+};
+
+// Descriptor of global unit `gu` (core units first, then queue positions), validated.
+__device__ __forceinline__ bool fetch_unit(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, uint32_t gu, int D,
+                           Unit* out) {
+    ExecDesc d;
+    if (gu < a.core_count) {
+        d = load_core(a, gu);
+    } else if (!load_queue_wg(a, sh, slot, gu - a.core_count, &d)) {
+        return false;
+    }
+    *out = resolve(a, b, d, D);
+    if (!out->ok) {
+        if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+        return false;
+    }
+    return true;
+}
+
+// Loads the descriptors of units sh.ulist[0..n) (n <= kUnitChunk, written by thread 0)
+// in parallel, one word per thread, into sh.udesc: core units from the core array,
+// queue positions from the device-side mirror once the mirror has copied them.
+// One memory round trip (two when queue positions must first be waited for).
+__device__ __forceinline__ bool load_units(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t n) {
+    __syncthreads();  // ulist written; earlier readers of udesc are done
+    stamp(a, 10);
+    if (threadIdx.x == 0) {
+        uint32_t need = 0;  // queue positions that must be mirrored
+        for (uint32_t i = 0; i < n; ++i)
+            if (sh.ulist[i] >= a.core_count) need = max(need, sh.ulist[i] - a.core_count + 1);
+        uint32_t ok = 1;
+        if (need) {
+            Waiter wt(a.spin_limit);
+            while (ld_agent(slot + kSyncReady) < need) {
+                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+                if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+                __builtin_amdgcn_s_sleep(1);
+            }
+        }
+        sh.word[2] = ok;
+    }
+    __syncthreads();
+    if (!__builtin_amdgcn_readfirstlane(sh.word[2])) return false;
+    if (threadIdx.x < 5 * n) {
+        const uint32_t i = threadIdx.x / 5, w = threadIdx.x % 5, g = sh.ulist[i];
+        sh.udesc[i][w] = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
+                                          : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
+    }
+    __syncthreads();
+    stamp(a, 11);
+    return true;
+}
+
+// Unit i of the last load_units, validated (wave-uniform values).
+__device__ __forceinline__ bool unit_from(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, uint32_t i,
+                                          int D, Unit* out) {
+    ExecDesc d;
+    d.logical_group = __builtin_amdgcn_readfirstlane(sh.udesc[i][0]);
+    d.physical_group = __builtin_amdgcn_readfirstlane(sh.udesc[i][1]);
+    d.source_slot = __builtin_amdgcn_readfirstlane(sh.udesc[i][2]);
+    d.dest_slot = __builtin_amdgcn_readfirstlane(sh.udesc[i][3]);
+    d.source_kind = (leanstream::runtime::SourceKind)__builtin_amdgcn_readfirstlane(sh.udesc[i][4]);
+    *out = resolve(a, b, d, D);
+    if (!out->ok) {
+        if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+        return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------------
+// Gate/up share: batches [g0, g1) of Batch<D>::N neurons (never straddling a unit; unit
+// u0 + bi / bpu holds batch bi), kGuBuffers batches in flight, h stored tagged with the
+// launch sequence. The weight loads of the first batches are issued before x is loaded
+// (x is only needed to compute). Descriptors of units [chunk0, chunk0 + chunk_n) are
+// already in sh.udesc from slot chunk_off on; later units are fetched kUnitChunk at a time.
+// Never waits for another workgroup's h, so every worker finishes its share.
+// ---------------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ bool gate_up_share(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
+                                              XRegs<D, Batch<D>::N>& xr, bool& have_x, uint32_t u0, uint32_t g0,
+                                              uint32_t g1, uint32_t bpu, uint32_t chunk0, uint32_t chunk_n,
+                                              uint32_t chunk_off) {
+    constexpr int NB = Batch<D>::N;
+    const uint32_t G = a.group_size;
+    if (g0 >= g1) return true;
+    struct Meta {
+        uint64_t* hrow;
+        int n0, nvalid;
+    };
+    const uint32_t ulast = u0 + (g1 - 1) / bpu;      // last unit of the share (inclusive)
+    auto issue = [&](uint32_t bi, GuLoads<D, NB>& L, Meta& m) -> bool {
+        const uint32_t unit = u0 + bi / bpu;
+        if (unit >= chunk0 + chunk_n) {
+            chunk0 = unit;
+            chunk_n = min((uint32_t)kUnitChunk, ulast + 1 - unit);
+            chunk_off = 0;
+            if (threadIdx.x == 0)
+                for (uint32_t i = 0; i < chunk_n; ++i) sh.ulist[i] = chunk0 + i;
+            if (!load_units(a, sh, slot, chunk_n)) return false;
+        }
+        Unit u;
+        if (!unit_from(a, sh, slot, b, chunk_off + unit - chunk0, D, &u)) return false;
+        if (threadIdx.x == 0 && a.first_compute && bi % bpu == 0) a.first_compute[u.dest] = now_ticks();
+        m.n0 = (int)((bi % bpu) * NB);
+        m.nvalid = min(NB, (int)G - m.n0);
+        m.hrow = a.hbuf + (size_t)u.dest * G;
+        gu_issue<D, NB>(u.grp, u.sc, m.n0, m.nvalid, L);
+        return true;
+    };
+    GuLoads<D, NB> L[kGuBuffers];
+    Meta M[kGuBuffers];
+#pragma unroll
+    for (int q = 0; q < kGuBuffers; ++q)
+        if (g0 + q < g1 && !issue(g0 + q, L[q], M[q])) return false;
+    if (!have_x) {
+        load_x<D, NB>(a.x, xr);
+        have_x = true;
+    }
+    for (uint32_t bi = g0; bi < g1; bi += kGuBuffers) {
+#pragma unroll
+        for (int q = 0; q < kGuBuffers; ++q) {
+            if (bi + q < g1) {
+                gu_compute<D, NB>(L[q], xr, M[q].hrow, M[q].n0, M[q].nvalid, a.seq);
+                if (bi + q == g0) stamp(a, kStampFirstData);
+                if (bi + q + kGuBuffers < g1 && !issue(bi + q + kGuBuffers, L[q], M[q])) return false;
+            }
+        }
+    }
+    return true;
+}
+
+// Execution counters (diagnostics): a unit counts once all of its down tiles are done.
+__device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot, uint32_t unit, uint32_t dest,
+                                                uint32_t tiles) {
+    if (threadIdx.x == 0 && add_agent(slot + kSyncUnits + unit * kLine, 1u) == tiles - 1)
+        __hip_atomic_fetch_add(a.executions + dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Placement of persistent worker `blk` of W. Workgroups are dispatched round-robin over
+// the XCDs (blk % kXcds); the work index k runs contiguously inside an XCD, so workers
+// [base, base + count) share this worker's XCD (and its L2) and neighbouring work
+// ranges -- consecutive tiles of one unit, which share scale lines -- meet in one L2.
+constexpr uint32_t kXcds = 8;
+struct Place {
+    uint32_t k;       // work index
+    uint32_t base;    // first work index on this XCD
+    uint32_t count;   // workers on this XCD
+};
+__device__ __forceinline__ Place place_of(uint32_t blk, uint32_t W) {
+    const uint32_t x = blk % kXcds, j = blk / kXcds;
+    uint32_t before = 0;  // workers on XCDs < x
+    for (uint32_t y = 0; y < x; ++y) before += (W + kXcds - 1 - y) / kXcds;
+    return {before + j, before, (W + kXcds - 1 - x) / kXcds};
+}
+
+// ---------------------------------------------------------------------------------
+// Down role. The (unit, column tile) pairs of units [u0, u1), in unit-major order, are
+// split into contiguous ranges, one per XCD (in proportion to its down workers); inside
+// its XCD's range a worker visits pairs tile-major (one column tile across consecutive
+// units), so a run of pairs sharing a tile is summed locally and reaches the column
+// accumulators as one atomic per column. Up to kMaxDnTiles pairs per round: their weight
+// loads are issued together, then the h of all of them is staged in one polling pass.
+// ---------------------------------------------------------------------------------
+
+// Tile-major walk over the unit-major pair range [pa, pb) (T tiles per unit): tile t
+// holds the relative units [first_unit(t), end_unit(t)), possibly none at the range's
+// partial ends.
+struct PairRange {
+    uint32_t ua, ta, ub, tb, T;
+    __device__ PairRange(uint32_t pa, uint32_t pb, uint32_t tiles)
+        : ua(pa / tiles), ta(pa % tiles), ub((pb - 1) / tiles), tb((pb - 1) % tiles), T(tiles) {}
+    __device__ uint32_t first_unit(uint32_t t) const { return ua + (t < ta ? 1u : 0u); }
+    __device__ uint32_t end_unit(uint32_t t) const { return ub + 1 - (t > tb ? 1u : 0u); }
+    // pair at tile-major offset s of the range
+    __device__ void locate(uint32_t s, uint32_t* unit, uint32_t* tile) const {
+        uint32_t t = 0;
+        for (; t + 1 < T; ++t) {
+            const uint32_t c = end_unit(t) - first_unit(t);
+            if (s < c) break;
+            s -= c;
+        }
+        *tile = t;
+        *unit = first_unit(t) + s;
+    }
+    // next pair in tile-major order (tiles without units are skipped)
+    __device__ void advance(uint32_t* unit, uint32_t* tile) const {
+        ++*unit;
+        while (*tile < T && *unit >= end_unit(*tile)) {
+            ++*tile;
+            if (*tile < T) *unit = first_unit(*tile);
+        }
+    }
+};
+
+// Column accumulation of one thread (column c0 + threadIdx.x of the current tile run):
+// a local fixed-point sum of m contributions, flushed as one packed atomic; the returned
+// word is checked at the next flush (or at the end) so the atomic's latency overlaps work.
+struct ColumnRun {
+    long long sum = 0;
+    uint32_t m = 0;
+    int col = -1;
+    unsigned long long pend = 0;
+    int pend_col = -1;
+};
+
+__device__ __forceinline__ void check_pending(const MlpArgs& a, ColumnRun& r, uint32_t U) {
+    if (r.pend_col >= 0 && U && (uint32_t)(r.pend >> 52) == U) write_output(a, r.pend_col, r.pend, U);
+    r.pend_col = -1;
+}
+
+__device__ __forceinline__ void flush_run(const MlpArgs& a, unsigned long long* yacc, ColumnRun& r, uint32_t U) {
+    if (r.m == 0) return;
+    const unsigned long long add =
+        (unsigned long long)(r.sum + (long long)r.m * kAccBias) + (unsigned long long)r.m * kAccOne;
+    const unsigned long long now =
+        __hip_atomic_fetch_add(yacc + r.col, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+    check_pending(a, r, U);
+    r.pend = now;
+    r.pend_col = r.col;
+    r.sum = 0;
+    r.m = 0;
+}
+
+// Adds the reduced tile value of this thread's column into its run (new run when the
+// column changes). Out-of-range values are clipped and reported.
+__device__ __forceinline__ void run_add(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, ColumnRun& r,
+                                        int col, float value, uint32_t U) {
+    if (col != r.col) {
+        flush_run(a, yacc, r, U);
+        r.col = col;
+    }
+    float v = value * kAccScale;
+    if (!(fabsf(v) < (float)(kAccBias - 1))) {  // out of range or NaN: clip and report
+        v = v > 0.f ? (float)(kAccBias - 1) : -(float)(kAccBias - 1);
+        raise_status(a, slot, kStatusRange);
+    }
+    r.sum += __float2ll_rn(v);
+    r.m += 1;
+}
+
+// One round of up to kMaxDnTiles (unit, column tile) pairs of the down projection:
+// every weight and scale load of the round is issued first (dn_issue_round), then h and
+// the scales are staged in LDS in one polling pass and each pair's tile is computed and
+// added into the column runs (dn_finish_round).
+struct DnRound {
+    DnLoads dl[kMaxDnTiles];
+    uint32_t sv[kMaxDnTiles];                        // this thread's staged scale (fp16 bits)
+    uint32_t tile[kMaxDnTiles], index[kMaxDnTiles];  // column tile, unit index
+    uint32_t npairs;
+};
+
+// unit_of(i, &unit) names pair i's validated unit.
+template <int D, class UnitOf>
+__device__ __forceinline__ bool dn_issue_round(const MlpArgs& a, Shared& sh, const DnGeom& gm, DnRound& rd,
+                                               UnitOf unit_of) {
+    const int tc = a.dn_tile;
+#pragma unroll
+    for (int i = 0; i < kMaxDnTiles; ++i) {
+        rd.sv[i] = 0;
+        if ((uint32_t)i < rd.npairs) {
+            Unit u;
+            if (!unit_of(i, &u)) return false;
+            dn_issue<D>(u.grp, gm, (int)rd.tile[i] * tc, rd.dl[i]);
+            rd.sv[i] = dn_scale_issue<D>(u.sc, gm, a.group_size, (int)rd.tile[i] * tc);
+            if (threadIdx.x == 0) sh.pdest[i] = u.dest;
+        }
+    }
+    return true;
+}
+
+template <int D>
+__device__ __forceinline__ bool dn_finish_round(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
+                                                const DnGeom& gm, const DnRound& rd, uint32_t U, ColumnRun& run) {
+    const int tc = a.dn_tile;
+    const uint32_t hstride = (uint32_t)gm.rpp * kMaxRows;
+    if (!stage_round(a, slot, sh, rd.npairs, gm, a.group_size, rd.sv)) return false;
+#pragma unroll
+    for (int i = 0; i < kMaxDnTiles; ++i) {
+        if ((uint32_t)i < rd.npairs) {
+            dn_compute(rd.dl[i], gm, sh.hs + i * hstride, sh.ss + i * kTileScales, sh.red, tc);
+            if (threadIdx.x < (uint32_t)tc)
+                run_add(a, slot, yacc, run, (int)rd.tile[i] * tc + threadIdx.x, sh.red[kRedFloats + threadIdx.x], U);
+            if (a.executions) count_execution(a, slot, rd.index[i], sh.pdest[i], D / tc);
+        }
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------------
+// Units [u0, u1) on W persistent workers. Every worker takes a share of both halves:
+//  - gate/up: a contiguous range of neuron batches (gate_up_share);
+//  - down: the (unit, column tile) pairs, in unit-major order, are split into one
+//    contiguous range per XCD (in proportion to its workers); inside it a worker visits
+//    its pairs tile-major (one column tile across consecutive units), so a run of pairs
+//    sharing a tile is summed locally and reaches the column accumulators as one atomic
+//    per column.
+// The loads of the first down round are issued before the gate/up share (one descriptor
+// fetch covers both), so they stream with the gate/up loads. A worker waits for h only
+// after its whole gate/up share is done, hence every h is eventually published.
+// ---------------------------------------------------------------------------------
+template <int D, bool FUSED>
+__device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
+                                              unsigned long long* yacc, XRegs<D, Batch<D>::N>& xr, bool& have_x,
+                                              uint32_t u0, uint32_t u1, const Place& pl, uint32_t W,
+                                              uint32_t early) {
+    constexpr int NB = Batch<D>::N;
     const int G = a.group_size;
-    // gate/up for every slice first so that the whole h row exists, then the tiles.
-    for (int j = 0; j < S; ++j) {
-        if (j == 0 && threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
-        GuLoads<D, NS> gl;
-        gu_issue<D, NS>(u.grp, u.sc, j * NS, gl);
-        gu_compute<D, NS>(gl, xr, a.hbuf + (size_t)u.dest * G, j * NS, a.seq);
+    const int tc = a.dn_tile;
+    const uint32_t T = D / tc;                                    // tiles per unit
+    // gate/up share
+    const uint32_t bpu = (G + NB - 1) / NB;                       // batches per unit
+    const uint32_t nb = (u1 - u0) * bpu;
+    const uint32_t per_g = (nb + W - 1) / W;
+    const uint32_t g0 = min(pl.k * per_g, nb), g1 = min(g0 + per_g, nb);
+    // down share: this XCD's pair range, then this worker's part of it
+    const uint32_t P = (u1 - u0) * T;
+    const uint32_t pa = (uint32_t)((uint64_t)P * pl.base / W);
+    const uint32_t pb = (uint32_t)((uint64_t)P * (pl.base + pl.count) / W);
+    const uint32_t j = pl.k - pl.base;
+    const uint32_t s0 = (uint32_t)((uint64_t)(pb - pa) * j / pl.count);
+    const uint32_t s1 = (uint32_t)((uint64_t)(pb - pa) * (j + 1) / pl.count);
+    const PairRange range(pa, pb > pa ? pb : pa + 1, T);
+    uint32_t cu = 0, ct = 0;   // next down pair: relative unit, tile
+    if (s0 < s1) range.locate(s0, &cu, &ct);
+    const DnGeom gm(G, tc);
+    // first down round + first gate/up units: one descriptor fetch
+    DnRound rd;
+    rd.npairs = s0 < s1 ? min((uint32_t)kMaxDnTiles, s1 - s0) : 0u;
+#pragma unroll
+    for (int i = 0; i < kMaxDnTiles; ++i) {
+        rd.tile[i] = 0;
+        rd.index[i] = 0;
+        if ((uint32_t)i < rd.npairs) {
+            rd.tile[i] = ct;
+            rd.index[i] = u0 + cu;
+            if (threadIdx.x == 0) sh.ulist[i] = u0 + cu;
+            range.advance(&cu, &ct);
+        }
     }
-    const int tc = D / S;
-    DnGeom gm(G, tc);
-    const uint32_t U = FUSED ? a.core_count + sh.ep_total : 0u;
-    for (int j = 0; j < S; ++j) {
-        const int c0 = j * tc;
-        DnLoads dl;
-        dn_issue<D>(u.grp, u.sc, gm, c0, dl);
-        if (threadIdx.x == 0) sh.word[3] = 0;
-        __syncthreads();
-        if (!dn_compute(a, slot, dl, gm, a.hbuf + (size_t)u.dest * G, sh.red, &sh.word[3], tc)) return;
-        accumulate_tile(a, slot, yacc, sh.red + kRedFloats, c0, tc, U);
-    }
-    if (a.executions) {
-        drain_vmem();
-        __syncthreads();
+    uint32_t gchunk0 = 0, gchunk_n = 0;
+    if (g0 < g1) {
+        gchunk0 = u0 + g0 / bpu;
+        gchunk_n = min((uint32_t)kUnitChunk - rd.npairs, u0 + (g1 - 1) / bpu + 1 - gchunk0);
         if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            for (uint32_t i = 0; i < gchunk_n; ++i) sh.ulist[rd.npairs + i] = gchunk0 + i;
     }
+    if (rd.npairs + gchunk_n && !load_units(a, sh, slot, rd.npairs + gchunk_n)) return false;
+    if (!dn_issue_round<D>(a, sh, gm, rd, [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); }))
+        return false;
+    if (!gate_up_share<D>(a, sh, slot, b, xr, have_x, u0, g0, g1, bpu, gchunk0, gchunk_n, rd.npairs)) return false;
+    if (s0 >= s1) return true;
+    uint32_t U = 0;
+    if (FUSED) {
+        if (!await_epoch(a, sh, slot, early)) return false;
+        U = a.core_count + sh.ep_total;
+    }
+    ColumnRun run;
+    for (uint32_t done = s0;;) {
+        if (!dn_finish_round<D>(a, sh, slot, yacc, gm, rd, U, run)) return false;
+        if (done == s0) stamp(a, kStampDnComputed);
+        done += rd.npairs;
+        if (done >= s1) break;
+        rd.npairs = min((uint32_t)kMaxDnTiles, s1 - done);
+#pragma unroll
+        for (int i = 0; i < kMaxDnTiles; ++i) {
+            if ((uint32_t)i < rd.npairs) {
+                rd.tile[i] = ct;
+                rd.index[i] = u0 + cu;
+                if (threadIdx.x == 0) sh.ulist[i] = u0 + cu;
+                range.advance(&cu, &ct);
+            }
+        }
+        if (!load_units(a, sh, slot, rd.npairs)) return false;
+        if (!dn_issue_round<D>(a, sh, gm, rd,
+                               [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); }))
+            return false;
+    }
+    flush_run(a, yacc, run, U);
+    check_pending(a, run, U);
+    return true;
+}
+
+// Process a whole unit inside one workgroup (claim path): gate/up of every neuron, then
+// every column tile of the down projection, without cross-workgroup waits.
+template <int D, bool FUSED>
+__device__ __forceinline__ bool run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
+                                              const XRegs<D, Batch<D>::N>& xr, const Unit& u, uint32_t index) {
+    constexpr int NB = Batch<D>::N;
+    const int G = a.group_size;
+    uint64_t* hrow = a.hbuf + (size_t)u.dest * G;
+    if (threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
+    for (int n0 = 0; n0 < G; n0 += NB) {
+        GuLoads<D, NB> gl;
+        gu_issue<D, NB>(u.grp, u.sc, n0, min(NB, G - n0), gl);
+        gu_compute<D, NB>(gl, xr, hrow, n0, min(NB, G - n0), a.seq);
+    }
+    const int tc = a.dn_tile;
+    const uint32_t T = D / tc;
+    const DnGeom gm(G, tc);
+    const uint32_t U = FUSED ? a.core_count + sh.ep_total : 0u;
+    ColumnRun run;
+    for (uint32_t t0 = 0; t0 < T; t0 += kMaxDnTiles) {
+        DnRound rd;
+        rd.npairs = min((uint32_t)kMaxDnTiles, T - t0);
+#pragma unroll
+        for (int i = 0; i < kMaxDnTiles; ++i) {
+            rd.tile[i] = t0 + (uint32_t)i;
+            rd.index[i] = index;
+        }
+        if (!dn_issue_round<D>(a, sh, gm, rd, [&](int, Unit* out) {
+                *out = u;
+                return true;
+            }))
+            return false;
+        if (!dn_finish_round<D>(a, sh, slot, yacc, gm, rd, U, run)) return false;
+    }
+    flush_run(a, yacc, run, U);
+    check_pending(a, run, U);
+    return true;
 }
 
 // ---------------------------------------------------------------------------------
@@ -569,7 +1012,7 @@ __device__ void run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, unsi
 // ---------------------------------------------------------------------------------
 // Runs on wave 0 of the mirror workgroup. `pre` is lane 0's early 64-bit load of
 // (total_count, epoch): adjacent words (byte offsets 8 and 12), read as one pair.
-__device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
+__device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
     const uint32_t lane = threadIdx.x & 63;
     uint32_t state = 0, total = 0;
     if (lane == 0) {
@@ -658,7 +1101,7 @@ __device__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
 
 // Descriptor of published position `pos` from the device-side table; false when the
 // worker must leave (abort or timeout) before the position is mirrored.
-__device__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out) {
+__device__ __forceinline__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out) {
     __syncthreads();  // previous readers of sh.desc / sh.word[2] are done
     if (threadIdx.x == 0) {
         uint32_t ok = 1;
@@ -673,17 +1116,18 @@ __device__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint
         sh.word[2] = ok;
     }
     __syncthreads();
-    out->logical_group = sh.desc[0];
-    out->physical_group = sh.desc[1];
-    out->source_slot = sh.desc[2];
-    out->dest_slot = sh.desc[3];
-    out->source_kind = (leanstream::runtime::SourceKind)sh.desc[4];
-    return sh.word[2] != 0;
+    // every lane reads the same words: make them wave-uniform (scalar registers)
+    out->logical_group = __builtin_amdgcn_readfirstlane(sh.desc[0]);
+    out->physical_group = __builtin_amdgcn_readfirstlane(sh.desc[1]);
+    out->source_slot = __builtin_amdgcn_readfirstlane(sh.desc[2]);
+    out->dest_slot = __builtin_amdgcn_readfirstlane(sh.desc[3]);
+    out->source_kind = (leanstream::runtime::SourceKind)__builtin_amdgcn_readfirstlane(sh.desc[4]);
+    return __builtin_amdgcn_readfirstlane(sh.word[2]) != 0;
 }
 
 // Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86),
 // against the mirrored ready count. Returns the number of claimed positions (0 = leave).
-__device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total) {
+__device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total) {
     __syncthreads();  // previous readers of sh.word[5..6] are done
     if (threadIdx.x == 0) {
         uint32_t got = 0, head = 0;
@@ -715,48 +1159,53 @@ __device__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uin
     return sh.word[6];
 }
 
-template <int D, int NS, bool FUSED>
-__device__ void consume_queue(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc, const XRegs<D, NS>& xr,
-                              const Bounds& b, uint32_t W, uint32_t w, uint32_t first_item, uint32_t it) {
-    if (!await_epoch(a, sh, slot, epoch_peek(sh, slot))) return;
-    const uint32_t total = sh.ep_total;
-    const uint32_t path = sh.ep_path;
-    if (!total) return;
-    const uint32_t S = a.slices;
-    if (path == 2) {
-        // all ready: static stripes of (position, slice) items, continuing the
-        // round-robin after the core items so every worker gets an equal share.
-        const uint32_t n_items = total * S;
-        for (uint32_t i = (w + W - (first_item % W)) % W; i < n_items; i += W) {
-            const uint32_t pos = i / S, j = i % S;
-            ExecDesc d;
-            if (!load_queue_wg(a, sh, slot, pos, &d)) return;
-            const Unit u = resolve(a, b, d, D);
-            if (!u.ok) {
-                if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
-                return;
-            }
-            if (threadIdx.x == 0 && j == 0 && a.claim_log && (pos & 1) == 0 && pos / 2 < a.claim_log_cap)
-                a.claim_log[pos / 2] = pos | (min(2u, total - pos) << 24);
-            run_item<D, NS, FUSED>(a, sh, slot, yacc, xr, u, a.core_count + pos, j, it++);
-        }
-        return;
-    }
+// Claim path (progressive publication): ready pairs claimed one at a time, each unit of
+// a pair processed whole by the claiming workgroup.
+template <int D, bool FUSED>
+__device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, unsigned long long* yacc,
+                           const XRegs<D, Batch<D>::N>& xr, uint32_t total) {
     for (;;) {
         const uint32_t got = claim_pair(a, sh, slot, total);
         if (!got) return;
         const uint32_t head = sh.word[5];
         for (uint32_t k = 0; k < got; ++k) {
-            ExecDesc d;
-            if (!load_queue_wg(a, sh, slot, head + k, &d)) return;
-            const Unit u = resolve(a, b, d, D);
-            if (!u.ok) {
-                if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
-                return;
-            }
-            run_unit_solo<D, NS, FUSED>(a, sh, slot, yacc, xr, u);
+            Unit u;
+            if (!fetch_unit(a, sh, slot, b, a.core_count + head + k, D, &u)) return;
+            if (!run_unit_solo<D, FUSED>(a, sh, slot, yacc, xr, u, a.core_count + head + k)) return;
         }
     }
+}
+
+// One persistent worker of a launch: its role share of the resident (core) units, then
+// of the queue (all-ready fast path), or the claim loop (progressive path).
+// Workers [0, NG) take the gate/up role, the others the down role.
+// One persistent worker of a launch: its share of the resident (core) units, then of
+// the queue (all-ready fast path), or the claim loop (progressive path).
+template <int D, bool FUSED, bool CORE, bool QUEUE>
+__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, uint32_t* slot) {
+    const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
+    const Place pl = place_of(blockIdx.x, W);
+    unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
+    init_shared(sh);
+    XRegs<D, Batch<D>::N> xr;
+    bool have_x = false;
+    const uint32_t early = epoch_peek(sh, slot);
+    if (CORE && a.core_count &&
+        !process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, 0, a.core_count, pl, W, early))
+        return;
+    stamp(a, kStampCoreDone);
+    if (!QUEUE) return;
+    if (!await_epoch(a, sh, slot, early)) return;
+    stamp(a, kStampEpoch);
+    const uint32_t total = sh.ep_total;
+    if (!total) return;
+    if (sh.ep_path == 2) {
+        process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, a.core_count, a.core_count + total, pl, W, 0);
+    } else {
+        if (!have_x) load_x<D, Batch<D>::N>(a.x, xr);
+        claim_loop<D, FUSED>(a, sh, slot, b, yacc, xr, total);
+    }
+    stamp(a, kStampQueueDone);
 }
 
 // The mirror workgroup: wave 0 mirrors the queue while waves 1..3 clear what the next
@@ -774,86 +1223,64 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
     for (uint32_t i = t; i < a.width; i += n) st_agent_u64(other_acc + i, 0ull);
 }
 
+// Completion proof of a launch (replaces a per-launch event): every workgroup counts
+// itself out once it has finished, in two levels to keep the count off one contended
+// word -- per group of workgroups blk % kXcds (kSyncExitGroups), then the last of each
+// group in kSyncExit. The very last one stores the launch sequence into the
+// host-coherent completion word; all reads of the launch's weights are complete by then.
+__device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) {
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    const uint32_t group = blockIdx.x % 8u;
+    const uint32_t members = (gridDim.x + 7u - group) / 8u;
+    const uint32_t groups = gridDim.x < 8u ? gridDim.x : 8u;
+    if (add_agent(slot + kSyncExitGroups + group * kLine, 1u) == members - 1 &&
+        add_agent(slot + kSyncExit, 1u) == groups - 1)
+        __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { return a.yacc + (a.seq & 1) * a.width; }
 
 // ---------------------------------------------------------------------------------
 // Kernels. Persistent launches have gridDim.x = workers + 1; the last block mirrors.
 // ---------------------------------------------------------------------------------
 
-// Fused layer: core items (stage A role), queue consumption (stage B role) and the
-// compact reduction (U-th contributor of each column tile), one persistent launch.
-template <int D, int NS>
+// Fused layer: resident (core) units, queue consumption and the compact reduction (the
+// contribution completing a column writes it), one persistent launch.
+template <int D>
 __global__ __launch_bounds__(kThreads, 2) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    const uint32_t W = gridDim.x - 1, w = blockIdx.x;
-    if (w == W) {
+    if (blockIdx.x == gridDim.x - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
-        return;
+    } else {
+        stamp(a, kStampEntry);
+        worker<D, true, true, true>(a, b, sh, slot);
+        stamp(a, kStampExit);
     }
-    stamp(a, kStampEntry);
-    unsigned long long* yacc = launch_acc(a);
-    const uint32_t S = a.slices;
-    const uint32_t n_core = a.core_count * S;
-    // the first core descriptor is read before anything else: every later load waits
-    // behind it in the in-order return queue
-    ExecDesc d0 = w < n_core ? load_core(a, w / S) : ExecDesc{};
-    init_shared(sh);
-    XRegs<D, NS> xr;
-    load_x<D, NS>(a.x, xr);
-    stamp(a, kStampXLoaded);
-    uint32_t it = 0;
-    for (uint32_t i = w; i < n_core; i += W) {
-        const uint32_t unit = i / S, j = i % S;
-        const Unit u = resolve(a, b, i == w ? d0 : load_core(a, unit), D);
-        if (!u.ok) {
-            if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
-            break;
-        }
-        run_item<D, NS, true>(a, sh, slot, yacc, xr, u, unit, j, it++);
-    }
-    consume_queue<D, NS, true>(a, sh, slot, yacc, xr, b, W, w, n_core, it);
-    stamp(a, kStampExit);
+    finish_launch(a, slot);
 }
 
-// Split path, stage A: core items only (no queue, no conversion).
-template <int D, int NS>
+// Split path, stage A: resident (core) units only; no queue, no conversion.
+template <int D>
 __global__ __launch_bounds__(kThreads, 2) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    unsigned long long* yacc = launch_acc(a);
-    init_shared(sh);
-    XRegs<D, NS> xr;
-    load_x<D, NS>(a.x, xr);
-    const uint32_t S = a.slices;
-    const uint32_t n_core = a.core_count * S;
-    for (uint32_t i = blockIdx.x; i < n_core; i += gridDim.x) {
-        const uint32_t unit = i / S, j = i % S;
-        const Unit u = resolve(a, b, load_core(a, unit), D);
-        if (!u.ok) {
-            if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
-            return;
-        }
-        run_item<D, NS, false>(a, sh, slot, yacc, xr, u, unit, j, 0);
-    }
+    worker<D, false, true, false>(a, b, sh, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
-template <int D, int NS>
+template <int D>
 __global__ __launch_bounds__(kThreads, 2) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    const uint32_t W = gridDim.x - 1;
-    if (blockIdx.x == W) {
+    if (blockIdx.x == gridDim.x - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         return;
     }
-    init_shared(sh);
-    XRegs<D, NS> xr;
-    load_x<D, NS>(a.x, xr);
-    consume_queue<D, NS, false>(a, sh, slot, launch_acc(a), xr, b, W, blockIdx.x, 0, 0);
+    worker<D, false, false, true>(a, b, sh, slot);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
@@ -863,15 +1290,20 @@ __global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
     const int col = blockIdx.x * kThreads + threadIdx.x;
     const unsigned long long w = __hip_atomic_load(launch_acc(a) + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     write_output(a, col, w, (uint32_t)(w >> 52));
+    finish_launch(a, a.sync + (a.seq & 1) * a.slot_words);   // last kernel of the split launch sequence
 }
 
-// Clears both ring slots and the accumulators (bind time, or after a failed enqueue).
-__global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns) {
+// Clears both ring slots, the accumulators and the tagged h rows (bind time, after a
+// failed enqueue, or when the launch sequence wraps): afterwards no stored tag can match
+// a sequence number the next launches use.
+__global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns,
+                                  uint64_t* hbuf, uint32_t hwords) {
     // `columns` covers both accumulator buffers
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += gridDim.x * blockDim.x)
-        st_agent(sync + i, 0u);
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < columns; i += gridDim.x * blockDim.x)
-        st_agent_u64(yacc + i, 0ull);
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride) st_agent(sync + i, 0u);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < columns; i += stride) st_agent_u64(yacc + i, 0ull);
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < hwords; i += stride)
+        __hip_atomic_store(hbuf + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------
@@ -880,36 +1312,33 @@ __global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long 
 namespace {
 
 struct Variant {
-    int width, ns;
+    int width;
     const void* fused;
     const void* stage_a;
     const void* stage_b;
     const void* reduce;
 };
 
-template <int D, int NS>
+template <int D>
 Variant make_variant() {
-    return {D, NS, reinterpret_cast<const void*>(&fused_layer_kernel<D, NS>),
-            reinterpret_cast<const void*>(&stage_a_kernel<D, NS>), reinterpret_cast<const void*>(&stage_b_kernel<D, NS>),
-            reinterpret_cast<const void*>(&reduce_kernel<D>)};
+    return {D, reinterpret_cast<const void*>(&fused_layer_kernel<D>), reinterpret_cast<const void*>(&stage_a_kernel<D>),
+            reinterpret_cast<const void*>(&stage_b_kernel<D>), reinterpret_cast<const void*>(&reduce_kernel<D>)};
 }
 
-#define LS_VARIANTS_FOR(D) make_variant<D, 1>(), make_variant<D, 2>(), make_variant<D, 4>(), make_variant<D, 8>()
-
-const Variant* find_variant(int width, int ns) {
-    static const Variant table[] = {LS_VARIANTS_FOR(256),  LS_VARIANTS_FOR(512),  LS_VARIANTS_FOR(1024),
-                                    LS_VARIANTS_FOR(2048), LS_VARIANTS_FOR(4096), LS_VARIANTS_FOR(8192)};
+const Variant* find_variant(int width) {
+    static const Variant table[] = {make_variant<256>(),  make_variant<512>(),  make_variant<1024>(),
+                                    make_variant<2048>(), make_variant<4096>(), make_variant<8192>()};
     for (const Variant& v : table)
-        if (v.width == width && v.ns == ns) return &v;
+        if (v.width == width) return &v;
     return nullptr;
 }
 
 }  // namespace
 
-bool variant_available(int width, int ns) { return find_variant(width, ns) != nullptr; }
+bool variant_available(int width) { return find_variant(width) != nullptr; }
 
-hipError_t resident_workers(int width, int ns, int entry_point, int* per_cu) {
-    const Variant* v = find_variant(width, ns);
+hipError_t resident_workers(int width, int entry_point, int* per_cu) {
+    const Variant* v = find_variant(width);
     if (!v) return hipErrorInvalidValue;
     const void* k = entry_point == kEntryFused ? v->fused : v->stage_b;
     int n = 0;
@@ -924,18 +1353,16 @@ hipError_t resident_workers(int width, int ns, int entry_point, int* per_cu) {
 }
 
 hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& bounds, hipStream_t stream) {
-    const Variant* v = find_variant(p.width, p.ns);
-    if (!v) return hipErrorInvalidValue;
+    const Variant* v = find_variant(p.width);
+    if (!v || p.workers < 1) return hipErrorInvalidValue;
     MlpArgs a = args;
     Bounds b = bounds;
     void* kargs[] = {&a, &b};
     if (p.entry_point == kEntryFused)
         return hipLaunchKernel(v->fused, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     hipError_t e = hipSuccess;
-    const uint32_t core_items = a.core_count * a.slices;
-    if (core_items) {
-        const uint32_t grid = core_items < (uint32_t)p.workers ? core_items : (uint32_t)p.workers;
-        e = hipLaunchKernel(v->stage_a, dim3(grid), dim3(kThreads), kargs, 0, stream);
+    if (a.core_count) {
+        e = hipLaunchKernel(v->stage_a, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
         if (e != hipSuccess) return e;
     }
     e = hipLaunchKernel(v->stage_b, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
@@ -944,11 +1371,13 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     return hipLaunchKernel(v->reduce, dim3(p.width / kThreads), dim3(kThreads), rargs, 0, stream);
 }
 
-hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, hipStream_t stream) {
-    uint32_t grid = (words + kThreads - 1) / kThreads;
+hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
+                      uint32_t hwords, hipStream_t stream) {
+    const uint32_t most = words > hwords ? words : hwords;
+    uint32_t grid = (most + kThreads - 1) / kThreads;
     if (grid > 1024) grid = 1024;
     if (!grid) grid = 1;
-    void* kargs[] = {&sync, &words, &yacc, &columns};
+    void* kargs[] = {&sync, &words, &yacc, &columns, &hbuf, &hwords};
     return hipLaunchKernel(reinterpret_cast<const void*>(&clear_sync_kernel), dim3(grid), dim3(kThreads), kargs, 0,
                            stream);
 }

@@ -302,3 +302,53 @@ def test_closed_form_known_answer(torch_gpu, count, byte, q):
     assert np.all(ex.cpu().numpy() == 1)
     be.close()
     queue.close()
+
+
+# ---------------------------------------------------------------------------- completion / reuse
+def test_completion_word_follows_the_launch(torch_gpu):
+    """ComputeBackend::complete (runtime.h:14): false while the launch waits for its layer
+    epoch, true once every workgroup has finished."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1"]
+    log("case: completion word while a launch waits for an unsealed queue")
+    layer = DeviceLayer(cfg)
+    layer.queue.reset(3)                       # epoch 3 not sealed yet: the launch waits
+    stream = torch.cuda.current_stream().cuda_stream
+    layer.backend.enqueue(0, 0, 3, layer.x, layer.y, stream, layer.core_ptr(0), layer.k, layer.queue)
+    time.sleep(0.02)
+    assert not layer.backend.complete()
+    layer.queue.seal(0)
+    deadline = time.time() + 5.0
+    while not layer.backend.complete() and time.time() < deadline:
+        time.sleep(0.001)
+    assert layer.backend.complete()
+    sync_and_check_status(torch, layer)
+    for i in range(3):                         # later launches move the word forward
+        layer.run_core(copy=0, epoch=3)
+    torch.cuda.synchronize()
+    assert layer.backend.complete()
+    layer.close()
+
+
+def test_rebinding_a_used_hidden_buffer(torch_gpu):
+    """A new backend bound to a hidden buffer that an earlier backend filled with tagged
+    h (same launch sequence numbers) must not consume the stale words."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1"]
+    log("case: second backend on the first backend's hidden buffer")
+    layer = DeviceLayer(cfg, copies=2)
+    layer.seal_empty_queue(1)
+    layer.run_core(copy=1, epoch=1)            # tags of sequence 1 for every row, copy-1 data
+    sync_and_check_status(torch, layer)
+    layer.backend.close()
+    layer.backend = NativeBackend()
+    n = cfg.groups
+    layer.backend.bind(cfg.width, cfg.group_size, layer.slot_capacity, layer.cache, layer.scales,
+                       physical_groups=2 * n, cache_groups=2 * n, staging=layer.cache, staging_groups=2 * n,
+                       queue_capacity=layer.queue.capacity, hidden=layer.hidden, partial=layer.partial,
+                       y32=layer.y32, executions=layer.executions)
+    layer.run_core(copy=0, epoch=1)            # sequence 1 again, copy-0 data
+    sync_and_check_status(torch, layer)
+    ref = oracle_for(layer, layer.core_rows[0])
+    compare(layer.y32.cpu().numpy(), ref["y32"], "rebound backend")
+    layer.close()
