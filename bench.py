@@ -42,7 +42,23 @@ def parse():
     ap.add_argument("--isolated", type=int, default=100, help="isolated launches timed one by one")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 5 plain 64 MiB device copies (counter calibration for rocprofv3 --pmc)")
     return ap.parse_args()
+
+
+def copy_calibration():
+    """Five plain device-to-device copies of 64 MiB: each dispatch reads and writes exactly
+    67108864 bytes, the known size that FETCH_SIZE / WRITE_SIZE are scaled against."""
+    import torch
+
+    n = 64 * 2 ** 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "dispatches": 5}), flush=True)
 
 
 def percentile(v, q):
@@ -110,6 +126,9 @@ def main():
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
         sys.exit(2)
+    if a.copy_calibration:
+        copy_calibration()
+        return
     import torch
 
     from leanstream_amd import synth
@@ -184,7 +203,7 @@ def main():
             "rotation_active_bytes": copies * active_bytes,
             "candidate": candidate,
             "resident_workers": workers,
-            "isolated_us_p10_p50_p90": [round(percentile(iso, q), 3) for q in (0.1, 0.5, 0.9)],
+            "isolated_us_p10_p50_p90": [round(percentile(iso, q), 3) for q in (0.1, 0.5, 0.9)] if iso else None,
         },
         "roofline": {
             "bound": "hbm",
