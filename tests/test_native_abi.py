@@ -1,0 +1,137 @@
+"""The C ABI of libleanstream_hip.so on the CPU (no GPU calls): exported symbols, the
+ready-queue producer on host memory, kernel selection, ranking."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from leanstream_amd import _native
+from leanstream_amd._native import DeviceQueue
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "leanstream_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ls_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_entry_point_is_exported_and_bound():
+    lib = _native.library()
+    names = declared_functions()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in include/leanstream_hip.h but not exported"
+    assert sorted(_native.EXPORTED) == names, "ctypes signatures and the header disagree"
+
+
+class HostQueue:
+    """DeviceExecQueue over plain numpy memory (the producer never touches the GPU)."""
+
+    def __init__(self, capacity):
+        self.desc = np.zeros(capacity * 5, dtype=np.uint32)
+        self.idx = np.zeros(capacity, dtype=np.uint32)
+        self.ctrl = np.zeros(32, dtype=np.uint32)   # 128-byte QueueControl
+        self.view = DeviceQueue(self.desc.ctypes.data, self.idx.ctypes.data, self.ctrl.ctypes.data, capacity)
+        self.lib = _native.library()
+        self.h = self.lib.ls_queue_create(C.byref(self.view))
+        assert self.h
+
+    def words(self):
+        c = self.ctrl
+        return dict(ready=int(c[0]), total=int(c[2]), epoch=int(c[3]), batch=int(c[4]), error=int(c[5]))
+
+    def close(self):
+        self.lib.ls_queue_destroy(self.h)
+
+
+def test_queue_publication_order_and_first_error_wins():
+    """execution_queue.cpp:4-46; open_source_runtime_test.cpp:61-67 (order {2,0,3,1})."""
+    q = HostQueue(8)
+    lib = q.lib
+    lib.ls_queue_reset(q.h, 7)
+    lib.ls_queue_seal(q.h, 4)
+    assert q.words() == dict(ready=0, total=4, epoch=7, batch=0, error=0)
+    for i in (2, 0, 3, 1):
+        lib.ls_queue_publish(q.h, i)
+    assert q.words() == dict(ready=4, total=4, epoch=7, batch=7, error=0)
+    assert q.idx[:4].tolist() == [2, 0, 3, 1]
+    lib.ls_queue_reset(q.h, 9)
+    lib.ls_queue_prepare(q.h, 5)
+    lib.ls_queue_append_unpublished(q.h, 3)
+    lib.ls_queue_append_unpublished(q.h, 0)
+    assert q.words()["epoch"] == 0          # nothing visible before activation
+    lib.ls_queue_activate(q.h)
+    assert q.words() == dict(ready=2, total=5, epoch=9, batch=0, error=0)
+    lib.ls_queue_fail(q.h, 5)
+    lib.ls_queue_fail(q.h, 7)
+    assert q.words()["error"] == 5
+    lib.ls_queue_reset(q.h, 10)
+    lib.ls_queue_seal(q.h, 3)
+    lib.ls_queue_publish_all(q.h)
+    assert q.words() == dict(ready=3, total=3, epoch=10, batch=10, error=0)
+    assert q.idx[:3].tolist() == [0, 1, 2]
+    q.close()
+
+
+def test_quantize_io_load_known_answers():
+    """kernel_selector_test.cpp:20-26."""
+    f = _native.library().ls_quantize_io_load
+    big = 0xFFFFFFFF
+    assert f(1, 1, 8) == 7 and f(10, 8, 8) == 7
+    assert f(0, 0, 8) == 0 and f(1, 0, 8) == 0 and f(1, 8, 0) == 0 and f(0, 8, 8) == 0
+    assert [f(i, 8, 8) for i in range(8)] == list(range(8))
+    assert f(big - 1, big, 8) == 7 and f(big - 1, big, big) == big - 1
+
+
+def test_hip_selector_table_and_fallback():
+    """kernel_selector.cpp:4-22 over the CDNA4 catalog: valid ids are taken from the
+    table, anything else (id out of the catalog, layer/bucket out of range) falls back
+    to the default candidate."""
+    lib = _native.library()
+    table = (C.c_uint8 * 6)(0, 1, 2, 3, 4, 255)
+    ctx = lib.ls_hip_create_table(table, 1, 6)
+    assert ctx
+    try:
+        assert [lib.ls_hip_select(ctx, 0, b) for b in range(5)] == [0, 1, 2, 3, 4]
+        default = lib.ls_hip_select(ctx, 0, 5)
+        assert default == 1
+        assert lib.ls_hip_select(ctx, 1, 0) == default and lib.ls_hip_select(ctx, 0, 6) == default
+        assert lib.ls_hip_last_candidate(ctx) == -1      # nothing enqueued yet
+    finally:
+        lib.ls_hip_destroy(ctx)
+    ctx = lib.ls_hip_create()
+    assert lib.ls_hip_select(ctx, 3, 3) == 1
+    lib.ls_hip_destroy(ctx)
+
+
+def test_compute_backend_view_size_check():
+    lib = _native.library()
+    ctx = lib.ls_hip_create()
+    buf = (C.c_uint8 * 64)()
+    assert lib.ls_hip_compute_backend(ctx, buf, 8) != 0          # too small for the struct
+    assert lib.ls_hip_compute_backend(ctx, buf, 64) == 0
+    ptrs = np.frombuffer(bytes(buf), dtype=np.uint64)[:6]
+    assert ptrs[0] == ctx and ptrs[1] != 0 and ptrs[2] != 0     # context, enqueue, complete
+    lib.ls_hip_destroy(ctx)
+
+
+@pytest.mark.parametrize("seed", [1, 2, 3])
+def test_rank_groups_matches_oracle(seed):
+    """predictor_cpu.cpp:192-201: top-k by (score desc, id asc)."""
+    rng = np.random.default_rng(seed)
+    scores = rng.standard_normal(448).astype(np.float32)
+    scores[rng.integers(0, 448, 40)] = 0.5     # ties
+    lib = _native.library()
+    for k in (0, 1, 58, 90, 448):
+        out = np.zeros(max(1, k), dtype=np.int32)
+        assert lib.ls_rank_groups(scores.ctypes.data, len(scores), k, out.ctypes.data) == 0
+        assert out[:k].tolist() == oracle.rank(scores, k).tolist()
+    bad = scores.copy()
+    bad[3] = np.nan
+    out = np.zeros(4, dtype=np.int32)
+    assert lib.ls_rank_groups(bad.ctypes.data, len(bad), 4, out.ctypes.data) != 0
