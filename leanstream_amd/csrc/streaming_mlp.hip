@@ -599,7 +599,6 @@ __device__ __forceinline__ bool fetch_unit(const MlpArgs& a, Shared& sh, uint32_
 // One memory round trip (two when queue positions must first be waited for).
 __device__ __forceinline__ bool load_units(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t n) {
     __syncthreads();  // ulist written; earlier readers of udesc are done
-    stamp(a, 10);
     if (threadIdx.x == 0) {
         uint32_t need = 0;  // queue positions that must be mirrored
         for (uint32_t i = 0; i < n; ++i)
@@ -623,7 +622,6 @@ __device__ __forceinline__ bool load_units(const MlpArgs& a, Shared& sh, uint32_
                                           : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
     __syncthreads();
-    stamp(a, 11);
     return true;
 }
 
@@ -647,16 +645,16 @@ __device__ __forceinline__ bool unit_from(const MlpArgs& a, Shared& sh, uint32_t
 // ---------------------------------------------------------------------------------
 // Gate/up share: batches [g0, g1) of Batch<D>::N neurons (never straddling a unit; unit
 // u0 + bi / bpu holds batch bi), kGuBuffers batches in flight, h stored tagged with the
-// launch sequence. The weight loads of the first batches are issued before x is loaded
-// (x is only needed to compute). Descriptors of units [chunk0, chunk0 + chunk_n) are
+// launch sequence. after_first() runs right after the first batch's loads are issued
+// (the caller's own loads go there). Descriptors of units [chunk0, chunk0 + chunk_n) are
 // already in sh.udesc from slot chunk_off on; later units are fetched kUnitChunk at a time.
 // Never waits for another workgroup's h, so every worker finishes its share.
 // ---------------------------------------------------------------------------------
-template <int D>
+template <int D, class AfterFirst>
 __device__ __forceinline__ bool gate_up_share(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
                                               XRegs<D, Batch<D>::N>& xr, bool& have_x, uint32_t u0, uint32_t g0,
                                               uint32_t g1, uint32_t bpu, uint32_t chunk0, uint32_t chunk_n,
-                                              uint32_t chunk_off) {
+                                              uint32_t chunk_off, AfterFirst after_first) {
     constexpr int NB = Batch<D>::N;
     const uint32_t G = a.group_size;
     if (g0 >= g1) return true;
@@ -684,14 +682,18 @@ __device__ __forceinline__ bool gate_up_share(const MlpArgs& a, Shared& sh, uint
         gu_issue<D, NB>(u.grp, u.sc, m.n0, m.nvalid, L);
         return true;
     };
-    GuLoads<D, NB> L[kGuBuffers];
-    Meta M[kGuBuffers];
-#pragma unroll
-    for (int q = 0; q < kGuBuffers; ++q)
-        if (g0 + q < g1 && !issue(g0 + q, L[q], M[q])) return false;
+    // Loads return in issue order (vmcnt), so the issue order is the order data can be
+    // used in: x, the first batch, then the caller's loads (after_first), then the rest.
     if (!have_x) {
         load_x<D, NB>(a.x, xr);
         have_x = true;
+    }
+    GuLoads<D, NB> L[kGuBuffers];
+    Meta M[kGuBuffers];
+#pragma unroll
+    for (int q = 0; q < kGuBuffers; ++q) {
+        if (g0 + q < g1 && !issue(g0 + q, L[q], M[q])) return false;
+        if (q == 0 && !after_first()) return false;
     }
     for (uint32_t bi = g0; bi < g1; bi += kGuBuffers) {
 #pragma unroll
@@ -713,58 +715,23 @@ __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot
         __hip_atomic_fetch_add(a.executions + dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// Placement of persistent worker `blk` of W. Workgroups are dispatched round-robin over
-// the XCDs (blk % kXcds); the work index k runs contiguously inside an XCD, so workers
-// [base, base + count) share this worker's XCD (and its L2) and neighbouring work
-// ranges -- consecutive tiles of one unit, which share scale lines -- meet in one L2.
-constexpr uint32_t kXcds = 8;
-struct Place {
-    uint32_t k;       // work index
-    uint32_t base;    // first work index on this XCD
-    uint32_t count;   // workers on this XCD
-};
-__device__ __forceinline__ Place place_of(uint32_t blk, uint32_t W) {
-    const uint32_t x = blk % kXcds, j = blk / kXcds;
-    uint32_t before = 0;  // workers on XCDs < x
-    for (uint32_t y = 0; y < x; ++y) before += (W + kXcds - 1 - y) / kXcds;
-    return {before + j, before, (W + kXcds - 1 - x) / kXcds};
-}
-
 // ---------------------------------------------------------------------------------
-// Down role. The (unit, column tile) pairs of units [u0, u1), in unit-major order, are
-// split into contiguous ranges, one per XCD (in proportion to its down workers); inside
-// its XCD's range a worker visits pairs tile-major (one column tile across consecutive
-// units), so a run of pairs sharing a tile is summed locally and reaches the column
-// accumulators as one atomic per column. Up to kMaxDnTiles pairs per round: their weight
-// loads are issued together, then the h of all of them is staged in one polling pass.
+// Down projection work: the (unit, column tile) pairs of units [u0, u1) in tile-major
+// order -- position p is tile p / units, unit p % units -- cut into one contiguous range
+// per worker. A worker's consecutive pairs mostly share a column tile, so a run of them
+// is summed locally and reaches the column accumulators as one atomic per column. Up to
+// kMaxDnTiles pairs per round: their weight loads are issued together, then the h of all
+// of them is staged in one polling pass.
 // ---------------------------------------------------------------------------------
 
-// Tile-major walk over the unit-major pair range [pa, pb) (T tiles per unit): tile t
-// holds the relative units [first_unit(t), end_unit(t)), possibly none at the range's
-// partial ends.
-struct PairRange {
-    uint32_t ua, ta, ub, tb, T;
-    __device__ PairRange(uint32_t pa, uint32_t pb, uint32_t tiles)
-        : ua(pa / tiles), ta(pa % tiles), ub((pb - 1) / tiles), tb((pb - 1) % tiles), T(tiles) {}
-    __device__ uint32_t first_unit(uint32_t t) const { return ua + (t < ta ? 1u : 0u); }
-    __device__ uint32_t end_unit(uint32_t t) const { return ub + 1 - (t > tb ? 1u : 0u); }
-    // pair at tile-major offset s of the range
-    __device__ void locate(uint32_t s, uint32_t* unit, uint32_t* tile) const {
-        uint32_t t = 0;
-        for (; t + 1 < T; ++t) {
-            const uint32_t c = end_unit(t) - first_unit(t);
-            if (s < c) break;
-            s -= c;
-        }
-        *tile = t;
-        *unit = first_unit(t) + s;
-    }
-    // next pair in tile-major order (tiles without units are skipped)
-    __device__ void advance(uint32_t* unit, uint32_t* tile) const {
-        ++*unit;
-        while (*tile < T && *unit >= end_unit(*tile)) {
-            ++*tile;
-            if (*tile < T) *unit = first_unit(*tile);
+// Position in the tile-major pair order (relative unit, tile).
+struct PairCursor {
+    uint32_t unit, tile, units;
+    __device__ PairCursor(uint32_t p, uint32_t n) : unit(p % n), tile(p / n), units(n) {}
+    __device__ void advance() {
+        if (++unit == units) {
+            unit = 0;
+            ++tile;
         }
     }
 };
@@ -866,19 +833,15 @@ __device__ __forceinline__ bool dn_finish_round(const MlpArgs& a, Shared& sh, ui
 // ---------------------------------------------------------------------------------
 // Units [u0, u1) on W persistent workers. Every worker takes a share of both halves:
 //  - gate/up: a contiguous range of neuron batches (gate_up_share);
-//  - down: the (unit, column tile) pairs, in unit-major order, are split into one
-//    contiguous range per XCD (in proportion to its workers); inside it a worker visits
-//    its pairs tile-major (one column tile across consecutive units), so a run of pairs
-//    sharing a tile is summed locally and reaches the column accumulators as one atomic
-//    per column.
-// The loads of the first down round are issued before the gate/up share (one descriptor
-// fetch covers both), so they stream with the gate/up loads. A worker waits for h only
-// after its whole gate/up share is done, hence every h is eventually published.
+//  - down: a contiguous range of the tile-major (unit, column tile) pairs (PairCursor).
+// The loads of the first down round are issued right after the first gate/up batch (one
+// descriptor fetch covers both), so they stream with the gate/up loads. A worker waits
+// for h only after its whole gate/up share is done, hence every h is eventually published.
 // ---------------------------------------------------------------------------------
 template <int D, bool FUSED>
 __device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
                                               unsigned long long* yacc, XRegs<D, Batch<D>::N>& xr, bool& have_x,
-                                              uint32_t u0, uint32_t u1, const Place& pl, uint32_t W,
+                                              uint32_t u0, uint32_t u1, uint32_t k, uint32_t W,
                                               uint32_t early) {
     constexpr int NB = Batch<D>::N;
     const int G = a.group_size;
@@ -888,17 +851,13 @@ __device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint
     const uint32_t bpu = (G + NB - 1) / NB;                       // batches per unit
     const uint32_t nb = (u1 - u0) * bpu;
     const uint32_t per_g = (nb + W - 1) / W;
-    const uint32_t g0 = min(pl.k * per_g, nb), g1 = min(g0 + per_g, nb);
-    // down share: this XCD's pair range, then this worker's part of it
-    const uint32_t P = (u1 - u0) * T;
-    const uint32_t pa = (uint32_t)((uint64_t)P * pl.base / W);
-    const uint32_t pb = (uint32_t)((uint64_t)P * (pl.base + pl.count) / W);
-    const uint32_t j = pl.k - pl.base;
-    const uint32_t s0 = (uint32_t)((uint64_t)(pb - pa) * j / pl.count);
-    const uint32_t s1 = (uint32_t)((uint64_t)(pb - pa) * (j + 1) / pl.count);
-    const PairRange range(pa, pb > pa ? pb : pa + 1, T);
-    uint32_t cu = 0, ct = 0;   // next down pair: relative unit, tile
-    if (s0 < s1) range.locate(s0, &cu, &ct);
+    const uint32_t g0 = min(k * per_g, nb), g1 = min(g0 + per_g, nb);
+    // down share: pairs [s0, s1) of the tile-major order
+    const uint32_t nu = u1 - u0;
+    const uint32_t P = nu * T;
+    const uint32_t per_d = (P + W - 1) / W;
+    const uint32_t s0 = min(k * per_d, P), s1 = min(s0 + per_d, P);
+    PairCursor cur(s0, nu);   // next down pair
     const DnGeom gm(G, tc);
     // first down round + first gate/up units: one descriptor fetch
     DnRound rd;
@@ -908,10 +867,10 @@ __device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint
         rd.tile[i] = 0;
         rd.index[i] = 0;
         if ((uint32_t)i < rd.npairs) {
-            rd.tile[i] = ct;
-            rd.index[i] = u0 + cu;
-            if (threadIdx.x == 0) sh.ulist[i] = u0 + cu;
-            range.advance(&cu, &ct);
+            rd.tile[i] = cur.tile;
+            rd.index[i] = u0 + cur.unit;
+            if (threadIdx.x == 0) sh.ulist[i] = u0 + cur.unit;
+            cur.advance();
         }
     }
     uint32_t gchunk0 = 0, gchunk_n = 0;
@@ -922,9 +881,15 @@ __device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint
             for (uint32_t i = 0; i < gchunk_n; ++i) sh.ulist[rd.npairs + i] = gchunk0 + i;
     }
     if (rd.npairs + gchunk_n && !load_units(a, sh, slot, rd.npairs + gchunk_n)) return false;
-    if (!dn_issue_round<D>(a, sh, gm, rd, [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); }))
+    auto issue_down = [&]() {
+        return dn_issue_round<D>(a, sh, gm, rd, [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); });
+    };
+    if (g0 < g1) {
+        if (!gate_up_share<D>(a, sh, slot, b, xr, have_x, u0, g0, g1, bpu, gchunk0, gchunk_n, rd.npairs, issue_down))
+            return false;
+    } else if (!issue_down()) {
         return false;
-    if (!gate_up_share<D>(a, sh, slot, b, xr, have_x, u0, g0, g1, bpu, gchunk0, gchunk_n, rd.npairs)) return false;
+    }
     if (s0 >= s1) return true;
     uint32_t U = 0;
     if (FUSED) {
@@ -941,10 +906,10 @@ __device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint
 #pragma unroll
         for (int i = 0; i < kMaxDnTiles; ++i) {
             if ((uint32_t)i < rd.npairs) {
-                rd.tile[i] = ct;
-                rd.index[i] = u0 + cu;
-                if (threadIdx.x == 0) sh.ulist[i] = u0 + cu;
-                range.advance(&cu, &ct);
+                rd.tile[i] = cur.tile;
+                rd.index[i] = u0 + cur.unit;
+                if (threadIdx.x == 0) sh.ulist[i] = u0 + cur.unit;
+                cur.advance();
             }
         }
         if (!load_units(a, sh, slot, rd.npairs)) return false;
@@ -1184,14 +1149,13 @@ __device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_
 template <int D, bool FUSED, bool CORE, bool QUEUE>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
-    const Place pl = place_of(blockIdx.x, W);
     unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
     init_shared(sh);
     XRegs<D, Batch<D>::N> xr;
     bool have_x = false;
     const uint32_t early = epoch_peek(sh, slot);
     if (CORE && a.core_count &&
-        !process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, 0, a.core_count, pl, W, early))
+        !process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, 0, a.core_count, blockIdx.x, W, early))
         return;
     stamp(a, kStampCoreDone);
     if (!QUEUE) return;
@@ -1200,7 +1164,7 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     const uint32_t total = sh.ep_total;
     if (!total) return;
     if (sh.ep_path == 2) {
-        process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, a.core_count, a.core_count + total, pl, W, 0);
+        process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, a.core_count, a.core_count + total, blockIdx.x, W, 0);
     } else {
         if (!have_x) load_x<D, Batch<D>::N>(a.x, xr);
         claim_loop<D, FUSED>(a, sh, slot, b, yacc, xr, total);
@@ -1225,7 +1189,7 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
 
 // Completion proof of a launch (replaces a per-launch event): every workgroup counts
 // itself out once it has finished, in two levels to keep the count off one contended
-// word -- per group of workgroups blk % kXcds (kSyncExitGroups), then the last of each
+// word -- per group of workgroups blk % 8 (kSyncExitGroups), then the last of each
 // group in kSyncExit. The very last one stores the launch sequence into the
 // host-coherent completion word; all reads of the launch's weights are complete by then.
 __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) {
