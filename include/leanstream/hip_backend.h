@@ -97,7 +97,7 @@ private:
     Impl* impl_ = nullptr;
     KernelSelector selector_;
     uint64_t spin_limit_ = 200000000ull;  // 2 s of the 100 MHz device clock
-    uint32_t slices_ = 0, dn_tile_ = 0, max_workers_ = 0;
+    uint32_t slices_ = 0, max_workers_ = 0;
     uint32_t workers_override_ = 0;
     int last_candidate_ = -1;
     static int submit(void*, uint32_t, const void*, void*, void*, Span<ExecDesc>, DeviceExecQueue, uint32_t,

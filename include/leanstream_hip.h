@@ -78,7 +78,7 @@ int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t ou
 uint32_t ls_hip_status(void* backend);
 void ls_hip_clear_status(void* backend);
 void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
-/* Down-projection column tiles per unit (d / tile). */
+/* Down-projection items (128-column tiles) per unit: d / 128. */
 uint32_t ls_hip_slices(void* backend);
 /* Overrides the selected candidate's persistent worker count (0 = the candidate's own
  * value). No reference counterpart: a tuning knob of the persistent launch. */

@@ -51,19 +51,6 @@ struct HipBackend::Impl {
 HipBackend::HipBackend(KernelDecisionTable table) : impl_(new Impl), selector_(hip_selector(table)) {}
 HipBackend::~HipBackend() { delete impl_; }
 
-namespace {
-
-// Columns per down-projection tile: a power of two in [64, 256] with at most
-// kMaxRowsPerThread rows per thread (G * tile <= 16 * 4 * 256: 16 columns of one row per
-// thread and load). G <= 256 always admits 64.
-uint32_t choose_dn_tile(uint32_t G, uint32_t d) {
-    for (uint32_t tc = 256; tc >= 64; tc >>= 1)
-        if (d % tc == 0 && static_cast<uint64_t>(G) * tc <= 16u * lsamd::kMaxRowsPerThread * 256u) return tc;
-    return 0;
-}
-
-}  // namespace
-
 int HipBackend::bind(const HipLayerBuffers& b) {
     Impl& p = *impl_;
     if (p.bound) return EBUSY;
@@ -72,8 +59,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
         return EINVAL;
     if (b.batch != 1) return ENOTSUP;
     if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
-    const uint32_t tile = choose_dn_tile(b.group_size, b.width);
-    if (!tile || !lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
+    if (!lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
     p.buf = b;
     const uint32_t units_cap = b.slot_capacity + b.queue_capacity;
     p.slot_words = lsamd::sync_slot_words(units_cap);
@@ -121,15 +107,12 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.status = p.status;
     a.width = b.width;
     a.group_size = b.group_size;
-    a.slices = b.width / tile;
-    a.dn_tile = tile;
-    a.g_recip = ((1ull << 32) + b.group_size - 1) / b.group_size;
+    a.slices = b.width / lsamd::kDnCols;
     a.slot_words = p.slot_words;
     a.units_cap = units_cap;
     a.slot_capacity = b.slot_capacity;
     p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
-    slices_ = b.width / tile;
-    dn_tile_ = tile;
+    slices_ = b.width / lsamd::kDnCols;
     max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused) - 1;
     p.needs_clear = false;
     p.last_seq = 0;

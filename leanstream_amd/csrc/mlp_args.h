@@ -42,7 +42,7 @@ constexpr long long kAccBias = 1ll << 39;
 constexpr unsigned long long kAccOne = 1ull << 52;
 constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
-constexpr uint32_t kMaxRowsPerThread = 4;  // down-projection rows per thread held in registers
+constexpr uint32_t kDnCols = 128;  // columns of one down-projection item (one scale block)
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
@@ -50,8 +50,8 @@ constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { r
 constexpr uint32_t kStampSlots = 32;
 enum StampPhase : uint32_t {
     kStampEntry = 0, kStampXLoaded = 1, kStampCoreDone = 2, kStampEpoch = 3, kStampQueueDone = 4,
-    kStampFirstData = 5,  // first gate/up batch or down tile computed
-    kStampDnComputed = 8,  // first round of a down worker computed
+    kStampFirstData = 5,   // first gate/up item computed (wave 0)
+    kStampDnComputed = 8,  // first down item computed (wave 0)
     kStampExit = 31,
 };
 
@@ -85,17 +85,15 @@ struct MlpArgs {
     uint32_t* executions;         // optional per-destination execution counters
     uint64_t* first_compute;      // optional per-destination start stamps (100 MHz clock)
     uint32_t* sync;               // base of the two ring slots
-    uint32_t* status;
-    uint32_t* done;               // host-coherent: the last workgroup of a launch stores seq             // host-coherent sticky status word
+    uint32_t* status;             // host-coherent sticky status word
+    uint32_t* done;               // host-coherent: the last workgroup of a launch stores seq
     uint32_t* claim_log;          // optional: per-claim (head | (len << 24)), in claim order
     uint32_t claim_log_cap;       // entries in claim_log
     uint64_t* stamps;             // optional: per-worker phase stamps [workers][kStampSlots] (100 MHz clock)
     // geometry / control
     uint32_t width;               // d
     uint32_t group_size;          // G
-    uint32_t slices;              // down-projection tiles per unit (d / dn_tile)
-    uint32_t dn_tile;             // columns per down-projection tile
-    uint64_t g_recip;             // ceil(2^32 / group_size): division by G as a multiply
+    uint32_t slices;              // down-projection items per unit (d / kDnCols)
     uint32_t slot_words;          // words per ring slot
     uint32_t units_cap;           // max units (core + queue) the ring slot covers
     uint32_t slot_capacity;       // rows in hbuf/partial

@@ -4,35 +4,36 @@
 //   w      = fp16( q * scale[c/128] ),  q = signed low-nibble-first INT4
 //   gate   = sum_c w_gate(c) x(c)   up = sum_c w_up(c) x(c)          (fp32)
 //   h      = fp16( fp16(silu(fp16(gate))) * fp16(up) )
-//   partial[dest][c] = sum_n h_n w_down(n, c)                         (fp32)
-//   y[c]   = fp16( sum over the U destination rows of partial[.][c] )
+//   y[c]   = fp16( sum over the U destination rows of sum_n h_n w_down(n, c) )  (fp32)
 //
-// Work decomposition (MI355X-specific): every descriptor ("unit", one group of G
-// neurons) is cut into S items. Item j computes gate/up for neurons
-// [j*G/S, (j+1)*G/S) and the down projection for columns [j*d/S, (j+1)*d/S).
-// The down half of an item needs h of all G neurons of its unit, so items of
-// one unit meet at a per-unit counter. Items are spread over a persistent grid
-// sized to the chip, so a 58-group layer occupies every CU.
+// Work decomposition (MI355X-specific). The units of a launch (descriptors, one group of
+// G neurons each) are cut into wave-sized items of about 4 KB of weights:
+//   - gate/up items: NPW neurons of one unit; one 64-lane wave computes their gate and
+//     up rows and publishes h;
+//   - down items: one 128-column tile (one scale block) of one unit over all G rows.
+// All gate/up items come first, then the down items (unit-major). Wave w of the
+// persistent grid takes items w, w + NW, w + 2 NW, ... and keeps the next item's loads in
+// flight while it computes the current one, so the whole chip walks through the layer in
+// one global order and HBM delivers it front to back. A down item needs the h of its
+// unit, produced by items about one round earlier, so it is normally ready by the time
+// the down weights arrive. Waves of a workgroup never wait for each other on this path;
+// a wave waits for h only after all of its own gate/up items.
 //
-// Exactness: dequantisation is exact. The nibble is biased (x ^ 8) and OR-ed into
-// an fp16 magic constant (0x6400 = 1024 for low nibbles, 0x5400 = 64 with a 4-bit
-// mantissa offset for high nibbles); subtracting 1032 / 72 yields q exactly, and a
-// packed fp16 multiply rounds q*scale once (round-to-nearest-even), which is the
-// reference's fp16_rn(float(q)*float(scale)). Products w*x are exact in fp32;
-// only the fp32 summation order differs from the reference.
+// Exactness: dequantisation is exact (dequant8); products w*x are exact in fp32; only the
+// fp32 summation order differs from the reference.
 //
-// Reduction: each unit's tile is added into int64 fixed-point column accumulators
-// (round(v * 2^24)); integer addition is associative, so y does not depend on the order
-// in which units finish -- the output is bit-identical across consumer modes,
-// publication orders and entry points. The U-th contributor of a column tile converts
-// it to fp32 / fp16 and clears it.
+// Reduction: a down item's 128 column sums are added into packed fixed-point column
+// accumulators (kAccOne in mlp_args.h). Integer addition is associative, so y does not
+// depend on the order in which items finish: the output is bit-identical across consumer
+// modes, publication orders and entry points. The U-th contribution of a column
+// converts it to fp32 / fp16.
 //
 // Cross-workgroup data (h, accumulators, counters) uses agent-scope relaxed atomics,
-// which compile to sc1 loads/stores that are coherent across the eight XCD L2s,
-// with an explicit vmcnt(0) wait before each signalling atomic. No acquire or
-// release fence is issued inside a spin loop (those expand to whole-L2
-// invalidate / write-back). Every wait is bounded by a wall-clock limit; on
-// expiry the status word records a timeout and every worker leaves.
+// which compile to sc1 loads/stores that are coherent across the eight XCD L2s. An h
+// word carries its launch tag in the same 64-bit word, so no fence orders it. No acquire
+// or release fence is issued inside a spin loop (those expand to whole-L2 invalidate /
+// write-back). Every wait is bounded by a wall-clock limit; on expiry the status word
+// records a timeout and every worker leaves.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "mlp_args.h"
@@ -45,12 +46,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
-constexpr int kMaxRows = kMaxRowsPerThread;   // down-projection rows per thread
-constexpr int kMaxDnTiles = 6;       // down-projection tiles prefetched per round by a down worker
-constexpr int kGuBuffers = 3;        // gate/up batches in flight per gate/up worker
-constexpr int kUnitChunk = 16;       // unit descriptors loaded per parallel descriptor fetch
-constexpr int kRedFloats = 4096;     // LDS scratch for the cross-thread column reduction (rpp * tile)
-constexpr int kTileScales = 256;     // LDS scale slots per down pair (G * scale blocks of the tile)
+constexpr int kWaves = kThreads / 64;
+constexpr int kDnRows = 64;          // rows of one down-item pass: 8 row groups x 8 rows
+constexpr int kDescItems = 12;       // item descriptors fetched per round trip (5 words each)
+static_assert(kDnCols == 128, "a down item is one scale block wide");
 
 // ---------------------------------------------------------------------------------
 // memory helpers
@@ -98,19 +97,30 @@ __device__ __forceinline__ uint32_t ld_stream4(const uint8_t* p) {
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ _Float16 half_bits(uint16_t v) { return __builtin_bit_cast(_Float16, v); }
 __device__ __forceinline__ float round_half(float v) { return (float)(_Float16)v; }
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// Lane 0's value for the whole wave (call with lane 0 active).
+__device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// One v_bitop3 per pair: magic(w, A, M) = A ? (w ^ M) : M bitwise (truth table 0x6A over
+// (w, A, M)). Inside the nibble mask A it flips each nibble's sign bit (two's complement
+// -> offset binary q + 8); outside it lays down the fp16 exponent of M. Low nibbles
+// become 1024 + (q + 8), high nibbles (mantissa bits 4-7 under exponent 64) 64 + (q + 8);
+// the bias subtraction is exact and the scale product is the one rounding.
+__device__ __forceinline__ uint32_t magic(uint32_t w, uint32_t mask, uint32_t m) {
+    return __builtin_amdgcn_bitop3_b32(w, mask, m, 0x6A);
+}
 
 // Exact dequantisation of eight signed nibbles (one 32-bit word) into four fp16
 // pairs: out[k] = (w(col k), w(col k+4)) when the word holds one row, or
 // (row a, row b) of one column when the halves of the word come from two rows.
 __device__ __forceinline__ void dequant8(uint32_t word, h2 s, h2 out[4]) {
-    const uint32_t m = word ^ 0x88888888u;      // two's complement -> offset binary
-    const uint32_t m8 = m >> 8;
+    const uint32_t w8 = word >> 8;
     const h2 lo_bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
     const h2 hi_bias = {(_Float16)-72.0f, (_Float16)-72.0f};
-    out[0] = (as_h2((m & 0x000F000Fu) | 0x64006400u) + lo_bias) * s;
-    out[1] = (as_h2((m & 0x00F000F0u) | 0x54005400u) + hi_bias) * s;
-    out[2] = (as_h2((m8 & 0x000F000Fu) | 0x64006400u) + lo_bias) * s;
-    out[3] = (as_h2((m8 & 0x00F000F0u) | 0x54005400u) + hi_bias) * s;
+    out[0] = (as_h2(magic(word, 0x000F000Fu, 0x64086408u)) + lo_bias) * s;
+    out[1] = (as_h2(magic(word, 0x00F000F0u, 0x54805480u)) + hi_bias) * s;
+    out[2] = (as_h2(magic(w8, 0x000F000Fu, 0x64086408u)) + lo_bias) * s;
+    out[3] = (as_h2(magic(w8, 0x00F000F0u, 0x54805480u)) + hi_bias) * s;
 }
 
 __device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
@@ -133,82 +143,121 @@ __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, u
     st_agent(slot + kSyncAbort, 1u);
 }
 
+// Lane 0 of the wave checks whether a wait must be abandoned (abort flag or spin limit
+// exceeded; the latter raises the timeout status). Wave-uniform result.
+__device__ __forceinline__ bool wave_should_stop(const MlpArgs& a, uint32_t* slot, const Waiter& wt) {
+    uint32_t st = 0;
+    if (lane_id() == 0) {
+        if (ld_agent(slot + kSyncAbort)) {
+            st = 1;
+        } else if (wt.expired()) {
+            raise_status(a, slot, kStatusTimeout);
+            st = 1;
+        }
+    }
+    return __builtin_amdgcn_readfirstlane(st) != 0;
+}
+
 // ---------------------------------------------------------------------------------
-// Geometry of the gate/up half of an item, specialised on width D and neurons per item NS.
+// Gate/up items. A width-D row of one projection is CPR 16-byte chunks; LPR lanes share a
+// row (CPL chunks each), so one wave covers NPW neurons: one item.
 // ---------------------------------------------------------------------------------
-template <int D, int NS>
+template <int D>
 struct GuGeom {
     static constexpr int CPR = D / 32;                 // 16-byte chunks per projection row
     static constexpr int LPR = CPR < 64 ? CPR : 64;    // lanes sharing one row
     static constexpr int CPL = CPR / LPR;              // chunks per lane per row
-    static constexpr int NPW = 64 / LPR;               // neurons per wave per pass
-    static constexpr int NPP = 4 * NPW;                // neurons per workgroup per pass
-    static constexpr int PASSES = (NS + NPP - 1) / NPP;
+    static constexpr int NPW = 64 / LPR;               // neurons per wave: one gate/up item
     static constexpr int BLOCKS = D / 128;             // scale blocks per row
     static_assert(D % 256 == 0 && CPR >= 8, "width must be a multiple of 256");
 };
 
-// x for this lane's chunks, rearranged into (k, k+4) pairs to match dequant8.
-template <int D, int NS>
+// x for this lane's chunks: loaded as raw words (load_x), then rearranged in place into
+// (k, k+4) fp16 pairs to match dequant8 (pair_x) when first needed, so that waiting for
+// x never holds up the issue of the weight loads.
+template <int D>
 struct XRegs {
-    h2 p[GuGeom<D, NS>::CPL][16];
+    uint32_t v[GuGeom<D>::CPL][16];
 };
 
-template <int D, int NS>
-__device__ __forceinline__ void load_x(const uint16_t* x, XRegs<D, NS>& xr) {
-    using Gm = GuGeom<D, NS>;
-    const int lane = threadIdx.x & 63;
-    const int r = lane % Gm::LPR;
+template <int D>
+__device__ __forceinline__ void load_x(const uint16_t* x, XRegs<D>& xr) {
+    using Gm = GuGeom<D>;
+    const int r = lane_id() % Gm::LPR;
 #pragma unroll
     for (int k = 0; k < Gm::CPL; ++k) {
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(x + 32 * (r + Gm::LPR * k));
+        const u32x4* src = reinterpret_cast<const u32x4*>(x + 32 * (r + Gm::LPR * k));
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            // halves 8g..8g+7 live in words 4g..4g+3 as (0,1)(2,3)(4,5)(6,7)
-            const uint32_t w0 = src[4 * g + 0], w1 = src[4 * g + 1], w2 = src[4 * g + 2], w3 = src[4 * g + 3];
-            xr.p[k][4 * g + 0] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x05040100u));  // (x0, x4)
-            xr.p[k][4 * g + 1] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x07060302u));  // (x1, x5)
-            xr.p[k][4 * g + 2] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x05040100u));  // (x2, x6)
-            xr.p[k][4 * g + 3] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x07060302u));  // (x3, x7)
+            const u32x4 w = src[g];
+            xr.v[k][4 * g + 0] = w.x;
+            xr.v[k][4 * g + 1] = w.y;
+            xr.v[k][4 * g + 2] = w.z;
+            xr.v[k][4 * g + 3] = w.w;
         }
     }
 }
 
-template <int D, int NS>
-struct GuLoads {
-    u32x4 w[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];
-    uint32_t s[GuGeom<D, NS>::PASSES][2][GuGeom<D, NS>::CPL];   // fp16 bits (32-bit registers)
+template <int D>
+__device__ __forceinline__ void pair_x(XRegs<D>& xr) {
+#pragma unroll
+    for (int k = 0; k < GuGeom<D>::CPL; ++k) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            // halves 8g..8g+7 live in words 4g..4g+3 as (0,1)(2,3)(4,5)(6,7)
+            const uint32_t w0 = xr.v[k][4 * g + 0], w1 = xr.v[k][4 * g + 1];
+            const uint32_t w2 = xr.v[k][4 * g + 2], w3 = xr.v[k][4 * g + 3];
+            xr.v[k][4 * g + 0] = __builtin_amdgcn_perm(w2, w0, 0x05040100u);  // (x0, x4)
+            xr.v[k][4 * g + 1] = __builtin_amdgcn_perm(w2, w0, 0x07060302u);  // (x1, x5)
+            xr.v[k][4 * g + 2] = __builtin_amdgcn_perm(w3, w1, 0x05040100u);  // (x2, x6)
+            xr.v[k][4 * g + 3] = __builtin_amdgcn_perm(w3, w1, 0x07060302u);  // (x3, x7)
+        }
+    }
+}
+
+// x state of a wave: 0 not loaded, 1 loaded (raw), 2 paired.
+template <int D>
+__device__ __forceinline__ void need_x(const uint16_t* x, XRegs<D>& xr, int& state, int want) {
+    if (state == 0 && want >= 1) {
+        load_x<D>(x, xr);
+        state = 1;
+    }
+    if (state == 1 && want == 2) {
+        pair_x<D>(xr);
+        state = 2;
+    }
+}
+
+template <int D>
+struct GuItem {
+    u32x4 w[2][GuGeom<D>::CPL];
+    uint32_t s[2][GuGeom<D>::CPL];   // fp16 bits (32-bit registers)
 };
 
-// Issue every gate/up load of one item. grp points at the unit's packed bytes,
-// sc at the unit's scale rows, n0 is the first neuron of the item.
-template <int D, int NS>
-__device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, int nvalid,
-                                         GuLoads<D, NS>& L) {
-    using Gm = GuGeom<D, NS>;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// Issue every load of a gate/up item: neurons n0 .. n0 + nvalid - 1 of the unit whose
+// packed bytes start at grp and scale rows at sc.
+template <int D>
+__device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, int nvalid, GuItem<D>& L) {
+    using Gm = GuGeom<D>;
+    const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+    const bool ok = sub < nvalid;
+    const int n = n0 + (ok ? sub : 0);
+    const uint8_t* row = grp + (size_t)n * (3 * D / 2);
+    const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
 #pragma unroll
-    for (int p = 0; p < Gm::PASSES; ++p) {
-        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;   // neuron within the batch
-        const bool ok = nu < nvalid;
-        const int n = n0 + (ok ? nu : 0);
-        const uint8_t* row = grp + (size_t)n * (3 * D / 2);
-        const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
-#pragma unroll
-        for (int k = 0; k < Gm::CPL; ++k) {
-            const int chunk = r + Gm::LPR * k;
-            if (ok) {
-                L.w[p][0][k] = ld_stream16(row + 16 * chunk);
-                L.w[p][1][k] = ld_stream16(row + D / 2 + 16 * chunk);
-                L.s[p][0][k] = srow[chunk >> 2];
-                L.s[p][1][k] = srow[Gm::BLOCKS + (chunk >> 2)];
-            } else {
-                L.w[p][0][k] = u32x4{0, 0, 0, 0};
-                L.w[p][1][k] = u32x4{0, 0, 0, 0};
-                L.s[p][0][k] = 0;
-                L.s[p][1][k] = 0;
-            }
+    for (int k = 0; k < Gm::CPL; ++k) {
+        const int chunk = r + Gm::LPR * k;
+        if (ok) {
+            L.w[0][k] = ld_stream16(row + 16 * chunk);
+            L.w[1][k] = ld_stream16(row + D / 2 + 16 * chunk);
+            L.s[0][k] = srow[chunk >> 2];
+            L.s[1][k] = srow[Gm::BLOCKS + (chunk >> 2)];
+        } else {
+            L.w[0][k] = u32x4{0, 0, 0, 0};
+            L.w[1][k] = u32x4{0, 0, 0, 0};
+            L.s[0][k] = 0;
+            L.s[1][k] = 0;
         }
     }
 }
@@ -235,173 +284,153 @@ __device__ __forceinline__ float group_sum(float x) {
     return x;
 }
 
-// Finish gate/up for the item: dot products, row reductions, activation.
-// Writes h (fp32, fp16-exact) for neurons n0..n0+NS-1 of unit row `hrow`.
-template <int D, int NS>
-__device__ __forceinline__ void gu_compute(const GuLoads<D, NS>& L, const XRegs<D, NS>& xr, uint64_t* hrow, int n0,
-                                           int nvalid, uint32_t seq) {
-    using Gm = GuGeom<D, NS>;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+// Finish a gate/up item: dot products, row reductions, activation. Publishes h of
+// neurons n0 .. n0 + nvalid - 1 into hrow, each word tagged with the launch sequence
+// (the word is its own ready flag).
+template <int D>
+__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const XRegs<D>& xr, uint64_t* hrow, int n0, int nvalid,
+                                           uint32_t seq) {
+    using Gm = GuGeom<D>;
+    const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+    float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int p = 0; p < Gm::PASSES; ++p) {
-        float acc[2] = {0.f, 0.f};
+    for (int proj = 0; proj < 2; ++proj) {
 #pragma unroll
-        for (int proj = 0; proj < 2; ++proj) {
+        for (int k = 0; k < Gm::CPL; ++k) {
+            const _Float16 sv = half_bits((uint16_t)L.s[proj][k]);
+            const h2 s2 = {sv, sv};
+            const u32x4 v = L.w[proj][k];
+            const uint32_t words[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-            for (int k = 0; k < Gm::CPL; ++k) {
-                const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
-                const h2 s2 = {sv, sv};
-                const u32x4 v = L.w[p][proj][k];
-                const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+            for (int g = 0; g < 4; ++g) {
+                h2 w[4];
+                dequant8(words[g], s2, w);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    h2 w[4];
-                    dequant8(words[g], s2, w);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], xr.p[k][4 * g + q], acc[proj]);
-                }
+                for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], as_h2(xr.v[k][4 * g + q]), acc[proj]);
             }
         }
-        acc[0] = group_sum<Gm::LPR>(acc[0]);
-        acc[1] = group_sum<Gm::LPR>(acc[1]);
-        const int nu = p * Gm::NPP + wave * Gm::NPW + sub;
-        if (r == Gm::LPR - 1 && nu < nvalid) {
-            const float g = round_half(acc[0]);
-            const float u = round_half(acc[1]);
-            const float s = round_half(g / (1.0f + __expf(-g)));
-            const float h = round_half(s * u);
-            // h tagged with the launch sequence: the word is its own ready flag.
-            __hip_atomic_store(hrow + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
+    }
+    acc[0] = group_sum<Gm::LPR>(acc[0]);
+    acc[1] = group_sum<Gm::LPR>(acc[1]);
+    if (r == Gm::LPR - 1 && sub < nvalid) {
+        const float g = round_half(acc[0]);
+        const float u = round_half(acc[1]);
+        const float s = round_half(g / (1.0f + __expf(-g)));
+        const float h = round_half(s * u);
+        __hip_atomic_store(hrow + n0 + sub, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 // ---------------------------------------------------------------------------------
-// Down projection of one column tile (tc columns) of one unit, all G neurons.
-// Thread t covers 16 columns -- one 8-byte load of 16 nibbles per row -- of rows
-// r0, r0 + rpp, ...: lanes = tc / 16 threads share a row, rpp = 256 / lanes rows per
-// pass, at most kMaxRows rows per thread (G * tc <= 16384).
+// Down items: one 128-column tile of one unit. A pass covers 64 rows: lane 8 g + dc
+// holds columns 16 dc .. 16 dc + 15 (one 8-byte load per row) of rows 8 g .. 8 g + 7,
+// plus the h and the down scale of row `lane` (for the LDS exchange).
 // ---------------------------------------------------------------------------------
-struct DnLoads {
-    u32x2 w[kMaxRows];
+struct DnItem {
+    u32x2 w[8];
+    uint64_t h;     // tagged h of row r0 + lane (tag == seq and value 0 beyond G)
+    uint32_t s;     // down scale of row r0 + lane for the tile's block (0 beyond G)
 };
-
-struct DnGeom {
-    int lanes, rpp, rpp_shift, dc, r0, nrows, nbk, nbk_shift;
-    __device__ DnGeom(int G, int tc) {
-        const int lanes_shift = __builtin_ctz((unsigned)tc) - 4;
-        lanes = 1 << lanes_shift;      // threads per row of the tile (tc is a power of two)
-        rpp_shift = 8 - lanes_shift;
-        rpp = 1 << rpp_shift;          // rows covered per pass of the workgroup
-        dc = threadIdx.x & (lanes - 1);
-        r0 = threadIdx.x >> lanes_shift;
-        nrows = r0 < G ? (G - r0 + rpp - 1) >> rpp_shift : 0;
-        nbk_shift = tc > 128 ? 1 : 0;
-        nbk = 1 << nbk_shift;          // 128-column scale blocks the tile spans
-    }
-};
-
-template <int D>
-__device__ __forceinline__ void dn_issue(const uint8_t* grp, const DnGeom& gm, int c0, DnLoads& L) {
-    const int col = c0 + 16 * gm.dc;
-#pragma unroll
-    for (int i = 0; i < kMaxRows; ++i) {
-        if (i < gm.nrows) {
-            const int n = gm.r0 + gm.rpp * i;
-            L.w[i] = ld_stream8(grp + (size_t)n * (3 * D / 2) + D + (col >> 1));
-        } else {
-            L.w[i] = u32x2{0, 0};
-        }
-    }
-}
-
-// This thread's share of the tile's down scales, staged in LDS by stage_round:
-// slot t < G * nbk holds row t / nbk, block t % nbk of the tile.
-template <int D>
-__device__ __forceinline__ uint32_t dn_scale_issue(const uint16_t* sc, const DnGeom& gm, int G, int c0) {
-    constexpr int BLOCKS = D / 128;
-    const int t = threadIdx.x;
-    if (t >= G * gm.nbk) return 0;
-    return sc[(size_t)(t >> gm.nbk_shift) * 3 * BLOCKS + 2 * BLOCKS + (c0 >> 7) + (t & (gm.nbk - 1))];
-}
 
 __device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __shfl(v, 0, 64); }
 
-// Float offset of the 4-column chunk q of column group dc in a row of the reduction
-// scratch (see dn_compute).
-__device__ __forceinline__ int red_swizzle(int dc, int q) { return 16 * dc + 4 * ((q + (dc >> 1)) & 3); }
-
-// Down projection of the tile with the pair's h (hs) and scales (ss) staged in LDS.
-// Each thread sums its rows in increasing order, two rows per dot2 (v_perm pairs the
-// nibbles of rows (j, j+1) column by column), into 16 column partials; the partials
-// of the rpp row groups are then summed in LDS in row-group order into
-// red[kRedFloats + t], tile column t.
-__device__ __forceinline__ void dn_compute(const DnLoads& L, const DnGeom& gm, const uint16_t* hs, const uint16_t* ss,
-                                           float* red, int tc) {
-    static_assert(kMaxRows == 4, "two row pairs per thread");
-    const u32x2 hp = *reinterpret_cast<const u32x2*>(hs + gm.r0 * kMaxRows);  // h of rows (0,1) (2,3)
-    const uint32_t hw[2] = {hp.x, hp.y};
-    const int blk = gm.dc >> 3;   // 16 dc / 128: scale block within the tile
-    float acc[16];
+template <int D>
+__device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc, const uint64_t* hrow, int G, int tile,
+                                         int r0, uint32_t seq, DnItem& it) {
+    constexpr int BLOCKS = D / 128;
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const uint8_t* base = grp + D + tile * (kDnCols / 2) + dc * 8;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) acc[c] = 0.f;
-#pragma unroll
-    for (int i = 0; i < kMaxRows; i += 2) {
-        if (i < gm.nrows) {
-            const bool pair = i + 1 < gm.nrows;
-            const u32x2 wa = L.w[i], wb = pair ? L.w[i + 1] : L.w[i];
-            const h2 hab = as_h2(hw[i / 2]);   // second half is zero when !pair
-            const int na = gm.r0 + gm.rpp * i, nb = pair ? na + gm.rpp : na;
-            const h2 sab = {half_bits(ss[na * gm.nbk + blk]), half_bits(ss[nb * gm.nbk + blk])};
-            const uint32_t xa[2] = {wa.x, wa.y}, xb[2] = {wb.x, wb.y};
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                h2 w[4];
-                dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
-#pragma unroll
-                for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
-                dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);   // columns 8q + 4..7
-#pragma unroll
-                for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
-            }
-        }
+    for (int j = 0; j < 8; ++j) {
+        const int n = r0 + 8 * g + j;
+        it.w[j] = n < G ? ld_stream8(base + (size_t)n * (3 * D / 2)) : u32x2{0, 0};
     }
-    // red's first half is free: the previous tile's column sums were read before the
-    // barrier that ended it. Row group r0's partial of tile column 16 dc + 4 q + e sits
-    // at r0 * tc + swz(dc, q) + e: each thread stores 4 x 16 bytes, and within any 8
-    // consecutive lanes the 16-byte chunks fall on distinct banks.
-    float* mine = red + gm.r0 * tc;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const float4 v = gm.nrows > 0 ? float4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]}
-                                      : float4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<float4*>(mine + red_swizzle(gm.dc, q)) = v;
-    }
-    __syncthreads();  // also: every thread is done with the previous tile's second half
-    for (int t = threadIdx.x; t < tc; t += kThreads) {
-        const int at = red_swizzle(t >> 4, (t >> 2) & 3) + (t & 3);
-        float v = 0.f;
-        for (int r0 = 0; r0 < gm.rpp; r0 += 16) {   // rpp is 16, 32 or 64
-            float p[16];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = red[(r0 + r) * tc + at];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) v += p[r];
-        }
-        red[kRedFloats + t] = v;   // reduced tile, natural column order
-    }
-    __syncthreads();
+    const int n = r0 + lane;
+    it.s = n < G ? sc[(size_t)n * 3 * BLOCKS + 2 * BLOCKS + tile] : 0u;
+    it.h = n < G ? ld_agent_u64(hrow + n) : (uint64_t)seq << 32;
 }
 
-// x / G for x < 2^16 (G <= 256) via the launch's reciprocal ceil(2^32 / G): exact, as
-// x * (ceil(2^32 / G) - 2^32 / G) < 2^32 / G.
-__device__ __forceinline__ uint32_t div_group(const MlpArgs& a, uint32_t x) {
-    return (uint32_t)(((uint64_t)x * a.g_recip) >> 32);
+// Waits until the h of every row of the pass carries the launch sequence. False when
+// the wait was abandoned (abort or timeout).
+__device__ __forceinline__ bool dn_wait_h(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int G, int r0,
+                                          DnItem& it) {
+    const uint64_t want = a.seq;
+    if (__all((it.h >> 32) == want)) return true;
+    const int n = r0 + lane_id();
+    Waiter wt(a.spin_limit);
+    for (;;) {
+        if (wave_should_stop(a, slot, wt)) return false;
+        __builtin_amdgcn_s_sleep(1);
+        if ((it.h >> 32) != want) it.h = ld_agent_u64(hrow + n);   // only rows < G can be stale
+        if (__all((it.h >> 32) == want)) return true;
+    }
+}
+
+// Adds one pass into the lane's 16 column partials. The pass's h and scales go through
+// this wave's LDS rows (hs, ss: 64 halves each) so that a lane reads its 8 rows as one
+// 16-byte vector each. Rows (8g + 2p, 8g + 2p + 1) share a dot2: v_perm pairs their
+// nibbles column by column. Rows beyond G have zero weights, h and scales.
+__device__ __forceinline__ void dn_accumulate(const DnItem& it, uint16_t* hs, uint16_t* ss, float acc[16]) {
+    const int lane = lane_id(), g = lane >> 3;
+    hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
+    ss[lane] = (uint16_t)it.s;
+    // The wave's LDS operations execute in order: the stores above land before the
+    // loads below. The fence only keeps the compiler from reordering them.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + 8 * g);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const u32x2 wa = it.w[2 * p], wb = it.w[2 * p + 1];
+        const h2 hab = as_h2(hw[p]), sab = as_h2(sw[p]);
+        const uint32_t xa[2] = {wa.x, wa.y}, xb[2] = {wb.x, wb.y};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            h2 w[4];
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);   // columns 8q + 4..7
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
+        }
+    }
+}
+
+__device__ __forceinline__ float swap_sum32(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float swap_sum16(float x, float y) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum over the 8 row groups (lanes 8 g + dc, same dc) in a fixed tree, without LDS.
+// v_permlane32_swap exchanges the upper half of one register with the lower half of
+// another, so (acc[c], acc[c+8]) summed after a swap leave column c (groups g, g + 4) in
+// lanes < 32 and column c + 8 in lanes >= 32; v_permlane16_swap does the same across
+// odd / even 16-lane rows; a row_ror:8 DPP add joins the two group parities. Returns
+// this lane's columns 16 dc + 2 g and 16 dc + 2 g + 1 of the tile.
+__device__ __forceinline__ void dn_reduce(const float acc[16], float& c0, float& c1) {
+    float s1[8], s2[4];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) s1[c] = swap_sum32(acc[c], acc[c + 8]);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s2[c] = swap_sum16(s1[c], s1[c + 4]);
+    // lane (g, dc) now holds columns 4 (g >> 1) + c of the 16 at dc, over the groups
+    // of g's parity; lane ^ 8 holds the same columns over the other parity.
+    const bool odd = (lane_id() >> 3) & 1;
+    const float x0 = odd ? s2[2] : s2[0], x1 = odd ? s2[3] : s2[1];
+    const float y0 = odd ? s2[0] : s2[2], y1 = odd ? s2[1] : s2[3];
+    c0 = x0 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y0), 0x128, 0xF, 0xF, false));
+    c1 = x1 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y1), 0x128, 0xF, 0xF, false));
 }
 
 // ---------------------------------------------------------------------------------
@@ -427,45 +456,30 @@ __device__ __forceinline__ Unit resolve(const MlpArgs& a, const Bounds& b, ExecD
     return u;
 }
 
-__device__ __forceinline__ ExecDesc load_core(const MlpArgs& a, uint32_t i) { return a.core[i]; }
-
 // ---------------------------------------------------------------------------------
-// Shared workgroup state
+// Shared workgroup state: per-wave LDS rows for the down items' h / scale exchange, and
+// the words the claim path and the path decision share.
 // ---------------------------------------------------------------------------------
 struct Shared {
-    alignas(16) float red[kRedFloats + 256];
-    alignas(16) uint16_t hs[kMaxDnTiles * 64 * kMaxRows];   // staged h of a round (stage_round layout)
-    uint16_t ss[kMaxDnTiles * kTileScales];                  // staged down scales of a round
-    uint32_t pdest[kMaxDnTiles];                             // dest rows of the round's pairs
-    uint32_t ulist[kUnitChunk];                              // units of a descriptor fetch
-    uint32_t udesc[kUnitChunk][5];                           // their descriptor words
+    alignas(16) uint16_t hs[kWaves][kDnRows];
+    alignas(16) uint16_t ss[kWaves][kDnRows];
     uint32_t word[8];
-    uint32_t desc[5];
-    // queue state learnt once per launch: known, ok, total, path
-    uint32_t ep_known, ep_ok, ep_total, ep_path;
+    uint32_t wpath[kWaves];
+    uint32_t wfail[kWaves];
 };
 
-__device__ __forceinline__ void init_shared(Shared& sh) {
-    if (threadIdx.x == 0) { sh.ep_known = 0; sh.ep_ok = 0; sh.ep_total = 0; sh.ep_path = 0; }
-    for (int i = threadIdx.x; i < kMaxDnTiles * 64 * kMaxRows; i += kThreads) sh.hs[i] = 0;
-    __syncthreads();
-}
+// The queue state of a launch as one wave learnt it (wave-uniform).
+struct Epoch {
+    uint32_t known, ok, total, path;
+};
 
-// Thread 0's early, non-blocking look at the mirrored epoch word (0 = not yet known).
-__device__ __forceinline__ uint32_t epoch_peek(const Shared& sh, const uint32_t* slot) {
-    return threadIdx.x == 0 && !sh.ep_known ? ld_agent(slot + kSyncEpoch) : 0u;
-}
-
-// (ok, total, path) of the queue, learnt once per workgroup from the word the mirror
-// workgroup publishes. `early` is thread 0's epoch_peek taken before the item's loads.
-__device__ __forceinline__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t early) {
-    // Every thread reads the flag before thread 0 may write it (barrier in between),
-    // so the whole workgroup takes the same branch.
-    const uint32_t known = sh.ep_known;
-    __syncthreads();
-    if (known) return sh.ep_ok != 0;
-    if (threadIdx.x == 0) {
-        uint32_t word = early;
+// (ok, total, path) of the queue from the word the mirror workgroup publishes. `early`
+// is lane 0's look at the word taken at the start of the launch.
+__device__ __forceinline__ bool await_epoch(const MlpArgs& a, uint32_t* slot, Epoch& ep, uint32_t early) {
+    if (ep.known) return ep.ok != 0;
+    uint32_t word = 0;
+    if (lane_id() == 0) {
+        word = early;
         Waiter wt(a.spin_limit);
         while (!(word & 3u)) {
             if (ld_agent(slot + kSyncAbort)) { word = 2; break; }
@@ -473,14 +487,13 @@ __device__ __forceinline__ bool await_epoch(const MlpArgs& a, Shared& sh, uint32
             __builtin_amdgcn_s_sleep(2);
             word = ld_agent(slot + kSyncEpoch);
         }
-        const bool ok = (word & 3u) == 1u;
-        sh.ep_ok = ok;
-        sh.ep_path = ok ? (word >> 2) & 3u : 0u;
-        sh.ep_total = ok ? word >> 4 : 0u;
-        sh.ep_known = 1;
     }
-    __syncthreads();
-    return sh.ep_ok != 0;
+    word = __builtin_amdgcn_readfirstlane(word);
+    ep.known = 1;
+    ep.ok = (word & 3u) == 1u;
+    ep.path = ep.ok ? (word >> 2) & 3u : 0u;
+    ep.total = ep.ok ? word >> 4 : 0u;
+    return ep.ok != 0;
 }
 
 // ---------------------------------------------------------------------------------
@@ -497,114 +510,71 @@ __device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned
     a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-
-__device__ __forceinline__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out);
-
-// h and down scales of a round's pairs staged in LDS. h as the fp16 values each
-// down-projection thread multiplies: hs[i * stride + r0 * kMaxRows + j] = h_i[r0 + rpp * j]
-// for pair i (stride = rpp * kMaxRows; zero for rows >= G, written once at start).
-// Every thread polls its share of the tagged words (dest rows in sh.pdest) until each
-// tag carries the launch sequence, then converts (exactly: h is fp16-representable).
-// Scales: ss[i * kTileScales + t] = sv[i] (dn_scale_issue). Returns false for the whole
-// workgroup when the wait was abandoned.
-constexpr int kStageWords = 8;   // h words per thread per staging pass
-__device__ __forceinline__ bool stage_round(const MlpArgs& a, uint32_t* slot, Shared& sh, uint32_t npairs,
-                                            const DnGeom& gm, int G, const uint32_t (&sv)[kMaxDnTiles]) {
-    const uint32_t total = npairs * (uint32_t)G;
-    const uint32_t stride = (uint32_t)gm.rpp * kMaxRows;
-    const uint64_t want = (uint64_t)a.seq;
-    uint32_t* stop_flag = &sh.word[3];
-    if (threadIdx.x == 0) *stop_flag = 0;
-    __syncthreads();  // pdest written; earlier readers of hs / ss and the flag are done
-#pragma unroll
-    for (int i = 0; i < kMaxDnTiles; ++i)
-        if ((uint32_t)i < npairs && (int)threadIdx.x < G * gm.nbk) sh.ss[i * kTileScales + threadIdx.x] = (uint16_t)sv[i];
-    for (uint32_t f0 = 0; f0 < total; f0 += kStageWords * kThreads) {
-        uint64_t v[kStageWords];
-        const uint64_t* src[kStageWords];
-#pragma unroll
-        for (int q = 0; q < kStageWords; ++q) {
-            const uint32_t f = f0 + threadIdx.x + q * kThreads;
-            const uint32_t i = div_group(a, f), n = f - i * G;
-            src[q] = f < total ? a.hbuf + (size_t)sh.pdest[i] * G + n : nullptr;
-            v[q] = src[q] ? ld_agent_u64(src[q]) : (want << 32);
-        }
-        uint32_t stop = 0;
-        Waiter wt(a.spin_limit);
-        for (;;) {
-            bool ok = true;
-#pragma unroll
-            for (int q = 0; q < kStageWords; ++q) ok = ok && (v[q] >> 32) == want;
-            if (__all(ok)) break;
-            uint32_t st = 0;
-            if ((threadIdx.x & 63) == 0) {
-                if (ld_agent(slot + kSyncAbort)) {
-                    st = 1;
-                } else if (wt.expired()) {
-                    raise_status(a, slot, kStatusTimeout);
-                    st = 1;
-                }
-            }
-            stop = wave_bcast(st);
-            if (stop) break;
-            __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-            for (int q = 0; q < kStageWords; ++q)
-                if ((v[q] >> 32) != want) v[q] = ld_agent_u64(src[q]);
-        }
-        if (stop) {
-            if ((threadIdx.x & 63) == 0) *stop_flag = 1;
-            break;
-        }
-#pragma unroll
-        for (int q = 0; q < kStageWords; ++q) {
-            const uint32_t f = f0 + threadIdx.x + q * kThreads;
-            if (f < total) {
-                const uint32_t i = div_group(a, f), n = f - i * G;
-                sh.hs[i * stride + (n & (gm.rpp - 1)) * kMaxRows + (n >> gm.rpp_shift)] =
-                    __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)v[q]));
-            }
-        }
+// One contribution of a column value: round(v * 2^20) biased by 2^39, count 1 in the
+// top field. Out-of-range values are clipped and reported.
+__device__ __forceinline__ unsigned long long acc_term(const MlpArgs& a, uint32_t* slot, float value) {
+    float v = value * kAccScale;
+    if (!(fabsf(v) < (float)(kAccBias - 1))) {  // out of range or NaN: clip and report
+        v = v > 0.f ? (float)(kAccBias - 1) : -(float)(kAccBias - 1);
+        raise_status(a, slot, kStatusRange);
     }
-    __syncthreads();
-    return *stop_flag == 0;
+    return (unsigned long long)(__float2ll_rn(v) + kAccBias) + kAccOne;
 }
 
-// Gate/up batch size of the width-D variant: one pass of the workgroup (4 waves).
-template <int D>
-struct Batch {
-    static constexpr int N = GuGeom<D, 1>::NPP;
+// The accumulator words returned by a wave's last column additions, checked once the
+// next additions are issued (or at the end), so the wave does not wait for the atomics'
+// round trip: the contribution that completes a column (count U) writes the output.
+struct Pending {
+    unsigned long long v0, v1;
+    int col;   // first of the two columns; < 0: nothing pending
 };
 
-// Descriptor of global unit `gu` (core units first, then queue positions), validated.
-__device__ __forceinline__ bool fetch_unit(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, uint32_t gu, int D,
-                           Unit* out) {
-    ExecDesc d;
-    if (gu < a.core_count) {
-        d = load_core(a, gu);
-    } else if (!load_queue_wg(a, sh, slot, gu - a.core_count, &d)) {
-        return false;
+__device__ __forceinline__ void check_pending(const MlpArgs& a, Pending& pd, uint32_t U) {
+    if (pd.col >= 0 && U) {
+        if ((uint32_t)(pd.v0 >> 52) == U) write_output(a, pd.col, pd.v0, U);
+        if ((uint32_t)(pd.v1 >> 52) == U) write_output(a, pd.col + 1, pd.v1, U);
     }
-    *out = resolve(a, b, d, D);
-    if (!out->ok) {
-        if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
-        return false;
-    }
-    return true;
+    pd.col = -1;
 }
 
-// Loads the descriptors of units sh.ulist[0..n) (n <= kUnitChunk, written by thread 0)
-// in parallel, one word per thread, into sh.udesc: core units from the core array,
-// queue positions from the device-side mirror once the mirror has copied them.
-// One memory round trip (two when queue positions must first be waited for).
-__device__ __forceinline__ bool load_units(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t n) {
-    __syncthreads();  // ulist written; earlier readers of udesc are done
-    if (threadIdx.x == 0) {
-        uint32_t need = 0;  // queue positions that must be mirrored
-        for (uint32_t i = 0; i < n; ++i)
-            if (sh.ulist[i] >= a.core_count) need = max(need, sh.ulist[i] - a.core_count + 1);
+__device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, int col,
+                                            float c0, float c1, uint32_t U, Pending& pd) {
+    const unsigned long long t0 = acc_term(a, slot, c0), t1 = acc_term(a, slot, c1);
+    const unsigned long long n0 = __hip_atomic_fetch_add(yacc + col, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t0;
+    const unsigned long long n1 =
+        __hip_atomic_fetch_add(yacc + col + 1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t1;
+    check_pending(a, pd, U);
+    pd.v0 = n0;
+    pd.v1 = n1;
+    pd.col = col;
+}
+
+// Execution counters (diagnostics): a unit counts once all of its down items are done.
+__device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot, uint32_t unit, uint32_t dest,
+                                                uint32_t items) {
+    if (lane_id() == 0 && add_agent(slot + kSyncUnits + unit * kLine, 1u) == items - 1)
+        __hip_atomic_fetch_add(a.executions + dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// ---------------------------------------------------------------------------------
+// Item walk of one wave over units [u0, u1).
+// ---------------------------------------------------------------------------------
+
+// Unit (relative to u0) of item i: gate/up items [0, NG), ipu per unit; then down items,
+// T per unit, unit-major.
+__device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T) {
+    return i < NG ? i / ipu : (i - NG) / T;
+}
+
+// Descriptor words of items k0 .. k0 + count - 1 of this wave (item i = wv + k NW) in
+// one round trip: lane 5 j + w holds word w of item k0 + j's unit. Queue positions are
+// read from the mirror once it has copied the first `need` of them.
+__device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t need, uint32_t wv,
+                                            uint32_t NW, uint32_t k0, uint32_t count, uint32_t NG, uint32_t ipu,
+                                            uint32_t T, uint32_t& word) {
+    if (need) {
         uint32_t ok = 1;
-        if (need) {
+        if (lane_id() == 0) {
             Waiter wt(a.spin_limit);
             while (ld_agent(slot + kSyncReady) < need) {
                 if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
@@ -612,352 +582,167 @@ __device__ __forceinline__ bool load_units(const MlpArgs& a, Shared& sh, uint32_
                 __builtin_amdgcn_s_sleep(1);
             }
         }
-        sh.word[2] = ok;
+        if (!__builtin_amdgcn_readfirstlane(ok)) return false;
     }
-    __syncthreads();
-    if (!__builtin_amdgcn_readfirstlane(sh.word[2])) return false;
-    if (threadIdx.x < 5 * n) {
-        const uint32_t i = threadIdx.x / 5, w = threadIdx.x % 5, g = sh.ulist[i];
-        sh.udesc[i][w] = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
-                                          : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
+    const uint32_t lane = lane_id();
+    word = 0;
+    if (lane < 5 * count) {
+        const uint32_t j = lane / 5, w = lane - 5 * j;
+        const uint32_t g = u0 + item_unit(wv + (k0 + j) * NW, NG, ipu, T);
+        word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
+                                : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
-    __syncthreads();
     return true;
 }
 
-// Unit i of the last load_units, validated (wave-uniform values).
-__device__ __forceinline__ bool unit_from(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, uint32_t i,
-                                          int D, Unit* out) {
+__device__ __forceinline__ bool unit_of(const MlpArgs& a, uint32_t* slot, const Bounds& b, uint32_t word, uint32_t j,
+                                        int D, Unit& u) {
     ExecDesc d;
-    d.logical_group = __builtin_amdgcn_readfirstlane(sh.udesc[i][0]);
-    d.physical_group = __builtin_amdgcn_readfirstlane(sh.udesc[i][1]);
-    d.source_slot = __builtin_amdgcn_readfirstlane(sh.udesc[i][2]);
-    d.dest_slot = __builtin_amdgcn_readfirstlane(sh.udesc[i][3]);
-    d.source_kind = (leanstream::runtime::SourceKind)__builtin_amdgcn_readfirstlane(sh.udesc[i][4]);
-    *out = resolve(a, b, d, D);
-    if (!out->ok) {
-        if (threadIdx.x == 0) raise_status(a, slot, kStatusBadDescriptor);
+    d.logical_group = __builtin_amdgcn_readlane(word, 5 * j + 0);
+    d.physical_group = __builtin_amdgcn_readlane(word, 5 * j + 1);
+    d.source_slot = __builtin_amdgcn_readlane(word, 5 * j + 2);
+    d.dest_slot = __builtin_amdgcn_readlane(word, 5 * j + 3);
+    d.source_kind = (leanstream::runtime::SourceKind)__builtin_amdgcn_readlane(word, 5 * j + 4);
+    u = resolve(a, b, d, D);
+    if (!u.ok) {
+        if (lane_id() == 0) raise_status(a, slot, kStatusBadDescriptor);
         return false;
     }
     return true;
 }
 
-// ---------------------------------------------------------------------------------
-// Gate/up share: batches [g0, g1) of Batch<D>::N neurons (never straddling a unit; unit
-// u0 + bi / bpu holds batch bi), kGuBuffers batches in flight, h stored tagged with the
-// launch sequence. after_first() runs right after the first batch's loads are issued
-// (the caller's own loads go there). Descriptors of units [chunk0, chunk0 + chunk_n) are
-// already in sh.udesc from slot chunk_off on; later units are fetched kUnitChunk at a time.
-// Never waits for another workgroup's h, so every worker finishes its share.
-// ---------------------------------------------------------------------------------
-template <int D, class AfterFirst>
-__device__ __forceinline__ bool gate_up_share(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
-                                              XRegs<D, Batch<D>::N>& xr, bool& have_x, uint32_t u0, uint32_t g0,
-                                              uint32_t g1, uint32_t bpu, uint32_t chunk0, uint32_t chunk_n,
-                                              uint32_t chunk_off, AfterFirst after_first) {
-    constexpr int NB = Batch<D>::N;
+// Wave-uniform bookkeeping of an item in flight.
+struct ItemMeta {
+    const uint8_t* grp;
+    const uint16_t* sc;
+    uint64_t* hrow;
+    uint32_t unit, dest, tile;
+    int n0, nvalid;
+};
+
+// This wave's items of units [u0, u1): wave wv of NW takes items wv, wv + NW, ...; the
+// next item's loads are issued before the current item is computed. Gate/up items never
+// wait for another wave; down items wait for their unit's h (after every gate/up item
+// of this wave), so every h is eventually published. With FUSED, the U-th contribution
+// of a column writes the output (U = core + queue units, learnt from the epoch word).
+template <int D, bool FUSED>
+__device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
+                                              unsigned long long* yacc, XRegs<D>& xr, int& xstate, Epoch& ep,
+                                              uint32_t early, Pending& pd, uint32_t u0, uint32_t u1, uint32_t wv,
+                                              uint32_t NW) {
+    using Gm = GuGeom<D>;
+    constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
-    if (g0 >= g1) return true;
-    struct Meta {
-        uint64_t* hrow;
-        int n0, nvalid;
-    };
-    const uint32_t ulast = u0 + (g1 - 1) / bpu;      // last unit of the share (inclusive)
-    auto issue = [&](uint32_t bi, GuLoads<D, NB>& L, Meta& m) -> bool {
-        const uint32_t unit = u0 + bi / bpu;
-        if (unit >= chunk0 + chunk_n) {
-            chunk0 = unit;
-            chunk_n = min((uint32_t)kUnitChunk, ulast + 1 - unit);
-            chunk_off = 0;
-            if (threadIdx.x == 0)
-                for (uint32_t i = 0; i < chunk_n; ++i) sh.ulist[i] = chunk0 + i;
-            if (!load_units(a, sh, slot, chunk_n)) return false;
+    const uint32_t nu = u1 - u0;
+    const uint32_t ipu = (G + Gm::NPW - 1) / Gm::NPW;   // gate/up items per unit
+    const uint32_t NG = nu * ipu, N = NG + nu * T;
+    if (wv >= N) return true;
+    const uint32_t K = (N - wv + NW - 1) / NW;                   // items of this wave
+    const uint32_t KG = wv < NG ? (NG - wv + NW - 1) / NW : 0;   // the first KG are gate/up
+    const uint32_t need = u1 > a.core_count ? u1 - a.core_count : 0;
+    // Descriptors first, then x: loads complete in issue order, so the first item's
+    // address computation waits for the descriptors only.
+    uint32_t word = 0, k0 = 0;
+    if (!fetch_descs(a, slot, u0, need, wv, NW, 0, min(K, (uint32_t)kDescItems), NG, ipu, T, word)) return false;
+    if (KG) need_x<D>(a.x, xr, xstate, 1);
+    const int wave = threadIdx.x >> 6;
+    uint16_t* hs = sh.hs[wave];
+    uint16_t* ss = sh.ss[wave];
+    GuItem<D> ga, gb;
+    DnItem dc_, dd_;
+    ItemMeta ma, mb, mc, md;
+    uint32_t U = 0;
+    bool have_u = !FUSED;
+
+    // Gate/up items come first in every wave's list. Phase 1 walks them with two
+    // gate/up slots (A: even k, B: odd k); the first down item is issued into down slot
+    // C during the last gate/up computation. Phase 2 walks the down items with slots C
+    // and D. Slots are fixed at compile time (issue / compute take their objects).
+    auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
+        if (k - k0 >= (uint32_t)kDescItems) {
+            k0 = k;
+            if (!fetch_descs(a, slot, u0, need, wv, NW, k0, min(K - k0, (uint32_t)kDescItems), NG, ipu, T, word))
+                return false;
         }
+        return unit_of(a, slot, b, word, k - k0, D, u);
+    };
+    auto issue_gu = [&](uint32_t k, GuItem<D>& gi, ItemMeta& m) -> bool {
         Unit u;
-        if (!unit_from(a, sh, slot, b, chunk_off + unit - chunk0, D, &u)) return false;
-        if (threadIdx.x == 0 && a.first_compute && bi % bpu == 0) a.first_compute[u.dest] = now_ticks();
-        m.n0 = (int)((bi % bpu) * NB);
-        m.nvalid = min(NB, (int)G - m.n0);
+        if (!fetch_unit(k, u)) return false;
+        const uint32_t i = wv + k * NW, rel = i / ipu;
+        m.dest = u.dest;
         m.hrow = a.hbuf + (size_t)u.dest * G;
-        gu_issue<D, NB>(u.grp, u.sc, m.n0, m.nvalid, L);
+        m.n0 = (int)((i - rel * ipu) * Gm::NPW);
+        m.nvalid = min(Gm::NPW, (int)G - m.n0);
+        gu_issue<D>(u.grp, u.sc, m.n0, m.nvalid, gi);
         return true;
     };
-    // Loads return in issue order (vmcnt), so the issue order is the order data can be
-    // used in: x, the first batch, then the caller's loads (after_first), then the rest.
-    if (!have_x) {
-        load_x<D, NB>(a.x, xr);
-        have_x = true;
-    }
-    GuLoads<D, NB> L[kGuBuffers];
-    Meta M[kGuBuffers];
-#pragma unroll
-    for (int q = 0; q < kGuBuffers; ++q) {
-        if (g0 + q < g1 && !issue(g0 + q, L[q], M[q])) return false;
-        if (q == 0 && !after_first()) return false;
-    }
-    for (uint32_t bi = g0; bi < g1; bi += kGuBuffers) {
-#pragma unroll
-        for (int q = 0; q < kGuBuffers; ++q) {
-            if (bi + q < g1) {
-                gu_compute<D, NB>(L[q], xr, M[q].hrow, M[q].n0, M[q].nvalid, a.seq);
-                if (bi + q == g0) stamp(a, kStampFirstData);
-                if (bi + q + kGuBuffers < g1 && !issue(bi + q + kGuBuffers, L[q], M[q])) return false;
-            }
-        }
-    }
-    return true;
-}
-
-// Execution counters (diagnostics): a unit counts once all of its down tiles are done.
-__device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot, uint32_t unit, uint32_t dest,
-                                                uint32_t tiles) {
-    if (threadIdx.x == 0 && add_agent(slot + kSyncUnits + unit * kLine, 1u) == tiles - 1)
-        __hip_atomic_fetch_add(a.executions + dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-}
-
-// ---------------------------------------------------------------------------------
-// Down projection work: the (unit, column tile) pairs of units [u0, u1) in tile-major
-// order -- position p is tile p / units, unit p % units -- cut into one contiguous range
-// per worker. A worker's consecutive pairs mostly share a column tile, so a run of them
-// is summed locally and reaches the column accumulators as one atomic per column. Up to
-// kMaxDnTiles pairs per round: their weight loads are issued together, then the h of all
-// of them is staged in one polling pass.
-// ---------------------------------------------------------------------------------
-
-// Position in the tile-major pair order (relative unit, tile).
-struct PairCursor {
-    uint32_t unit, tile, units;
-    __device__ PairCursor(uint32_t p, uint32_t n) : unit(p % n), tile(p / n), units(n) {}
-    __device__ void advance() {
-        if (++unit == units) {
-            unit = 0;
-            ++tile;
-        }
-    }
-};
-
-// Column accumulation of one thread (column c0 + threadIdx.x of the current tile run):
-// a local fixed-point sum of m contributions, flushed as one packed atomic; the returned
-// word is checked at the next flush (or at the end) so the atomic's latency overlaps work.
-struct ColumnRun {
-    long long sum = 0;
-    uint32_t m = 0;
-    int col = -1;
-    unsigned long long pend = 0;
-    int pend_col = -1;
-};
-
-__device__ __forceinline__ void check_pending(const MlpArgs& a, ColumnRun& r, uint32_t U) {
-    if (r.pend_col >= 0 && U && (uint32_t)(r.pend >> 52) == U) write_output(a, r.pend_col, r.pend, U);
-    r.pend_col = -1;
-}
-
-__device__ __forceinline__ void flush_run(const MlpArgs& a, unsigned long long* yacc, ColumnRun& r, uint32_t U) {
-    if (r.m == 0) return;
-    const unsigned long long add =
-        (unsigned long long)(r.sum + (long long)r.m * kAccBias) + (unsigned long long)r.m * kAccOne;
-    const unsigned long long now =
-        __hip_atomic_fetch_add(yacc + r.col, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
-    check_pending(a, r, U);
-    r.pend = now;
-    r.pend_col = r.col;
-    r.sum = 0;
-    r.m = 0;
-}
-
-// Adds the reduced tile value of this thread's column into its run (new run when the
-// column changes). Out-of-range values are clipped and reported.
-__device__ __forceinline__ void run_add(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, ColumnRun& r,
-                                        int col, float value, uint32_t U) {
-    if (col != r.col) {
-        flush_run(a, yacc, r, U);
-        r.col = col;
-    }
-    float v = value * kAccScale;
-    if (!(fabsf(v) < (float)(kAccBias - 1))) {  // out of range or NaN: clip and report
-        v = v > 0.f ? (float)(kAccBias - 1) : -(float)(kAccBias - 1);
-        raise_status(a, slot, kStatusRange);
-    }
-    r.sum += __float2ll_rn(v);
-    r.m += 1;
-}
-
-// One round of up to kMaxDnTiles (unit, column tile) pairs of the down projection:
-// every weight and scale load of the round is issued first (dn_issue_round), then h and
-// the scales are staged in LDS in one polling pass and each pair's tile is computed and
-// added into the column runs (dn_finish_round).
-struct DnRound {
-    DnLoads dl[kMaxDnTiles];
-    uint32_t sv[kMaxDnTiles];                        // this thread's staged scale (fp16 bits)
-    uint32_t tile[kMaxDnTiles], index[kMaxDnTiles];  // column tile, unit index
-    uint32_t npairs;
-};
-
-// unit_of(i, &unit) names pair i's validated unit.
-template <int D, class UnitOf>
-__device__ __forceinline__ bool dn_issue_round(const MlpArgs& a, Shared& sh, const DnGeom& gm, DnRound& rd,
-                                               UnitOf unit_of) {
-    const int tc = a.dn_tile;
-#pragma unroll
-    for (int i = 0; i < kMaxDnTiles; ++i) {
-        rd.sv[i] = 0;
-        if ((uint32_t)i < rd.npairs) {
-            Unit u;
-            if (!unit_of(i, &u)) return false;
-            dn_issue<D>(u.grp, gm, (int)rd.tile[i] * tc, rd.dl[i]);
-            rd.sv[i] = dn_scale_issue<D>(u.sc, gm, a.group_size, (int)rd.tile[i] * tc);
-            if (threadIdx.x == 0) sh.pdest[i] = u.dest;
-        }
-    }
-    return true;
-}
-
-template <int D>
-__device__ __forceinline__ bool dn_finish_round(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
-                                                const DnGeom& gm, const DnRound& rd, uint32_t U, ColumnRun& run) {
-    const int tc = a.dn_tile;
-    const uint32_t hstride = (uint32_t)gm.rpp * kMaxRows;
-    if (!stage_round(a, slot, sh, rd.npairs, gm, a.group_size, rd.sv)) return false;
-#pragma unroll
-    for (int i = 0; i < kMaxDnTiles; ++i) {
-        if ((uint32_t)i < rd.npairs) {
-            dn_compute(rd.dl[i], gm, sh.hs + i * hstride, sh.ss + i * kTileScales, sh.red, tc);
-            if (threadIdx.x < (uint32_t)tc)
-                run_add(a, slot, yacc, run, (int)rd.tile[i] * tc + threadIdx.x, sh.red[kRedFloats + threadIdx.x], U);
-            if (a.executions) count_execution(a, slot, rd.index[i], sh.pdest[i], D / tc);
-        }
-    }
-    return true;
-}
-
-// ---------------------------------------------------------------------------------
-// Units [u0, u1) on W persistent workers. Every worker takes a share of both halves:
-//  - gate/up: a contiguous range of neuron batches (gate_up_share);
-//  - down: a contiguous range of the tile-major (unit, column tile) pairs (PairCursor).
-// The loads of the first down round are issued right after the first gate/up batch (one
-// descriptor fetch covers both), so they stream with the gate/up loads. A worker waits
-// for h only after its whole gate/up share is done, hence every h is eventually published.
-// ---------------------------------------------------------------------------------
-template <int D, bool FUSED>
-__device__ __forceinline__ bool process_units(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
-                                              unsigned long long* yacc, XRegs<D, Batch<D>::N>& xr, bool& have_x,
-                                              uint32_t u0, uint32_t u1, uint32_t k, uint32_t W,
-                                              uint32_t early) {
-    constexpr int NB = Batch<D>::N;
-    const int G = a.group_size;
-    const int tc = a.dn_tile;
-    const uint32_t T = D / tc;                                    // tiles per unit
-    // gate/up share
-    const uint32_t bpu = (G + NB - 1) / NB;                       // batches per unit
-    const uint32_t nb = (u1 - u0) * bpu;
-    const uint32_t per_g = (nb + W - 1) / W;
-    const uint32_t g0 = min(k * per_g, nb), g1 = min(g0 + per_g, nb);
-    // down share: pairs [s0, s1) of the tile-major order
-    const uint32_t nu = u1 - u0;
-    const uint32_t P = nu * T;
-    const uint32_t per_d = (P + W - 1) / W;
-    const uint32_t s0 = min(k * per_d, P), s1 = min(s0 + per_d, P);
-    PairCursor cur(s0, nu);   // next down pair
-    const DnGeom gm(G, tc);
-    // first down round + first gate/up units: one descriptor fetch
-    DnRound rd;
-    rd.npairs = s0 < s1 ? min((uint32_t)kMaxDnTiles, s1 - s0) : 0u;
-#pragma unroll
-    for (int i = 0; i < kMaxDnTiles; ++i) {
-        rd.tile[i] = 0;
-        rd.index[i] = 0;
-        if ((uint32_t)i < rd.npairs) {
-            rd.tile[i] = cur.tile;
-            rd.index[i] = u0 + cur.unit;
-            if (threadIdx.x == 0) sh.ulist[i] = u0 + cur.unit;
-            cur.advance();
-        }
-    }
-    uint32_t gchunk0 = 0, gchunk_n = 0;
-    if (g0 < g1) {
-        gchunk0 = u0 + g0 / bpu;
-        gchunk_n = min((uint32_t)kUnitChunk - rd.npairs, u0 + (g1 - 1) / bpu + 1 - gchunk0);
-        if (threadIdx.x == 0)
-            for (uint32_t i = 0; i < gchunk_n; ++i) sh.ulist[rd.npairs + i] = gchunk0 + i;
-    }
-    if (rd.npairs + gchunk_n && !load_units(a, sh, slot, rd.npairs + gchunk_n)) return false;
-    auto issue_down = [&]() {
-        return dn_issue_round<D>(a, sh, gm, rd, [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); });
+    auto issue_dn = [&](uint32_t k, DnItem& di, ItemMeta& m) -> bool {
+        Unit u;
+        if (!fetch_unit(k, u)) return false;
+        const uint32_t d = wv + k * NW - NG;
+        m.grp = u.grp;
+        m.sc = u.sc;
+        m.dest = u.dest;
+        m.hrow = a.hbuf + (size_t)u.dest * G;
+        m.unit = u0 + d / T;
+        m.tile = d % T;
+        dn_issue<D>(u.grp, u.sc, m.hrow, (int)G, (int)m.tile, 0, a.seq, di);
+        // a fresh look at the epoch word, in flight with the item (U is needed to finish it)
+        if (FUSED && !ep.known && lane_id() == 0) early = ld_agent(slot + kSyncEpoch);
+        return true;
     };
-    if (g0 < g1) {
-        if (!gate_up_share<D>(a, sh, slot, b, xr, have_x, u0, g0, g1, bpu, gchunk0, gchunk_n, rd.npairs, issue_down))
-            return false;
-    } else if (!issue_down()) {
-        return false;
-    }
-    if (s0 >= s1) return true;
-    uint32_t U = 0;
-    if (FUSED) {
-        if (!await_epoch(a, sh, slot, early)) return false;
-        U = a.core_count + sh.ep_total;
-    }
-    ColumnRun run;
-    for (uint32_t done = s0;;) {
-        if (!dn_finish_round<D>(a, sh, slot, yacc, gm, rd, U, run)) return false;
-        if (done == s0) stamp(a, kStampDnComputed);
-        done += rd.npairs;
-        if (done >= s1) break;
-        rd.npairs = min((uint32_t)kMaxDnTiles, s1 - done);
-#pragma unroll
-        for (int i = 0; i < kMaxDnTiles; ++i) {
-            if ((uint32_t)i < rd.npairs) {
-                rd.tile[i] = cur.tile;
-                rd.index[i] = u0 + cur.unit;
-                if (threadIdx.x == 0) sh.ulist[i] = u0 + cur.unit;
-                cur.advance();
-            }
+    // the item after k: gate/up into `gn`, or the first down item into slot C
+    auto issue_next = [&](uint32_t k, GuItem<D>& gn, ItemMeta& mn) -> bool {
+        if (k >= K) return true;
+        return k < KG ? issue_gu(k, gn, mn) : issue_dn(k, dc_, mc);
+    };
+    auto compute_gu = [&](uint32_t k, const GuItem<D>& gi, const ItemMeta& m) {
+        if (a.first_compute && m.n0 == 0 && lane_id() == 0) a.first_compute[m.dest] = now_ticks();
+        need_x<D>(a.x, xr, xstate, 2);
+        gu_compute<D>(gi, xr, m.hrow, m.n0, m.nvalid, a.seq);
+        if (k == 0) stamp(a, kStampFirstData);
+    };
+    auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
+        if (!have_u) {
+            if (!await_epoch(a, slot, ep, early)) return false;
+            U = a.core_count + ep.total;
+            have_u = true;
         }
-        if (!load_units(a, sh, slot, rd.npairs)) return false;
-        if (!dn_issue_round<D>(a, sh, gm, rd,
-                               [&](int i, Unit* u) { return unit_from(a, sh, slot, b, (uint32_t)i, D, u); }))
-            return false;
-    }
-    flush_run(a, yacc, run, U);
-    check_pending(a, run, U);
-    return true;
-}
+        float acc[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+        for (int r0 = 0; r0 < (int)G; r0 += kDnRows) {
+            if (r0) dn_issue<D>(m.grp, m.sc, m.hrow, (int)G, (int)m.tile, r0, a.seq, di);
+            if (!dn_wait_h(a, slot, m.hrow, (int)G, r0, di)) return false;
+            dn_accumulate(di, hs, ss, acc);
+        }
+        float c0, c1;
+        dn_reduce(acc, c0, c1);
+        const int lane = lane_id();
+        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + 16 * (lane & 7) + 2 * (lane >> 3), c0, c1, U, pd);
+        if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
+        if (k == KG) stamp(a, kStampDnComputed);
+        return true;
+    };
 
-// Process a whole unit inside one workgroup (claim path): gate/up of every neuron, then
-// every column tile of the down projection, without cross-workgroup waits.
-template <int D, bool FUSED>
-__device__ __forceinline__ bool run_unit_solo(const MlpArgs& a, Shared& sh, uint32_t* slot, unsigned long long* yacc,
-                                              const XRegs<D, Batch<D>::N>& xr, const Unit& u, uint32_t index) {
-    constexpr int NB = Batch<D>::N;
-    const int G = a.group_size;
-    uint64_t* hrow = a.hbuf + (size_t)u.dest * G;
-    if (threadIdx.x == 0 && a.first_compute) a.first_compute[u.dest] = now_ticks();
-    for (int n0 = 0; n0 < G; n0 += NB) {
-        GuLoads<D, NB> gl;
-        gu_issue<D, NB>(u.grp, u.sc, n0, min(NB, G - n0), gl);
-        gu_compute<D, NB>(gl, xr, hrow, n0, min(NB, G - n0), a.seq);
-    }
-    const int tc = a.dn_tile;
-    const uint32_t T = D / tc;
-    const DnGeom gm(G, tc);
-    const uint32_t U = FUSED ? a.core_count + sh.ep_total : 0u;
-    ColumnRun run;
-    for (uint32_t t0 = 0; t0 < T; t0 += kMaxDnTiles) {
-        DnRound rd;
-        rd.npairs = min((uint32_t)kMaxDnTiles, T - t0);
-#pragma unroll
-        for (int i = 0; i < kMaxDnTiles; ++i) {
-            rd.tile[i] = t0 + (uint32_t)i;
-            rd.index[i] = index;
+    if (!issue_next(0, ga, ma)) return false;
+    for (uint32_t k = 0; k < KG; k += 2) {
+        if (!issue_next(k + 1, gb, mb)) return false;
+        compute_gu(k, ga, ma);
+        if (k + 1 < KG) {
+            if (!issue_next(k + 2, ga, ma)) return false;
+            compute_gu(k + 1, gb, mb);
         }
-        if (!dn_issue_round<D>(a, sh, gm, rd, [&](int, Unit* out) {
-                *out = u;
-                return true;
-            }))
-            return false;
-        if (!dn_finish_round<D>(a, sh, slot, yacc, gm, rd, U, run)) return false;
     }
-    flush_run(a, yacc, run, U);
-    check_pending(a, run, U);
+    for (uint32_t k = KG; k < K; k += 2) {
+        if (k + 1 < K && !issue_dn(k + 1, dd_, md)) return false;
+        if (!compute_dn(k, dc_, mc)) return false;
+        if (k + 1 < K) {
+            if (k + 2 < K && !issue_dn(k + 2, dc_, mc)) return false;
+            if (!compute_dn(k + 1, dd_, md)) return false;
+        }
+    }
     return true;
 }
 
@@ -1064,40 +849,19 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
     }
 }
 
-// Descriptor of published position `pos` from the device-side table; false when the
-// worker must leave (abort or timeout) before the position is mirrored.
-__device__ __forceinline__ bool load_queue_wg(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t pos, ExecDesc* out) {
-    __syncthreads();  // previous readers of sh.desc / sh.word[2] are done
-    if (threadIdx.x == 0) {
-        uint32_t ok = 1;
-        Waiter wt(a.spin_limit);
-        while (ld_agent(slot + kSyncReady) <= pos) {
-            if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
-            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (ok)
-            for (int k = 0; k < 5; ++k) sh.desc[k] = ld_agent(a.qmirror + 5 * pos + k);
-        sh.word[2] = ok;
-    }
-    __syncthreads();
-    // every lane reads the same words: make them wave-uniform (scalar registers)
-    out->logical_group = __builtin_amdgcn_readfirstlane(sh.desc[0]);
-    out->physical_group = __builtin_amdgcn_readfirstlane(sh.desc[1]);
-    out->source_slot = __builtin_amdgcn_readfirstlane(sh.desc[2]);
-    out->dest_slot = __builtin_amdgcn_readfirstlane(sh.desc[3]);
-    out->source_kind = (leanstream::runtime::SourceKind)__builtin_amdgcn_readfirstlane(sh.desc[4]);
-    return __builtin_amdgcn_readfirstlane(sh.word[2]) != 0;
-}
-
 // Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86),
-// against the mirrored ready count. Returns the number of claimed positions (0 = leave).
-__device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total) {
-    __syncthreads();  // previous readers of sh.word[5..6] are done
+// against the mirrored ready count. Every wave of the workgroup takes part; `ok` is this
+// wave's success so far. Returns the number of claimed positions (0 = leave, also when
+// any wave of the workgroup failed).
+__device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total, bool ok) {
+    if (lane_id() == 0) sh.wfail[threadIdx.x >> 6] = ok ? 0u : 1u;
+    __syncthreads();  // failure flags written; previous readers of sh.word[5..6] are done
     if (threadIdx.x == 0) {
         uint32_t got = 0, head = 0;
+        bool failed = false;
+        for (int w = 0; w < kWaves; ++w) failed = failed || sh.wfail[w];
         Waiter wt(a.spin_limit);
-        for (;;) {
+        while (!failed) {
             if (ld_agent(slot + kSyncAbort)) break;
             const uint32_t ready = ld_agent(slot + kSyncReady);
             head = ld_agent(slot + kSyncClaimHead);
@@ -1121,55 +885,63 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
         sh.word[6] = got;
     }
     __syncthreads();
-    return sh.word[6];
+    return __builtin_amdgcn_readfirstlane(sh.word[6]);
 }
 
-// Claim path (progressive publication): ready pairs claimed one at a time, each unit of
-// a pair processed whole by the claiming workgroup.
+// Claim path (progressive publication): ready pairs claimed one at a time; the four
+// waves of the claiming workgroup walk the pair's items (gate/up first, then down).
 template <int D, bool FUSED>
-__device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b, unsigned long long* yacc,
-                           const XRegs<D, Batch<D>::N>& xr, uint32_t total) {
+__device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
+                                           unsigned long long* yacc, XRegs<D>& xr, int& xstate, Epoch& ep,
+                                           Pending& pd, uint32_t total) {
+    bool ok = true;
     for (;;) {
-        const uint32_t got = claim_pair(a, sh, slot, total);
+        const uint32_t got = claim_pair(a, sh, slot, total, ok);
         if (!got) return;
-        const uint32_t head = sh.word[5];
-        for (uint32_t k = 0; k < got; ++k) {
-            Unit u;
-            if (!fetch_unit(a, sh, slot, b, a.core_count + head + k, D, &u)) return;
-            if (!run_unit_solo<D, FUSED>(a, sh, slot, yacc, xr, u, a.core_count + head + k)) return;
-        }
+        const uint32_t head = __builtin_amdgcn_readfirstlane(sh.word[5]);
+        ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, 0u, pd, a.core_count + head,
+                                     a.core_count + head + got, threadIdx.x >> 6, kWaves);
     }
 }
 
-// One persistent worker of a launch: its role share of the resident (core) units, then
-// of the queue (all-ready fast path), or the claim loop (progressive path).
-// Workers [0, NG) take the gate/up role, the others the down role.
-// One persistent worker of a launch: its share of the resident (core) units, then of
-// the queue (all-ready fast path), or the claim loop (progressive path).
+// One persistent worker workgroup of a launch: each of its waves walks its share of the
+// resident (core) units' items, then of the queue's (all-ready fast path); or the
+// workgroup runs the claim loop (progressive path).
 template <int D, bool FUSED, bool CORE, bool QUEUE>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t NW = W * kWaves, wv = blockIdx.x * kWaves + wave;
     unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
-    init_shared(sh);
-    XRegs<D, Batch<D>::N> xr;
-    bool have_x = false;
-    const uint32_t early = epoch_peek(sh, slot);
-    if (CORE && a.core_count &&
-        !process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, 0, a.core_count, blockIdx.x, W, early))
-        return;
+    XRegs<D> xr;
+    int xstate = 0;
+    Epoch ep = {0, 0, 0, 0};
+    Pending pd;
+    pd.col = -1;
+    const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
+    bool ok = true;
+    if (CORE && a.core_count)
+        ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, early, pd, 0, a.core_count, wv, NW);
     stamp(a, kStampCoreDone);
-    if (!QUEUE) return;
-    if (!await_epoch(a, sh, slot, early)) return;
-    stamp(a, kStampEpoch);
-    const uint32_t total = sh.ep_total;
-    if (!total) return;
-    if (sh.ep_path == 2) {
-        process_units<D, FUSED>(a, sh, slot, b, yacc, xr, have_x, a.core_count, a.core_count + total, blockIdx.x, W, 0);
-    } else {
-        if (!have_x) load_x<D, Batch<D>::N>(a.x, xr);
-        claim_loop<D, FUSED>(a, sh, slot, b, yacc, xr, total);
+    if (QUEUE) {
+        ok = ok && await_epoch(a, slot, ep, early);
+        stamp(a, kStampEpoch);
+        // One decision for the whole workgroup (the claim path synchronises its waves).
+        if (lane_id() == 0) sh.wpath[wave] = ok && ep.total ? ep.path : 0u;
+        __syncthreads();
+        uint32_t path = sh.wpath[0];
+        for (int w = 1; w < kWaves; ++w)
+            if (sh.wpath[w] != path) path = 0;
+        path = __builtin_amdgcn_readfirstlane(path);
+        if (path == 2) {
+            ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, early, pd, a.core_count,
+                                         a.core_count + ep.total, wv, NW);
+        } else if (path == 1) {
+            claim_loop<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, pd, ep.total);
+        }
+        stamp(a, kStampQueueDone);
     }
-    stamp(a, kStampQueueDone);
+    check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
 }
 
 // The mirror workgroup: wave 0 mirrors the queue while waves 1..3 clear what the next
@@ -1202,6 +974,7 @@ __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) 
         add_agent(slot + kSyncExit, 1u) == groups - 1)
         __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
+
 
 __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { return a.yacc + (a.seq & 1) * a.width; }
 
