@@ -7,9 +7,9 @@
 //   y[c]   = fp16( sum over the U destination rows of sum_n h_n w_down(n, c) )  (fp32)
 //
 // Work decomposition (MI355X-specific). The units of a launch (descriptors, one group of
-// G neurons each) are cut into wave-sized items of about 4 KB of weights:
-//   - gate/up items: NPW neurons of one unit; one 64-lane wave computes their gate and
-//     up rows and publishes h;
+// G neurons each) are cut into wave-sized items of a few KB of weights:
+//   - gate/up items: NPI neurons of one unit (about 8 KB of weights); one 64-lane wave
+//     computes their gate and up rows and publishes h;
 //   - down items: one 128-column tile (one scale block) of one unit over all G rows.
 // All gate/up items come first, then the down items (unit-major). Wave w of the
 // persistent grid takes items w, w + NW, w + 2 NW, ... and keeps the next item's loads in
@@ -98,6 +98,10 @@ __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, 
 __device__ __forceinline__ _Float16 half_bits(uint16_t v) { return __builtin_bit_cast(_Float16, v); }
 __device__ __forceinline__ float round_half(float v) { return (float)(_Float16)v; }
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+// The wave's index in the workgroup, in a scalar register (the compiler cannot tell that
+// threadIdx.x >> 6 is uniform across a wave, and would keep everything derived from it in
+// vector registers).
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 // Lane 0's value for the whole wave (call with lane 0 active).
 __device__ __forceinline__ uint32_t wave_bcast(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -160,14 +164,17 @@ __device__ __forceinline__ bool wave_should_stop(const MlpArgs& a, uint32_t* slo
 
 // ---------------------------------------------------------------------------------
 // Gate/up items. A width-D row of one projection is CPR 16-byte chunks; LPR lanes share a
-// row (CPL chunks each), so one wave covers NPW neurons: one item.
+// row (CPL chunks each), so one wave pass covers NPW neurons; an item is RPL passes
+// (about 8 KB of gate/up weights), NPI neurons.
 // ---------------------------------------------------------------------------------
 template <int D>
 struct GuGeom {
     static constexpr int CPR = D / 32;                 // 16-byte chunks per projection row
     static constexpr int LPR = CPR < 64 ? CPR : 64;    // lanes sharing one row
     static constexpr int CPL = CPR / LPR;              // chunks per lane per row
-    static constexpr int NPW = 64 / LPR;               // neurons per wave: one gate/up item
+    static constexpr int NPW = 64 / LPR;               // neurons per wave pass
+    static constexpr int RPL = CPL >= 4 ? 1 : 4 / CPL;  // passes per item: 32 * CPL * RPL = 128 bytes per lane
+    static constexpr int NPI = NPW * RPL;              // neurons per gate/up item
     static constexpr int BLOCKS = D / 128;             // scale blocks per row
     static_assert(D % 256 == 0 && CPR >= 8, "width must be a multiple of 256");
 };
@@ -230,34 +237,64 @@ __device__ __forceinline__ void need_x(const uint16_t* x, XRegs<D>& xr, int& sta
 
 template <int D>
 struct GuItem {
-    u32x4 w[2][GuGeom<D>::CPL];
-    uint32_t s[2][GuGeom<D>::CPL];   // fp16 bits (32-bit registers)
+    u32x4 w[GuGeom<D>::RPL][2][GuGeom<D>::CPL];
+    uint32_t s[GuGeom<D>::RPL][2][GuGeom<D>::CPL];   // fp16 bits (32-bit registers)
 };
 
+// A wave-uniform pointer, in scalar registers: loads then take a scalar base plus a
+// 32-bit per-lane offset (the values are uniform; the compiler cannot always prove it).
+template <class T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
 // Issue every load of a gate/up item: neurons n0 .. n0 + nvalid - 1 of the unit whose
-// packed bytes start at grp and scale rows at sc.
+// packed bytes start at grp and scale rows at sc; pass p covers neurons n0 + p NPW + sub.
+// A full item (every neuron valid) needs no per-lane guard.
 template <int D>
 __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, int nvalid, GuItem<D>& L) {
     using Gm = GuGeom<D>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
-    const bool ok = sub < nvalid;
-    const int n = n0 + (ok ? sub : 0);
-    const uint8_t* row = grp + (size_t)n * (3 * D / 2);
-    const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
+    if (nvalid == Gm::NPI) {
 #pragma unroll
-    for (int k = 0; k < Gm::CPL; ++k) {
-        const int chunk = r + Gm::LPR * k;
-        if (ok) {
-            L.w[0][k] = ld_stream16(row + 16 * chunk);
-            L.w[1][k] = ld_stream16(row + D / 2 + 16 * chunk);
-            L.s[0][k] = srow[chunk >> 2];
-            L.s[1][k] = srow[Gm::BLOCKS + (chunk >> 2)];
-        } else {
-            L.w[0][k] = u32x4{0, 0, 0, 0};
-            L.w[1][k] = u32x4{0, 0, 0, 0};
-            L.s[0][k] = 0;
-            L.s[1][k] = 0;
+        for (int p = 0; p < Gm::RPL; ++p) {
+            const uint8_t* row = uniform_ptr(grp + (size_t)(n0 + p * Gm::NPW) * (3 * D / 2));
+            const uint16_t* srow = uniform_ptr(sc + (size_t)(n0 + p * Gm::NPW) * 3 * Gm::BLOCKS);
+            const uint32_t wo = (uint32_t)sub * (3 * D / 2) + 16 * r, so = (uint32_t)sub * 3 * Gm::BLOCKS + (r >> 2);
+#pragma unroll
+            for (int k = 0; k < Gm::CPL; ++k) {
+                L.w[p][0][k] = ld_stream16(row + wo + 16 * Gm::LPR * k);
+                L.w[p][1][k] = ld_stream16(row + wo + 16 * Gm::LPR * k + D / 2);
+                L.s[p][0][k] = srow[so + (Gm::LPR / 4) * k];
+                L.s[p][1][k] = srow[so + (Gm::LPR / 4) * k + Gm::BLOCKS];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int p = 0; p < Gm::RPL; ++p) {
+        const int nu = p * Gm::NPW + sub;
+        const bool ok = nu < nvalid;
+        const int n = n0 + (ok ? nu : 0);
+        const uint8_t* row = grp + (size_t)n * (3 * D / 2);
+        const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
+#pragma unroll
+        for (int k = 0; k < Gm::CPL; ++k) {
+            const int chunk = r + Gm::LPR * k;
+            if (ok) {
+                L.w[p][0][k] = ld_stream16(row + 16 * chunk);
+                L.w[p][1][k] = ld_stream16(row + D / 2 + 16 * chunk);
+                L.s[p][0][k] = srow[chunk >> 2];
+                L.s[p][1][k] = srow[Gm::BLOCKS + (chunk >> 2)];
+            } else {
+                L.w[p][0][k] = u32x4{0, 0, 0, 0};
+                L.w[p][1][k] = u32x4{0, 0, 0, 0};
+                L.s[p][0][k] = 0;
+                L.s[p][1][k] = 0;
+            }
         }
     }
 }
@@ -293,33 +330,37 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const XRegs<D>& x
     using Gm = GuGeom<D>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
-    float acc[2] = {0.f, 0.f};
 #pragma unroll
-    for (int proj = 0; proj < 2; ++proj) {
+    for (int p = 0; p < Gm::RPL; ++p) {
+        float acc[2] = {0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < Gm::CPL; ++k) {
-            const _Float16 sv = half_bits((uint16_t)L.s[proj][k]);
-            const h2 s2 = {sv, sv};
-            const u32x4 v = L.w[proj][k];
-            const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+        for (int proj = 0; proj < 2; ++proj) {
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                h2 w[4];
-                dequant8(words[g], s2, w);
+            for (int k = 0; k < Gm::CPL; ++k) {
+                const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
+                const h2 s2 = {sv, sv};
+                const u32x4 v = L.w[p][proj][k];
+                const uint32_t words[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-                for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], as_h2(xr.v[k][4 * g + q]), acc[proj]);
+                for (int g = 0; g < 4; ++g) {
+                    h2 w[4];
+                    dequant8(words[g], s2, w);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], as_h2(xr.v[k][4 * g + q]), acc[proj]);
+                }
             }
         }
-    }
-    acc[0] = group_sum<Gm::LPR>(acc[0]);
-    acc[1] = group_sum<Gm::LPR>(acc[1]);
-    if (r == Gm::LPR - 1 && sub < nvalid) {
-        const float g = round_half(acc[0]);
-        const float u = round_half(acc[1]);
-        const float s = round_half(g / (1.0f + __expf(-g)));
-        const float h = round_half(s * u);
-        __hip_atomic_store(hrow + n0 + sub, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        acc[0] = group_sum<Gm::LPR>(acc[0]);
+        acc[1] = group_sum<Gm::LPR>(acc[1]);
+        const int nu = p * Gm::NPW + sub;
+        if (r == Gm::LPR - 1 && nu < nvalid) {
+            const float g = round_half(acc[0]);
+            const float u = round_half(acc[1]);
+            const float s = round_half(g / (1.0f + __expf(-g)));
+            const float h = round_half(s * u);
+            __hip_atomic_store(hrow + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -342,12 +383,23 @@ template <int D>
 __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc, const uint64_t* hrow, int G, int tile,
                                          int r0, uint32_t seq, DnItem& it) {
     constexpr int BLOCKS = D / 128;
+    constexpr int RB = 3 * D / 2;
     const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    if (r0 + kDnRows <= G) {   // every row of the pass exists: no per-lane guard
+        const uint8_t* base = uniform_ptr(grp + (size_t)r0 * RB + D + tile * (kDnCols / 2));
+        const uint32_t wo = (uint32_t)(8 * g) * RB + dc * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) it.w[j] = ld_stream8(base + wo + j * RB);
+        const uint16_t* srow = uniform_ptr(sc + (size_t)r0 * 3 * BLOCKS + 2 * BLOCKS + tile);
+        it.s = srow[(uint32_t)lane * 3 * BLOCKS];
+        it.h = ld_agent_u64(uniform_ptr(hrow + r0) + lane);
+        return;
+    }
     const uint8_t* base = grp + D + tile * (kDnCols / 2) + dc * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int n = r0 + 8 * g + j;
-        it.w[j] = n < G ? ld_stream8(base + (size_t)n * (3 * D / 2)) : u32x2{0, 0};
+        it.w[j] = n < G ? ld_stream8(base + (size_t)n * RB) : u32x2{0, 0};
     }
     const int n = r0 + lane;
     it.s = n < G ? sc[(size_t)n * 3 * BLOCKS + 2 * BLOCKS + tile] : 0u;
@@ -634,7 +686,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
     const uint32_t nu = u1 - u0;
-    const uint32_t ipu = (G + Gm::NPW - 1) / Gm::NPW;   // gate/up items per unit
+    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per unit
     const uint32_t NG = nu * ipu, N = NG + nu * T;
     if (wv >= N) return true;
     const uint32_t K = (N - wv + NW - 1) / NW;                   // items of this wave
@@ -645,7 +697,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     uint32_t word = 0, k0 = 0;
     if (!fetch_descs(a, slot, u0, need, wv, NW, 0, min(K, (uint32_t)kDescItems), NG, ipu, T, word)) return false;
     if (KG) need_x<D>(a.x, xr, xstate, 1);
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
     uint16_t* hs = sh.hs[wave];
     uint16_t* ss = sh.ss[wave];
     GuItem<D> ga, gb;
@@ -672,8 +724,8 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         const uint32_t i = wv + k * NW, rel = i / ipu;
         m.dest = u.dest;
         m.hrow = a.hbuf + (size_t)u.dest * G;
-        m.n0 = (int)((i - rel * ipu) * Gm::NPW);
-        m.nvalid = min(Gm::NPW, (int)G - m.n0);
+        m.n0 = (int)((i - rel * ipu) * Gm::NPI);
+        m.nvalid = min(Gm::NPI, (int)G - m.n0);
         gu_issue<D>(u.grp, u.sc, m.n0, m.nvalid, gi);
         return true;
     };
@@ -854,7 +906,7 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
 // wave's success so far. Returns the number of claimed positions (0 = leave, also when
 // any wave of the workgroup failed).
 __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total, bool ok) {
-    if (lane_id() == 0) sh.wfail[threadIdx.x >> 6] = ok ? 0u : 1u;
+    if (lane_id() == 0) sh.wfail[wave_id()] = ok ? 0u : 1u;
     __syncthreads();  // failure flags written; previous readers of sh.word[5..6] are done
     if (threadIdx.x == 0) {
         uint32_t got = 0, head = 0;
@@ -900,7 +952,7 @@ __device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_
         if (!got) return;
         const uint32_t head = __builtin_amdgcn_readfirstlane(sh.word[5]);
         ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, 0u, pd, a.core_count + head,
-                                     a.core_count + head + got, threadIdx.x >> 6, kWaves);
+                                     a.core_count + head + got, wave_id(), kWaves);
     }
 }
 
@@ -910,7 +962,7 @@ __device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_
 template <int D, bool FUSED, bool CORE, bool QUEUE>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = wave_id();
     const uint32_t NW = W * kWaves, wv = blockIdx.x * kWaves + wave;
     unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
     XRegs<D> xr;
