@@ -12,9 +12,9 @@
 //     computes their gate and up rows and publishes h;
 //   - down items: one 128-column tile (one scale block) of one unit over all G rows.
 // All gate/up items come first, then the down items (unit-major). Wave w of the
-// persistent grid takes items w, w + NW, w + 2 NW, ... and keeps the next item's loads in
-// flight while it computes the current one, so the whole chip walks through the layer in
-// one global order and HBM delivers it front to back. A down item needs the h of its
+// persistent grid takes items w, w + NW, w + 2 NW, ..., one in flight at a time; with
+// three workgroups per CU (12 waves) the whole layer is in flight at once at the
+// Ministral-8B shape, and HBM delivers it front to back. A down item needs the h of its
 // unit, produced by items about one round earlier, so it is normally ready by the time
 // the down weights arrive. Waves of a workgroup never wait for each other on this path;
 // a wave waits for h only after all of its own gate/up items.
@@ -47,8 +47,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kWgPerCu = 3;          // resident workgroups per CU (register budget 168 per lane)
 constexpr int kDnRows = 64;          // rows of one down-item pass: 8 row groups x 8 rows
 constexpr int kDescItems = 12;       // item descriptors fetched per round trip (5 words each)
+constexpr bool kSplitRoles = false;  // all-ready path: gate/up and down items on different workgroups
 static_assert(kDnCols == 128, "a down item is one scale block wide");
 
 // ---------------------------------------------------------------------------------
@@ -179,60 +181,77 @@ struct GuGeom {
     static_assert(D % 256 == 0 && CPR >= 8, "width must be a multiple of 256");
 };
 
-// x for this lane's chunks: loaded as raw words (load_x), then rearranged in place into
-// (k, k+4) fp16 pairs to match dequant8 (pair_x) when first needed, so that waiting for
-// x never holds up the issue of the weight loads.
+// x is shared by the workgroup through LDS, as (k, k+4) fp16 pairs to match dequant8,
+// in the order gu_compute reads it: block (k, g) of lane r (words 4g .. 4g+3 of its
+// chunk k, x columns 32 (r + LPR k) + 8g .. + 7) at xl[(4k + g) LPR + r], so a wave's 64
+// lanes read 1 KB of consecutive LDS per block. Each wave loads a quarter of x as raw
+// 16-byte pieces at its start (load_xpart) and writes it, paired, once it must have
+// arrived (stage_xpart: after the wave's first descriptors, loaded later, or when it
+// leaves); a wave about to compute gate/up waits until all four quarters are in.
 template <int D>
-struct XRegs {
-    uint32_t v[GuGeom<D>::CPL][16];
+struct XGeom {
+    static constexpr int N = D / 8;                               // 16-byte pieces of x
+    static constexpr int PER = (N + kThreads - 1) / kThreads;   // pieces per thread
 };
 
 template <int D>
-__device__ __forceinline__ void load_x(const uint16_t* x, XRegs<D>& xr) {
+struct XPart {
+    u32x4 v[XGeom<D>::PER];
+    bool staged;
+};
+
+template <int D>
+__device__ __forceinline__ void load_xpart(const uint16_t* x, XPart<D>& xp) {
+    const u32x4* src = reinterpret_cast<const u32x4*>(x);
+#pragma unroll
+    for (int j = 0; j < XGeom<D>::PER; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        xp.v[j] = i < XGeom<D>::N ? src[i] : u32x4{0, 0, 0, 0};
+    }
+    xp.staged = false;
+}
+
+template <int D>
+__device__ __forceinline__ void stage_xpart(XPart<D>& xp, u32x4* xl, uint32_t* count) {
     using Gm = GuGeom<D>;
-    const int r = lane_id() % Gm::LPR;
+    if (xp.staged) return;
 #pragma unroll
-    for (int k = 0; k < Gm::CPL; ++k) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(x + 32 * (r + Gm::LPR * k));
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const u32x4 w = src[g];
-            xr.v[k][4 * g + 0] = w.x;
-            xr.v[k][4 * g + 1] = w.y;
-            xr.v[k][4 * g + 2] = w.z;
-            xr.v[k][4 * g + 3] = w.w;
+    for (int j = 0; j < XGeom<D>::PER; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        if (i < XGeom<D>::N) {
+            const int c = i >> 2, g = i & 3, r = c % Gm::LPR, k = c / Gm::LPR;
+            // halves 8g .. 8g+7 of chunk c arrive as (0,1)(2,3)(4,5)(6,7)
+            const u32x4 w = xp.v[j];
+            u32x4 pr;
+            pr.x = __builtin_amdgcn_perm(w.z, w.x, 0x05040100u);  // (x0, x4)
+            pr.y = __builtin_amdgcn_perm(w.z, w.x, 0x07060302u);  // (x1, x5)
+            pr.z = __builtin_amdgcn_perm(w.w, w.y, 0x05040100u);  // (x2, x6)
+            pr.w = __builtin_amdgcn_perm(w.w, w.y, 0x07060302u);  // (x3, x7)
+            xl[(4 * k + g) * Gm::LPR + r] = pr;
         }
     }
+    // A wave's LDS operations execute in order, so the count is raised after its stores
+    // land; the fence keeps the compiler from reordering them.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane_id() == 0) __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    xp.staged = true;
 }
 
-template <int D>
-__device__ __forceinline__ void pair_x(XRegs<D>& xr) {
-#pragma unroll
-    for (int k = 0; k < GuGeom<D>::CPL; ++k) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            // halves 8g..8g+7 live in words 4g..4g+3 as (0,1)(2,3)(4,5)(6,7)
-            const uint32_t w0 = xr.v[k][4 * g + 0], w1 = xr.v[k][4 * g + 1];
-            const uint32_t w2 = xr.v[k][4 * g + 2], w3 = xr.v[k][4 * g + 3];
-            xr.v[k][4 * g + 0] = __builtin_amdgcn_perm(w2, w0, 0x05040100u);  // (x0, x4)
-            xr.v[k][4 * g + 1] = __builtin_amdgcn_perm(w2, w0, 0x07060302u);  // (x1, x5)
-            xr.v[k][4 * g + 2] = __builtin_amdgcn_perm(w3, w1, 0x05040100u);  // (x2, x6)
-            xr.v[k][4 * g + 3] = __builtin_amdgcn_perm(w3, w1, 0x07060302u);  // (x3, x7)
+// Waits until every wave of the workgroup has staged its part of x. Every wave stages its
+// part before it can wait for anything else, so this ends; the wall-clock bound only
+// guards against a broken invariant.
+__device__ __forceinline__ bool wait_x(const MlpArgs& a, uint32_t* slot, const uint32_t* count) {
+    if (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= (uint32_t)kWaves) return true;
+    Waiter wt(a.spin_limit);
+    while (__hip_atomic_load(count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < (uint32_t)kWaves) {
+        if (wt.expired()) {
+            if (lane_id() == 0) raise_status(a, slot, kStatusTimeout);
+            return false;
         }
+        __builtin_amdgcn_s_sleep(1);
     }
-}
-
-// x state of a wave: 0 not loaded, 1 loaded (raw), 2 paired.
-template <int D>
-__device__ __forceinline__ void need_x(const uint16_t* x, XRegs<D>& xr, int& state, int want) {
-    if (state == 0 && want >= 1) {
-        load_x<D>(x, xr);
-        state = 1;
-    }
-    if (state == 1 && want == 2) {
-        pair_x<D>(xr);
-        state = 2;
-    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return true;
 }
 
 template <int D>
@@ -325,39 +344,46 @@ __device__ __forceinline__ float group_sum(float x) {
 // neurons n0 .. n0 + nvalid - 1 into hrow, each word tagged with the launch sequence
 // (the word is its own ready flag).
 template <int D>
-__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const XRegs<D>& xr, uint64_t* hrow, int n0, int nvalid,
+__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, uint64_t* hrow, int n0, int nvalid,
                                            uint32_t seq) {
     using Gm = GuGeom<D>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+    float acc[Gm::RPL][2];
 #pragma unroll
-    for (int p = 0; p < Gm::RPL; ++p) {
-        float acc[2] = {0.f, 0.f};
+    for (int p = 0; p < Gm::RPL; ++p) acc[p][0] = acc[p][1] = 0.f;
 #pragma unroll
-        for (int proj = 0; proj < 2; ++proj) {
+    for (int k = 0; k < Gm::CPL; ++k) {
 #pragma unroll
-            for (int k = 0; k < Gm::CPL; ++k) {
-                const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
-                const h2 s2 = {sv, sv};
-                const u32x4 v = L.w[p][proj][k];
-                const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+        for (int g = 0; g < 4; ++g) {
+            const u32x4 xv = xl[(4 * k + g) * Gm::LPR + r];
+            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
+            for (int p = 0; p < Gm::RPL; ++p) {
+#pragma unroll
+                for (int proj = 0; proj < 2; ++proj) {
+                    const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
+                    const h2 s2 = {sv, sv};
+                    const u32x4 v = L.w[p][proj][k];
+                    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
                     h2 w[4];
                     dequant8(words[g], s2, w);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[proj] = dot2(w[q], as_h2(xr.v[k][4 * g + q]), acc[proj]);
+                    for (int q = 0; q < 4; ++q) acc[p][proj] = dot2(w[q], as_h2(xw[q]), acc[p][proj]);
                 }
             }
         }
-        acc[0] = group_sum<Gm::LPR>(acc[0]);
-        acc[1] = group_sum<Gm::LPR>(acc[1]);
+    }
+#pragma unroll
+    for (int p = 0; p < Gm::RPL; ++p) {
+        const float gsum = group_sum<Gm::LPR>(acc[p][0]);
+        const float usum = group_sum<Gm::LPR>(acc[p][1]);
         const int nu = p * Gm::NPW + sub;
         if (r == Gm::LPR - 1 && nu < nvalid) {
-            const float g = round_half(acc[0]);
-            const float u = round_half(acc[1]);
-            const float s = round_half(g / (1.0f + __expf(-g)));
-            const float h = round_half(s * u);
+            const float g = round_half(gsum);
+            const float u = round_half(usum);
+            const float sl = round_half(g / (1.0f + __expf(-g)));
+            const float h = round_half(sl * u);
             __hip_atomic_store(hrow + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -518,6 +544,7 @@ struct Shared {
     uint32_t word[8];
     uint32_t wpath[kWaves];
     uint32_t wfail[kWaves];
+    uint32_t xcount;   // waves that have staged their part of x
 };
 
 // The queue state of a launch as one wave learnt it (wave-uniform).
@@ -618,11 +645,60 @@ __device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t 
     return i < NG ? i / ipu : (i - NG) / T;
 }
 
-// Descriptor words of items k0 .. k0 + count - 1 of this wave (item i = wv + k NW) in
-// one round trip: lane 5 j + w holds word w of item k0 + j's unit. Queue positions are
-// read from the mirror once it has copied the first `need` of them.
-__device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t need, uint32_t wv,
-                                            uint32_t NW, uint32_t k0, uint32_t count, uint32_t NG, uint32_t ipu,
+// How the waves taking part share the items of a unit range: wave w of nw. With
+// gu_waves = 0 (mixed) every wave takes the list [gate/up items, down items] at w, w + nw,
+// ...: its gate/up items first, then its down items. Otherwise (split) waves
+// [0, gu_waves) take only gate/up items and the others only down items, so a wave that
+// publishes h never polls for h: its polls and atomics never queue behind its own h
+// stores, whose acknowledgement from memory is slow under a full load stream.
+struct WaveRole {
+    uint32_t w, nw, gu_waves;
+};
+
+// The items of one wave: gate/up items g0, g0 + gs, ... (KG of them), then down items
+// d0, d0 + ds, ... (K - KG); item(k) is the k-th one's index in the range's list
+// (gate/up items [0, NG), then down items).
+struct ItemList {
+    uint32_t NG, g0, gs, d0, ds, KG, K;
+    __device__ __forceinline__ uint32_t item(uint32_t k) const { return k < KG ? g0 + k * gs : NG + d0 + (k - KG) * ds; }
+};
+
+__device__ __forceinline__ uint32_t stride_count(uint32_t first, uint32_t n, uint32_t stride) {
+    return first < n ? (n - first + stride - 1) / stride : 0u;
+}
+
+__device__ __forceinline__ ItemList make_items(const WaveRole& r, uint32_t NG, uint32_t ND) {
+    ItemList l;
+    l.NG = NG;
+    if (r.gu_waves == 0) {
+        l.g0 = r.w;
+        l.gs = r.nw;
+        l.KG = stride_count(r.w, NG, r.nw);
+        l.d0 = r.w + l.KG * r.nw - NG;
+        l.ds = r.nw;
+        l.K = l.KG + stride_count(l.d0, ND, r.nw);
+    } else if (r.w < r.gu_waves) {
+        l.g0 = r.w;
+        l.gs = r.gu_waves;
+        l.KG = l.K = stride_count(r.w, NG, r.gu_waves);
+        l.d0 = 0;
+        l.ds = 1;
+    } else {
+        l.g0 = 0;
+        l.gs = 1;
+        l.KG = 0;
+        l.d0 = r.w - r.gu_waves;
+        l.ds = r.nw - r.gu_waves;
+        l.K = stride_count(l.d0, ND, l.ds);
+    }
+    return l;
+}
+
+// Descriptor words of items k0 .. k0 + count - 1 of this wave in one round trip: lane
+// 5 j + w holds word w of item k0 + j's unit. Queue positions are read from the mirror
+// once it has copied the first `need` of them.
+__device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t need,
+                                            const ItemList& il, uint32_t k0, uint32_t count, uint32_t ipu,
                                             uint32_t T, uint32_t& word) {
     if (need) {
         uint32_t ok = 1;
@@ -640,7 +716,7 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
     word = 0;
     if (lane < 5 * count) {
         const uint32_t j = lane / 5, w = lane - 5 * j;
-        const uint32_t g = u0 + item_unit(wv + (k0 + j) * NW, NG, ipu, T);
+        const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T);
         word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
                                 : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
@@ -672,48 +748,54 @@ struct ItemMeta {
     int n0, nvalid;
 };
 
-// This wave's items of units [u0, u1): wave wv of NW takes items wv, wv + NW, ...; the
-// next item's loads are issued before the current item is computed. Gate/up items never
+// This wave's items of units [u0, u1) (its share under `role`); the next item's loads
+// are issued before the current item is computed. Gate/up items never
 // wait for another wave; down items wait for their unit's h (after every gate/up item
 // of this wave), so every h is eventually published. With FUSED, the U-th contribution
 // of a column writes the output (U = core + queue units, learnt from the epoch word).
 template <int D, bool FUSED>
 __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
-                                              unsigned long long* yacc, XRegs<D>& xr, int& xstate, Epoch& ep,
-                                              uint32_t early, Pending& pd, uint32_t u0, uint32_t u1, uint32_t wv,
-                                              uint32_t NW) {
+                                              unsigned long long* yacc, XPart<D>& xp, u32x4* xl, Epoch& ep,
+                                              uint32_t early, Pending& pd, uint32_t u0, uint32_t u1,
+                                              const WaveRole& role) {
     using Gm = GuGeom<D>;
     constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
     const uint32_t nu = u1 - u0;
     const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per unit
-    const uint32_t NG = nu * ipu, N = NG + nu * T;
-    if (wv >= N) return true;
-    const uint32_t K = (N - wv + NW - 1) / NW;                   // items of this wave
-    const uint32_t KG = wv < NG ? (NG - wv + NW - 1) / NW : 0;   // the first KG are gate/up
+    const uint32_t NG = nu * ipu;
+    const ItemList il = make_items(role, NG, nu * T);
+    const uint32_t K = il.K, KG = il.KG;   // items of this wave; the first KG are gate/up
+    // Every exit stages this wave's part of x first (siblings may be waiting for it).
+    auto leave = [&](bool r) -> bool {
+        stage_xpart<D>(xp, xl, &sh.xcount);
+        return r;
+    };
+    if (!K) return leave(true);
     const uint32_t need = u1 > a.core_count ? u1 - a.core_count : 0;
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
     uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, need, wv, NW, 0, min(K, (uint32_t)kDescItems), NG, ipu, T, word)) return false;
-    if (KG) need_x<D>(a.x, xr, xstate, 1);
+    if (!fetch_descs(a, slot, u0, need, il, 0, min(K, (uint32_t)kDescItems), ipu, T, word)) return leave(false);
+    // x was loaded before the descriptors, so (in-order completion) it is here too
+    stage_xpart<D>(xp, xl, &sh.xcount);
     const int wave = wave_id();
     uint16_t* hs = sh.hs[wave];
     uint16_t* ss = sh.ss[wave];
-    GuItem<D> ga, gb;
-    DnItem dc_, dd_;
-    ItemMeta ma, mb, mc, md;
+    GuItem<D> gi;
+    DnItem di;
+    ItemMeta m;
     uint32_t U = 0;
     bool have_u = !FUSED;
 
-    // Gate/up items come first in every wave's list. Phase 1 walks them with two
-    // gate/up slots (A: even k, B: odd k); the first down item is issued into down slot
-    // C during the last gate/up computation. Phase 2 walks the down items with slots C
-    // and D. Slots are fixed at compile time (issue / compute take their objects).
+    // One item in flight per wave: the memory-level parallelism comes from the number of
+    // resident waves (three workgroups per CU), which keeps the registers per wave low
+    // and leaves the loads of every other wave to hide this one's compute. Gate/up items
+    // come first in every wave's list.
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, need, wv, NW, k0, min(K - k0, (uint32_t)kDescItems), NG, ipu, T, word))
+            if (!fetch_descs(a, slot, u0, need, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, word))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -721,7 +803,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     auto issue_gu = [&](uint32_t k, GuItem<D>& gi, ItemMeta& m) -> bool {
         Unit u;
         if (!fetch_unit(k, u)) return false;
-        const uint32_t i = wv + k * NW, rel = i / ipu;
+        const uint32_t i = il.item(k), rel = i / ipu;
         m.dest = u.dest;
         m.hrow = a.hbuf + (size_t)u.dest * G;
         m.n0 = (int)((i - rel * ipu) * Gm::NPI);
@@ -732,7 +814,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     auto issue_dn = [&](uint32_t k, DnItem& di, ItemMeta& m) -> bool {
         Unit u;
         if (!fetch_unit(k, u)) return false;
-        const uint32_t d = wv + k * NW - NG;
+        const uint32_t d = il.item(k) - NG;
         m.grp = u.grp;
         m.sc = u.sc;
         m.dest = u.dest;
@@ -744,15 +826,9 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         if (FUSED && !ep.known && lane_id() == 0) early = ld_agent(slot + kSyncEpoch);
         return true;
     };
-    // the item after k: gate/up into `gn`, or the first down item into slot C
-    auto issue_next = [&](uint32_t k, GuItem<D>& gn, ItemMeta& mn) -> bool {
-        if (k >= K) return true;
-        return k < KG ? issue_gu(k, gn, mn) : issue_dn(k, dc_, mc);
-    };
     auto compute_gu = [&](uint32_t k, const GuItem<D>& gi, const ItemMeta& m) {
         if (a.first_compute && m.n0 == 0 && lane_id() == 0) a.first_compute[m.dest] = now_ticks();
-        need_x<D>(a.x, xr, xstate, 2);
-        gu_compute<D>(gi, xr, m.hrow, m.n0, m.nvalid, a.seq);
+        gu_compute<D>(gi, xl, m.hrow, m.n0, m.nvalid, a.seq);
         if (k == 0) stamp(a, kStampFirstData);
     };
     auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
@@ -778,22 +854,14 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         return true;
     };
 
-    if (!issue_next(0, ga, ma)) return false;
-    for (uint32_t k = 0; k < KG; k += 2) {
-        if (!issue_next(k + 1, gb, mb)) return false;
-        compute_gu(k, ga, ma);
-        if (k + 1 < KG) {
-            if (!issue_next(k + 2, ga, ma)) return false;
-            compute_gu(k + 1, gb, mb);
-        }
+    for (uint32_t k = 0; k < KG; ++k) {
+        if (!issue_gu(k, gi, m)) return false;
+        if (k == 0 && !wait_x(a, slot, &sh.xcount)) return false;
+        compute_gu(k, gi, m);
     }
-    for (uint32_t k = KG; k < K; k += 2) {
-        if (k + 1 < K && !issue_dn(k + 1, dd_, md)) return false;
-        if (!compute_dn(k, dc_, mc)) return false;
-        if (k + 1 < K) {
-            if (k + 2 < K && !issue_dn(k + 2, dc_, mc)) return false;
-            if (!compute_dn(k + 1, dd_, md)) return false;
-        }
+    for (uint32_t k = KG; k < K; ++k) {
+        if (!issue_dn(k, di, m)) return false;
+        if (!compute_dn(k, di, m)) return false;
     }
     return true;
 }
@@ -940,59 +1008,72 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
     return __builtin_amdgcn_readfirstlane(sh.word[6]);
 }
 
-// Claim path (progressive publication): ready pairs claimed one at a time; the four
-// waves of the claiming workgroup walk the pair's items (gate/up first, then down).
-template <int D, bool FUSED>
-__device__ __forceinline__ void claim_loop(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
-                                           unsigned long long* yacc, XRegs<D>& xr, int& xstate, Epoch& ep,
-                                           Pending& pd, uint32_t total) {
-    bool ok = true;
-    for (;;) {
-        const uint32_t got = claim_pair(a, sh, slot, total, ok);
-        if (!got) return;
-        const uint32_t head = __builtin_amdgcn_readfirstlane(sh.word[5]);
-        ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, 0u, pd, a.core_count + head,
-                                     a.core_count + head + got, wave_id(), kWaves);
-    }
-}
-
-// One persistent worker workgroup of a launch: each of its waves walks its share of the
-// resident (core) units' items, then of the queue's (all-ready fast path); or the
-// workgroup runs the claim loop (progressive path).
+// One persistent worker workgroup of a launch. Its waves walk their share of the resident
+// (core) units' items, then either their share of the queue's (all-ready fast path) or,
+// claiming ready pairs one at a time, the claimed pairs' items, which the workgroup's
+// four waves share (progressive path). Every range goes through the one call of
+// process_items below, so the item loop exists once in the kernel's code (one copy per
+// range kind would triple the code and raise the register count).
 template <int D, bool FUSED, bool CORE, bool QUEUE>
-__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, uint32_t* slot) {
+__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
     const uint32_t wave = wave_id();
-    const uint32_t NW = W * kWaves, wv = blockIdx.x * kWaves + wave;
+    // Roles by workgroup: the first gu_wgs workgroups take the gate/up items, the others
+    // the down items (one workgroup alone takes both).
+    const uint32_t gu_wgs = kSplitRoles && W >= 2 ? (W + 1) / 2 : 0;
+    const WaveRole role{blockIdx.x * kWaves + wave, W * kWaves, gu_wgs * kWaves};
     unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
-    XRegs<D> xr;
-    int xstate = 0;
+    XPart<D> xp;
+    load_xpart<D>(a.x, xp);
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
     const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
     bool ok = true;
-    if (CORE && a.core_count)
-        ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, early, pd, 0, a.core_count, wv, NW);
-    stamp(a, kStampCoreDone);
-    if (QUEUE) {
-        ok = ok && await_epoch(a, slot, ep, early);
-        stamp(a, kStampEpoch);
-        // One decision for the whole workgroup (the claim path synchronises its waves).
-        if (lane_id() == 0) sh.wpath[wave] = ok && ep.total ? ep.path : 0u;
-        __syncthreads();
-        uint32_t path = sh.wpath[0];
-        for (int w = 1; w < kWaves; ++w)
-            if (sh.wpath[w] != path) path = 0;
-        path = __builtin_amdgcn_readfirstlane(path);
-        if (path == 2) {
-            ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, early, pd, a.core_count,
-                                         a.core_count + ep.total, wv, NW);
-        } else if (path == 1) {
-            claim_loop<D, FUSED>(a, sh, slot, b, yacc, xr, xstate, ep, pd, ep.total);
+    enum : uint32_t { kCore, kDecide, kClaim, kDone };
+    uint32_t stage = CORE ? kCore : kDecide;
+    for (;;) {
+        uint32_t u0 = 0, u1 = 0, e = early;
+        WaveRole r = role;
+        if (stage == kCore) {
+            u1 = a.core_count;
+            stage = kDecide;
+        } else if (stage == kDecide) {
+            stamp(a, kStampCoreDone);
+            if (!QUEUE) break;
+            ok = ok && await_epoch(a, slot, ep, early);
+            stamp(a, kStampEpoch);
+            // One decision for the whole workgroup (the claim path synchronises its waves).
+            if (lane_id() == 0) sh.wpath[wave] = ok && ep.total ? ep.path : 0u;
+            __syncthreads();
+            uint32_t path = sh.wpath[0];
+            for (int w = 1; w < kWaves; ++w)
+                if (sh.wpath[w] != path) path = 0;
+            path = __builtin_amdgcn_readfirstlane(path);
+            if (path == 2) {
+                u0 = a.core_count;
+                u1 = u0 + ep.total;
+                stage = kDone;
+            } else if (path == 1) {
+                stage = kClaim;
+                continue;
+            } else {
+                break;
+            }
+        } else if (stage == kClaim) {
+            const uint32_t got = claim_pair(a, sh, slot, ep.total, ok);
+            if (!got) break;
+            u0 = a.core_count + __builtin_amdgcn_readfirstlane(sh.word[5]);
+            u1 = u0 + got;
+            r = WaveRole{wave, kWaves, 0};
+            e = 0;
+        } else {
+            break;
         }
-        stamp(a, kStampQueueDone);
+        if (u1 > u0) ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
     }
+    stage_xpart<D>(xp, xl, &sh.xcount);
+    if (QUEUE) stamp(a, kStampQueueDone);
     check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
 }
 
@@ -1037,15 +1118,18 @@ __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { re
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void fused_layer_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
+    __shared__ u32x4 xl[XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    if (threadIdx.x == 0) sh.xcount = 0;
+    __syncthreads();
     if (blockIdx.x == gridDim.x - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
     } else {
         stamp(a, kStampEntry);
-        worker<D, true, true, true>(a, b, sh, slot);
+        worker<D, true, true, true>(a, b, sh, xl, slot);
         stamp(a, kStampExit);
     }
     finish_launch(a, slot);
@@ -1053,23 +1137,29 @@ __global__ __launch_bounds__(kThreads, 2) void fused_layer_kernel(MlpArgs a, Bou
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void stage_a_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
+    __shared__ u32x4 xl[XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    worker<D, false, true, false>(a, b, sh, slot);
+    if (threadIdx.x == 0) sh.xcount = 0;
+    __syncthreads();
+    worker<D, false, true, false>(a, b, sh, xl, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
 template <int D>
-__global__ __launch_bounds__(kThreads, 2) void stage_b_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
+    __shared__ u32x4 xl[XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    if (threadIdx.x == 0) sh.xcount = 0;
+    __syncthreads();
     if (blockIdx.x == gridDim.x - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         return;
     }
-    worker<D, false, false, true>(a, b, sh, slot);
+    worker<D, false, false, true>(a, b, sh, xl, slot);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
