@@ -188,8 +188,9 @@ int HipBackend::submit(void* ctx, uint32_t layer, const void* input, void* outpu
 bool HipBackend::complete(void* ctx, uint32_t layer) {
     auto& b = *static_cast<HipBackend*>(ctx);
     if (b.completed) return b.completed(b.lifecycle_context, layer);
-    // The last workgroup of a launch to finish stores its sequence (see finish_launch in
-    // the kernel source): wrap-aware comparison against the last enqueued launch.
+    // Each launch stores its sequence once every one of its workgroups is done (the
+    // fused launch's mirror workgroup, or the split sequence's last reduction block):
+    // wrap-aware comparison against the last enqueued launch.
     const Impl& p = *b.impl_;
     if (!p.last_seq) return true;
     const uint32_t done = __atomic_load_n(p.done, __ATOMIC_ACQUIRE);

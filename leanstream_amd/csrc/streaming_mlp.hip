@@ -1092,11 +1092,39 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
     for (uint32_t i = t; i < a.width; i += n) st_agent_u64(other_acc + i, 0ull);
 }
 
-// Completion proof of a launch (replaces a per-launch event): every workgroup counts
-// itself out once it has finished, in two levels to keep the count off one contended
-// word -- per group of workgroups blk % 8 (kSyncExitGroups), then the last of each
-// group in kSyncExit. The very last one stores the launch sequence into the
-// host-coherent completion word; all reads of the launch's weights are complete by then.
+// Completion proof of a fused launch (replaces a per-launch event). Every worker
+// workgroup counts itself out once its memory operations are complete, with a
+// non-returning atomic into the counter of its group (blk % 8, so no word takes more
+// than an eighth of the increments), and leaves at once. The mirror workgroup, after
+// mirroring the queue, polls the eight counters; when every worker is out it stores the
+// launch sequence into the host-coherent completion word. All reads of the launch's
+// weights and all writes of its outputs are complete by then.
+__device__ __forceinline__ void count_out(uint32_t* slot) {
+    __syncthreads();   // the barrier waits for the workgroup's outstanding stores and atomics
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_fetch_add(slot + kSyncExitGroups + (blockIdx.x % 8u) * kLine, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, uint32_t workers) {
+    const uint32_t lane = lane_id();
+    const uint32_t want = lane < 8u ? (workers + 7u - lane) / 8u : 0u;   // workers b < W with b % 8 == lane
+    Waiter wt(a.spin_limit);
+    for (;;) {
+        const uint32_t got = lane < 8u ? ld_agent(slot + kSyncExitGroups + lane * kLine) : 0u;
+        if (__all(got >= want)) break;
+        if (wt.expired()) {   // a worker cannot leave: report it, then complete anyway
+            if (lane == 0) raise_status(a, slot, kStatusTimeout);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    if (lane == 0) __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// Completion proof of the split launch sequence, at the end of its last kernel (the
+// reduction): every workgroup counts itself out in two levels -- per group blk % 8, then
+// the last of each group in kSyncExit -- and the very last one stores the sequence.
 __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) {
     __syncthreads();
     if (threadIdx.x != 0) return;
@@ -1107,7 +1135,6 @@ __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) 
         add_agent(slot + kSyncExit, 1u) == groups - 1)
         __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
-
 
 __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { return a.yacc + (a.seq & 1) * a.width; }
 
@@ -1127,12 +1154,13 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs
     if (blockIdx.x == gridDim.x - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
+        if (threadIdx.x < 64) await_workers(a, slot, gridDim.x - 1);
     } else {
         stamp(a, kStampEntry);
         worker<D, true, true, true>(a, b, sh, xl, slot);
         stamp(a, kStampExit);
+        count_out(slot);
     }
-    finish_launch(a, slot);
 }
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
