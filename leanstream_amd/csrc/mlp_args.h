@@ -42,7 +42,7 @@ constexpr long long kAccBias = 1ll << 39;
 constexpr unsigned long long kAccOne = 1ull << 52;
 constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
-constexpr uint32_t kDnCols = 128;  // columns of one down-projection item (one scale block)
+constexpr uint32_t kDnCols = 256;  // columns of one down-projection item (two scale blocks)
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 

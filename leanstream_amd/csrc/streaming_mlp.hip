@@ -10,10 +10,10 @@
 // G neurons each) are cut into wave-sized items of a few KB of weights:
 //   - gate/up items: NPI neurons of one unit (about 8 KB of weights); one 64-lane wave
 //     computes their gate and up rows and publishes h;
-//   - down items: one 128-column tile (one scale block) of one unit over all G rows.
+//   - down items: one 256-column tile (two scale blocks) of one unit over all G rows.
 // All gate/up items come first, then the down items (unit-major). Wave w of the
 // persistent grid takes items w, w + NW, w + 2 NW, ..., one in flight at a time; with
-// three workgroups per CU (12 waves) the whole layer is in flight at once at the
+// two workgroups per CU (8 waves) nearly the whole layer is in flight at once at the
 // Ministral-8B shape, and HBM delivers it front to back. A down item needs the h of its
 // unit, produced by items about one round earlier, so it is normally ready by the time
 // the down weights arrive. Waves of a workgroup never wait for each other on this path;
@@ -47,11 +47,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kWgPerCu = 3;          // resident workgroups per CU (register budget 168 per lane)
+constexpr int kWgPerCu = 2;          // resident workgroups per CU (register budget 256 per lane)
 constexpr int kDnRows = 64;          // rows of one down-item pass: 8 row groups x 8 rows
 constexpr int kDescItems = 12;       // item descriptors fetched per round trip (5 words each)
 constexpr bool kSplitRoles = false;  // all-ready path: gate/up and down items on different workgroups
-static_assert(kDnCols == 128, "a down item is one scale block wide");
+static_assert(kDnCols == 256, "a down item is two scale blocks wide");
 
 // ---------------------------------------------------------------------------------
 // memory helpers
@@ -391,14 +391,15 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, 
 }
 
 // ---------------------------------------------------------------------------------
-// Down items: one 128-column tile of one unit. A pass covers 64 rows: lane 8 g + dc
-// holds columns 16 dc .. 16 dc + 15 (one 8-byte load per row) of rows 8 g .. 8 g + 7,
-// plus the h and the down scale of row `lane` (for the LDS exchange).
+// Down items: one 256-column tile (two scale blocks) of one unit. A pass covers 64 rows:
+// lane 8 g + dc holds columns 32 dc .. 32 dc + 31 (one 16-byte load per row, so every
+// row is read as whole 128-byte lines) of rows 8 g .. 8 g + 7, plus the h and the two
+// down scales of row `lane` (for the LDS exchange).
 // ---------------------------------------------------------------------------------
 struct DnItem {
-    u32x2 w[8];
+    u32x4 w[8];
     uint64_t h;     // tagged h of row r0 + lane (tag == seq and value 0 beyond G)
-    uint32_t s;     // down scale of row r0 + lane for the tile's block (0 beyond G)
+    uint32_t s;     // down scales of row r0 + lane for the tile's two blocks (0 beyond G)
 };
 
 __device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
@@ -411,24 +412,25 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
     constexpr int BLOCKS = D / 128;
     constexpr int RB = 3 * D / 2;
     const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    // the tile's two scales of a row are adjacent fp16 (block 2 tile is even): one 32-bit load
     if (r0 + kDnRows <= G) {   // every row of the pass exists: no per-lane guard
         const uint8_t* base = uniform_ptr(grp + (size_t)r0 * RB + D + tile * (kDnCols / 2));
-        const uint32_t wo = (uint32_t)(8 * g) * RB + dc * 8;
+        const uint32_t wo = (uint32_t)(8 * g) * RB + dc * 16;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) it.w[j] = ld_stream8(base + wo + j * RB);
-        const uint16_t* srow = uniform_ptr(sc + (size_t)r0 * 3 * BLOCKS + 2 * BLOCKS + tile);
-        it.s = srow[(uint32_t)lane * 3 * BLOCKS];
+        for (int j = 0; j < 8; ++j) it.w[j] = ld_stream16(base + wo + j * RB);
+        const uint16_t* srow = uniform_ptr(sc + (size_t)r0 * 3 * BLOCKS + 2 * BLOCKS + 2 * tile);
+        it.s = *reinterpret_cast<const uint32_t*>(srow + (uint32_t)lane * 3 * BLOCKS);
         it.h = ld_agent_u64(uniform_ptr(hrow + r0) + lane);
         return;
     }
-    const uint8_t* base = grp + D + tile * (kDnCols / 2) + dc * 8;
+    const uint8_t* base = grp + D + tile * (kDnCols / 2) + dc * 16;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
         const int n = r0 + 8 * g + j;
-        it.w[j] = n < G ? ld_stream8(base + (size_t)n * RB) : u32x2{0, 0};
+        it.w[j] = n < G ? ld_stream16(base + (size_t)n * RB) : u32x4{0, 0, 0, 0};
     }
     const int n = r0 + lane;
-    it.s = n < G ? sc[(size_t)n * 3 * BLOCKS + 2 * BLOCKS + tile] : 0u;
+    it.s = n < G ? *reinterpret_cast<const uint32_t*>(sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile) : 0u;
     it.h = n < G ? ld_agent_u64(hrow + n) : (uint64_t)seq << 32;
 }
 
@@ -448,28 +450,29 @@ __device__ __forceinline__ bool dn_wait_h(const MlpArgs& a, uint32_t* slot, cons
     }
 }
 
-// Adds one pass into the lane's 16 column partials. The pass's h and scales go through
-// this wave's LDS rows (hs, ss: 64 halves each) so that a lane reads its 8 rows as one
-// 16-byte vector each. Rows (8g + 2p, 8g + 2p + 1) share a dot2: v_perm pairs their
-// nibbles column by column. Rows beyond G have zero weights, h and scales.
-__device__ __forceinline__ void dn_accumulate(const DnItem& it, uint16_t* hs, uint16_t* ss, float acc[16]) {
-    const int lane = lane_id(), g = lane >> 3;
+// Adds one pass into the lane's 32 column partials. The pass's h and scales go through
+// this wave's LDS rows (hs: 64 halves; ss: 64 halves per block) so that a lane reads its
+// 8 rows as one 16-byte vector each. Rows (8g + 2p, 8g + 2p + 1) share a dot2: v_perm
+// pairs their nibbles column by column. Rows beyond G have zero weights, h and scales.
+__device__ __forceinline__ void dn_accumulate(const DnItem& it, uint16_t* hs, uint16_t* ss, float acc[32]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
     hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
     ss[lane] = (uint16_t)it.s;
+    ss[kDnRows + lane] = (uint16_t)(it.s >> 16);
     // The wave's LDS operations execute in order: the stores above land before the
     // loads below. The fence only keeps the compiler from reordering them.
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
-    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + 8 * g);
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + kDnRows * (dc >> 2) + 8 * g);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        const u32x2 wa = it.w[2 * p], wb = it.w[2 * p + 1];
+        const u32x4 wa = it.w[2 * p], wb = it.w[2 * p + 1];
         const h2 hab = as_h2(hw[p]), sab = as_h2(sw[p]);
-        const uint32_t xa[2] = {wa.x, wa.y}, xb[2] = {wb.x, wb.y};
+        const uint32_t xa[4] = {wa.x, wa.y, wa.z, wa.w}, xb[4] = {wb.x, wb.y, wb.z, wb.w};
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
+        for (int q = 0; q < 4; ++q) {
             h2 w[4];
             dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
 #pragma unroll
@@ -492,23 +495,24 @@ __device__ __forceinline__ float swap_sum16(float x, float y) {
 
 // Sum over the 8 row groups (lanes 8 g + dc, same dc) in a fixed tree, without LDS.
 // v_permlane32_swap exchanges the upper half of one register with the lower half of
-// another, so (acc[c], acc[c+8]) summed after a swap leave column c (groups g, g + 4) in
-// lanes < 32 and column c + 8 in lanes >= 32; v_permlane16_swap does the same across
-// odd / even 16-lane rows; a row_ror:8 DPP add joins the two group parities. Returns
-// this lane's columns 16 dc + 2 g and 16 dc + 2 g + 1 of the tile.
-__device__ __forceinline__ void dn_reduce(const float acc[16], float& c0, float& c1) {
-    float s1[8], s2[4];
+// another, so (acc[c], acc[c+16]) summed after a swap leave column c (groups g, g + 4) in
+// lanes < 32 and column c + 16 in lanes >= 32; v_permlane16_swap does the same across
+// odd / even 16-lane rows with (c, c+8); a row_ror:8 DPP add joins the two group
+// parities. Returns this lane's columns 32 dc + 4 g + i (i < 4) of the tile.
+__device__ __forceinline__ void dn_reduce(const float acc[32], float out[4]) {
+    float s1[16], s2[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) s1[c] = swap_sum32(acc[c], acc[c + 8]);
+    for (int c = 0; c < 16; ++c) s1[c] = swap_sum32(acc[c], acc[c + 16]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) s2[c] = swap_sum16(s1[c], s1[c + 4]);
-    // lane (g, dc) now holds columns 4 (g >> 1) + c of the 16 at dc, over the groups
-    // of g's parity; lane ^ 8 holds the same columns over the other parity.
+    for (int c = 0; c < 8; ++c) s2[c] = swap_sum16(s1[c], s1[c + 8]);
+    // lane (g, dc) now holds 8 of the 32 columns over the groups of g's parity; lane ^ 8
+    // holds the same columns over the other parity.
     const bool odd = (lane_id() >> 3) & 1;
-    const float x0 = odd ? s2[2] : s2[0], x1 = odd ? s2[3] : s2[1];
-    const float y0 = odd ? s2[0] : s2[2], y1 = odd ? s2[1] : s2[3];
-    c0 = x0 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y0), 0x128, 0xF, 0xF, false));
-    c1 = x1 + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y1), 0x128, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x = odd ? s2[4 + i] : s2[i], y = odd ? s2[i] : s2[4 + i];
+        out[i] = x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x128, 0xF, 0xF, false));
+    }
 }
 
 // ---------------------------------------------------------------------------------
@@ -540,7 +544,8 @@ __device__ __forceinline__ Unit resolve(const MlpArgs& a, const Bounds& b, ExecD
 // ---------------------------------------------------------------------------------
 struct Shared {
     alignas(16) uint16_t hs[kWaves][kDnRows];
-    alignas(16) uint16_t ss[kWaves][kDnRows];
+    alignas(16) uint16_t ss[kWaves][2 * kDnRows];
+    alignas(16) float red[kWaves][kDnCols];   // a down item's column sums, re-dealt for the atomics
     uint32_t word[8];
     uint32_t wpath[kWaves];
     uint32_t wfail[kWaves];
@@ -603,28 +608,33 @@ __device__ __forceinline__ unsigned long long acc_term(const MlpArgs& a, uint32_
 // The accumulator words returned by a wave's last column additions, checked once the
 // next additions are issued (or at the end), so the wave does not wait for the atomics'
 // round trip: the contribution that completes a column (count U) writes the output.
+// Lane l's four columns are col + l + 64 i (i < 4): each atomic instruction covers 64
+// consecutive columns (four 128-byte lines).
 struct Pending {
-    unsigned long long v0, v1;
-    int col;   // first of the two columns; < 0: nothing pending
+    unsigned long long v[4];
+    int col;   // first column of the lane's four; < 0: nothing pending
 };
 
 __device__ __forceinline__ void check_pending(const MlpArgs& a, Pending& pd, uint32_t U) {
     if (pd.col >= 0 && U) {
-        if ((uint32_t)(pd.v0 >> 52) == U) write_output(a, pd.col, pd.v0, U);
-        if ((uint32_t)(pd.v1 >> 52) == U) write_output(a, pd.col + 1, pd.v1, U);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if ((uint32_t)(pd.v[i] >> 52) == U) write_output(a, pd.col + 64 * i, pd.v[i], U);
     }
     pd.col = -1;
 }
 
 __device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, int col,
-                                            float c0, float c1, uint32_t U, Pending& pd) {
-    const unsigned long long t0 = acc_term(a, slot, c0), t1 = acc_term(a, slot, c1);
-    const unsigned long long n0 = __hip_atomic_fetch_add(yacc + col, t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t0;
-    const unsigned long long n1 =
-        __hip_atomic_fetch_add(yacc + col + 1, t1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t1;
+                                            const float c[4], uint32_t U, Pending& pd) {
+    unsigned long long n[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned long long t = acc_term(a, slot, c[i]);
+        n[i] = __hip_atomic_fetch_add(yacc + col + 64 * i, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t;
+    }
     check_pending(a, pd, U);
-    pd.v0 = n0;
-    pd.v1 = n1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pd.v[i] = n[i];
     pd.col = col;
 }
 
@@ -789,8 +799,8 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     bool have_u = !FUSED;
 
     // One item in flight per wave: the memory-level parallelism comes from the number of
-    // resident waves (three workgroups per CU), which keeps the registers per wave low
-    // and leaves the loads of every other wave to hide this one's compute. Gate/up items
+    // resident waves, which keeps the registers per wave low and leaves the loads of every
+    // other wave to hide this one's compute. Gate/up items
     // come first in every wave's list.
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
@@ -837,18 +847,26 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
             U = a.core_count + ep.total;
             have_u = true;
         }
-        float acc[16];
+        float acc[32];
 #pragma unroll
-        for (int c = 0; c < 16; ++c) acc[c] = 0.f;
+        for (int c = 0; c < 32; ++c) acc[c] = 0.f;
         for (int r0 = 0; r0 < (int)G; r0 += kDnRows) {
             if (r0) dn_issue<D>(m.grp, m.sc, m.hrow, (int)G, (int)m.tile, r0, a.seq, di);
             if (!dn_wait_h(a, slot, m.hrow, (int)G, r0, di)) return false;
             dn_accumulate(di, hs, ss, acc);
         }
-        float c0, c1;
-        dn_reduce(acc, c0, c1);
+        float cs[4];
+        dn_reduce(acc, cs);
+        // re-deal through LDS: lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds
+        // columns l + 64 i
         const int lane = lane_id();
-        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + 16 * (lane & 7) + 2 * (lane >> 3), c0, c1, U, pd);
+        float* red = sh.red[wave];
+        *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs[i] = red[lane + 64 * i];
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + lane, cs, U, pd);
         if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
