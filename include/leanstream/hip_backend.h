@@ -41,7 +41,7 @@ inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexc
 struct HipLayerBuffers {
     uint32_t width = 0;            // d, multiple of 256 (256..8192)
     uint32_t group_size = 0;       // G neurons per group
-    uint32_t batch = 1;            // tokens per call (1 supported)
+    uint32_t batch = 1;            // tokens per call (1 .. 4)
     uint32_t slot_capacity = 0;    // destination rows (>= core + queue capacity)
     uint32_t cache_groups = 0;     // slots in the cache arena
     uint32_t staging_groups = 0;   // slots in the staging arena
@@ -50,7 +50,7 @@ struct HipLayerBuffers {
     const void* cache = nullptr;   // packed groups [cache_groups][G][3][d/2]
     const void* staging = nullptr; // packed groups [staging_groups][G][3][d/2]
     const void* scales = nullptr;  // fp16 [physical_groups*G][3][d/128]
-    void* hidden = nullptr;        // u64 [slot_capacity][G]: fp32 bits of h | launch sequence << 32
+    void* hidden = nullptr;        // u64 [slot_capacity][batch][G]: fp32 bits of h | launch sequence << 32
     void* partial = nullptr;       // reserved (the reduction accumulates in backend-owned fixed point)
     void* y32 = nullptr;           // optional fp32 [d] pre-rounding output
     uint32_t* executions = nullptr;     // optional per-destination execution counts

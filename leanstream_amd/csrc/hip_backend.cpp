@@ -57,7 +57,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (!b.width || b.width % 256 || !b.group_size || b.group_size > 256 || !b.slot_capacity || !b.physical_groups ||
         !b.scales || (b.cache_groups && !b.cache) || (b.staging_groups && !b.staging))
         return EINVAL;
-    if (b.batch != 1) return ENOTSUP;
+    if (!b.batch || b.batch > lsamd::kMaxBatch) return ENOTSUP;
     if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
     if (!lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
     p.buf = b;
@@ -67,7 +67,8 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess) e = hipMalloc(&p.qmirror, sizeof(uint32_t) * 5 * std::max<uint32_t>(1, b.queue_capacity));
     if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * b.batch);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
-    if (e == hipSuccess && !b.hidden) e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * b.group_size);
+    if (e == hipSuccess && !b.hidden)
+        e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * b.batch * b.group_size);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
@@ -81,7 +82,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
     if (e == hipSuccess)
         e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * b.batch, hbuf,
-                              b.slot_capacity * b.group_size, nullptr);
+                              b.slot_capacity * b.batch * b.group_size, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         p.release();
@@ -106,6 +107,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.yacc = p.yacc;
     a.status = p.status;
     a.width = b.width;
+    a.batch = b.batch;
     a.group_size = b.group_size;
     a.slices = b.width / lsamd::kDnCols;
     a.slot_words = p.slot_words;
@@ -152,7 +154,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     // before the sequence wraps) zeroes every tag, so no stored tag can match a later one.
     if (p.needs_clear || p.seq == UINT32_MAX) {
         e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * p.buf.batch, a.hbuf,
-                              p.buf.slot_capacity * p.buf.group_size, hs);
+                              p.buf.slot_capacity * p.buf.batch * p.buf.group_size, hs);
         if (e != hipSuccess) return static_cast<int>(e);
         p.needs_clear = false;
     }

@@ -43,6 +43,7 @@ constexpr unsigned long long kAccOne = 1ull << 52;
 constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
 constexpr uint32_t kDnCols = 256;  // columns of one down-projection item (two scale blocks)
+constexpr uint32_t kMaxBatch = 4;  // batch rows of one launch (x of every row is kept in LDS)
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
@@ -73,15 +74,15 @@ struct MlpArgs {
     QueueControl* control;        // host-coherent control block
     uint32_t capacity;
     // data
-    const uint16_t* x;            // fp16 [d]
+    const uint16_t* x;            // fp16 [batch][d]
     const uint8_t* cache;         // packed groups, slot-major
     const uint8_t* staging;
     const uint16_t* scales;       // fp16 [(physical*G + n)*3 + proj][d/128]
-    uint64_t* hbuf;               // [slot][G] h = fp16(silu(g)*u) as fp32 bits | launch seq << 32
+    uint64_t* hbuf;               // [slot][batch][G] h = fp16(silu(g)*u) as fp32 bits | launch seq << 32
     float* partial;               // unused by the fixed-point reduction (kept in the buffer block)
-    unsigned long long* yacc;     // [2][d] packed accumulators (see kAccOne), buffer (seq & 1) per launch
-    uint16_t* y;                  // fp16 [d]
-    float* y32;                   // optional fp32 [d] pre-rounding output
+    unsigned long long* yacc;     // [2][batch][d] packed accumulators (see kAccOne), buffer (seq & 1) per launch
+    uint16_t* y;                  // fp16 [batch][d]
+    float* y32;                   // optional fp32 [batch][d] pre-rounding output
     uint32_t* executions;         // optional per-destination execution counters
     uint64_t* first_compute;      // optional per-destination start stamps (100 MHz clock)
     uint32_t* sync;               // base of the two ring slots
@@ -100,6 +101,7 @@ struct MlpArgs {
     uint32_t epoch;
     uint32_t seq;                 // launch sequence number (selects the ring slot)
     uint32_t batch_mode;          // 1: wait for batch_epoch before consuming the queue
+    uint32_t batch;               // rows of x / y (1 .. kMaxBatch)
     uint64_t spin_limit;          // bounded waits, in 100 MHz ticks
 };
 

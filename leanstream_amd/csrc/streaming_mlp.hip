@@ -181,17 +181,21 @@ struct GuGeom {
     static_assert(D % 256 == 0 && CPR >= 8, "width must be a multiple of 256");
 };
 
-// x is shared by the workgroup through LDS, as (k, k+4) fp16 pairs to match dequant8,
-// in the order gu_compute reads it: block (k, g) of lane r (words 4g .. 4g+3 of its
-// chunk k, x columns 32 (r + LPR k) + 8g .. + 7) at xl[(4k + g) LPR + r], so a wave's 64
-// lanes read 1 KB of consecutive LDS per block. Each wave loads a quarter of x as raw
-// 16-byte pieces at its start (load_xpart) and writes it, paired, once it must have
-// arrived (stage_xpart: after the wave's first descriptors, loaded later, or when it
-// leaves); a wave about to compute gate/up waits until all four quarters are in.
+// x (every batch row) is shared by the workgroup through LDS, as (k, k+4) fp16 pairs to
+// match dequant8, in the order gu_compute reads it: block (k, g) of lane r (words
+// 4g .. 4g+3 of its chunk k, x columns 32 (r + LPR k) + 8g .. + 7) of row b at
+// xl[b N + (4k + g) LPR + r], so a wave's 64 lanes read 1 KB of consecutive LDS per block.
+// Each wave loads a quarter of row 0 as raw 16-byte pieces into registers at its start,
+// and every fourth 64-piece block of rows 1 .. batch-1 straight into LDS
+// (global_load_lds); once they must have landed (after the wave's first descriptors,
+// loaded later and completed in order, or when it leaves) it writes / pairs them in place
+// and counts itself in (stage_x); a wave about to compute gate/up waits until all four
+// waves are in.
 template <int D>
 struct XGeom {
-    static constexpr int N = D / 8;                               // 16-byte pieces of x
-    static constexpr int PER = (N + kThreads - 1) / kThreads;   // pieces per thread
+    static constexpr int N = D / 8;                               // 16-byte pieces of one row of x
+    static constexpr int PER = (N + kThreads - 1) / kThreads;   // row-0 pieces per thread
+    static constexpr int INSTR = (N + 63) / 64;                   // 64-piece blocks per row
 };
 
 template <int D>
@@ -200,34 +204,62 @@ struct XPart {
     bool staged;
 };
 
+// LDS position of piece `raw` of a row (and back).
 template <int D>
-__device__ __forceinline__ void load_xpart(const uint16_t* x, XPart<D>& xp) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(x);
-#pragma unroll
-    for (int j = 0; j < XGeom<D>::PER; ++j) {
-        const int i = threadIdx.x + j * kThreads;
-        xp.v[j] = i < XGeom<D>::N ? src[i] : u32x4{0, 0, 0, 0};
-    }
-    xp.staged = false;
+__device__ __forceinline__ uint32_t x_position(uint32_t raw) {
+    using Gm = GuGeom<D>;
+    const uint32_t c = raw >> 2, g = raw & 3, r = c % Gm::LPR, k = c / Gm::LPR;
+    return (4 * k + g) * Gm::LPR + r;
+}
+template <int D>
+__device__ __forceinline__ uint32_t x_raw(uint32_t pos) {
+    using Gm = GuGeom<D>;
+    const uint32_t blk = pos / Gm::LPR, r = pos % Gm::LPR, k = blk >> 2, g = blk & 3;
+    return 4 * (r + Gm::LPR * k) + g;
+}
+
+__device__ __forceinline__ u32x4 pair_halves(u32x4 w) {   // (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+    return u32x4{__builtin_amdgcn_perm(w.z, w.x, 0x05040100u), __builtin_amdgcn_perm(w.z, w.x, 0x07060302u),
+                 __builtin_amdgcn_perm(w.w, w.y, 0x05040100u), __builtin_amdgcn_perm(w.w, w.y, 0x07060302u)};
 }
 
 template <int D>
-__device__ __forceinline__ void stage_xpart(XPart<D>& xp, u32x4* xl, uint32_t* count) {
-    using Gm = GuGeom<D>;
+__device__ __forceinline__ void load_x(const uint16_t* x, uint32_t batch, XPart<D>& xp, u32x4* xl) {
+    using Xg = XGeom<D>;
+    const u32x4* src = reinterpret_cast<const u32x4*>(x);
+#pragma unroll
+    for (int j = 0; j < Xg::PER; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        xp.v[j] = i < Xg::N ? src[i] : u32x4{0, 0, 0, 0};
+    }
+    xp.staged = false;
+    const uint32_t lane = lane_id();
+    for (uint32_t j = wave_id(); j < (batch - 1) * Xg::INSTR; j += kWaves) {
+        const uint32_t row = 1 + j / Xg::INSTR, pos = (j % Xg::INSTR) * 64 + lane;
+        if (pos < (uint32_t)Xg::N) {
+            typedef __attribute__((address_space(3))) void* lds_ptr;
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + (size_t)row * Xg::N + x_raw<D>(pos)),
+                                             (lds_ptr)(xl + row * Xg::N + (pos - lane)), 16, 0, 0);
+        }
+    }
+}
+
+template <int D>
+__device__ __forceinline__ void stage_x(XPart<D>& xp, uint32_t batch, u32x4* xl, uint32_t* count) {
+    using Xg = XGeom<D>;
     if (xp.staged) return;
 #pragma unroll
-    for (int j = 0; j < XGeom<D>::PER; ++j) {
+    for (int j = 0; j < Xg::PER; ++j) {
         const int i = threadIdx.x + j * kThreads;
-        if (i < XGeom<D>::N) {
-            const int c = i >> 2, g = i & 3, r = c % Gm::LPR, k = c / Gm::LPR;
-            // halves 8g .. 8g+7 of chunk c arrive as (0,1)(2,3)(4,5)(6,7)
-            const u32x4 w = xp.v[j];
-            u32x4 pr;
-            pr.x = __builtin_amdgcn_perm(w.z, w.x, 0x05040100u);  // (x0, x4)
-            pr.y = __builtin_amdgcn_perm(w.z, w.x, 0x07060302u);  // (x1, x5)
-            pr.z = __builtin_amdgcn_perm(w.w, w.y, 0x05040100u);  // (x2, x6)
-            pr.w = __builtin_amdgcn_perm(w.w, w.y, 0x07060302u);  // (x3, x7)
-            xl[(4 * k + g) * Gm::LPR + r] = pr;
+        if (i < Xg::N) xl[x_position<D>(i)] = pair_halves(xp.v[j]);
+    }
+    if (batch > 1) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this wave's LDS loads of rows 1.. have landed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const uint32_t lane = lane_id();
+        for (uint32_t j = wave_id(); j < (batch - 1) * Xg::INSTR; j += kWaves) {
+            const uint32_t row = 1 + j / Xg::INSTR, pos = (j % Xg::INSTR) * 64 + lane;
+            if (pos < (uint32_t)Xg::N) xl[row * Xg::N + pos] = pair_halves(xl[row * Xg::N + pos]);
         }
     }
     // A wave's LDS operations execute in order, so the count is raised after its stores
@@ -345,7 +377,7 @@ __device__ __forceinline__ float group_sum(float x) {
 // (the word is its own ready flag).
 template <int D>
 __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, uint64_t* hrow, int n0, int nvalid,
-                                           uint32_t seq) {
+                                           uint32_t seq) {   // xl: this item's batch row
     using Gm = GuGeom<D>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
@@ -356,7 +388,7 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, 
     for (int k = 0; k < Gm::CPL; ++k) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const u32x4 xv = xl[(4 * k + g) * Gm::LPR + r];
+            const u32x4 xv = xl[(4 * k + g) * Gm::LPR + r];   // paired (stage_x)
             const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (int p = 0; p < Gm::RPL; ++p) {
@@ -649,8 +681,8 @@ __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot
 // Item walk of one wave over units [u0, u1).
 // ---------------------------------------------------------------------------------
 
-// Unit (relative to u0) of item i: gate/up items [0, NG), ipu per unit; then down items,
-// T per unit, unit-major.
+// Batch unit (relative to u0) of item i: gate/up items [0, NG), ipu per batch unit; then
+// down items, T per batch unit, unit-major. Batch unit v is row v % batch of unit v / batch.
 __device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T) {
     return i < NG ? i / ipu : (i - NG) / T;
 }
@@ -709,7 +741,7 @@ __device__ __forceinline__ ItemList make_items(const WaveRole& r, uint32_t NG, u
 // once it has copied the first `need` of them.
 __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t need,
                                             const ItemList& il, uint32_t k0, uint32_t count, uint32_t ipu,
-                                            uint32_t T, uint32_t& word) {
+                                            uint32_t T, uint32_t nb, uint32_t& word) {
     if (need) {
         uint32_t ok = 1;
         if (lane_id() == 0) {
@@ -726,7 +758,8 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
     word = 0;
     if (lane < 5 * count) {
         const uint32_t j = lane / 5, w = lane - 5 * j;
-        const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T);
+        const uint32_t v = item_unit(il.item(k0 + j), il.NG, ipu, T);
+        const uint32_t g = u0 + (nb == 1 ? v : v / nb);
         word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
                                 : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
@@ -754,7 +787,7 @@ struct ItemMeta {
     const uint8_t* grp;
     const uint16_t* sc;
     uint64_t* hrow;
-    uint32_t unit, dest, tile;
+    uint32_t unit, dest, tile, row;   // row: the batch row
     int n0, nvalid;
 };
 
@@ -771,14 +804,15 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     using Gm = GuGeom<D>;
     constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
-    const uint32_t nu = u1 - u0;
-    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per unit
+    const uint32_t nb = a.batch;
+    const uint32_t nu = (u1 - u0) * nb;                  // batch units: every unit once per batch row
+    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per batch unit
     const uint32_t NG = nu * ipu;
     const ItemList il = make_items(role, NG, nu * T);
     const uint32_t K = il.K, KG = il.KG;   // items of this wave; the first KG are gate/up
     // Every exit stages this wave's part of x first (siblings may be waiting for it).
     auto leave = [&](bool r) -> bool {
-        stage_xpart<D>(xp, xl, &sh.xcount);
+        stage_x<D>(xp, a.batch, xl, &sh.xcount);
         return r;
     };
     if (!K) return leave(true);
@@ -786,9 +820,9 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
     uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, need, il, 0, min(K, (uint32_t)kDescItems), ipu, T, word)) return leave(false);
-    // x was loaded before the descriptors, so (in-order completion) it is here too
-    stage_xpart<D>(xp, xl, &sh.xcount);
+    if (!fetch_descs(a, slot, u0, need, il, 0, min(K, (uint32_t)kDescItems), ipu, T, nb, word)) return leave(false);
+    // x was loaded before the descriptors, so (in-order completion) it is in too
+    stage_x<D>(xp, a.batch, xl, &sh.xcount);
     const int wave = wave_id();
     uint16_t* hs = sh.hs[wave];
     uint16_t* ss = sh.ss[wave];
@@ -805,7 +839,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, need, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, word))
+            if (!fetch_descs(a, slot, u0, need, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, nb, word))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -814,8 +848,9 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         Unit u;
         if (!fetch_unit(k, u)) return false;
         const uint32_t i = il.item(k), rel = i / ipu;
+        m.row = nb == 1 ? 0u : rel % nb;
         m.dest = u.dest;
-        m.hrow = a.hbuf + (size_t)u.dest * G;
+        m.hrow = a.hbuf + ((size_t)u.dest * nb + m.row) * G;
         m.n0 = (int)((i - rel * ipu) * Gm::NPI);
         m.nvalid = min(Gm::NPI, (int)G - m.n0);
         gu_issue<D>(u.grp, u.sc, m.n0, m.nvalid, gi);
@@ -824,13 +859,14 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     auto issue_dn = [&](uint32_t k, DnItem& di, ItemMeta& m) -> bool {
         Unit u;
         if (!fetch_unit(k, u)) return false;
-        const uint32_t d = il.item(k) - NG;
+        const uint32_t d = il.item(k) - NG, rel = d / T;
+        m.row = nb == 1 ? 0u : rel % nb;
         m.grp = u.grp;
         m.sc = u.sc;
         m.dest = u.dest;
-        m.hrow = a.hbuf + (size_t)u.dest * G;
-        m.unit = u0 + d / T;
-        m.tile = d % T;
+        m.hrow = a.hbuf + ((size_t)u.dest * nb + m.row) * G;
+        m.unit = u0 + (nb == 1 ? rel : rel / nb);
+        m.tile = d - rel * T;
         dn_issue<D>(u.grp, u.sc, m.hrow, (int)G, (int)m.tile, 0, a.seq, di);
         // a fresh look at the epoch word, in flight with the item (U is needed to finish it)
         if (FUSED && !ep.known && lane_id() == 0) early = ld_agent(slot + kSyncEpoch);
@@ -838,7 +874,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     };
     auto compute_gu = [&](uint32_t k, const GuItem<D>& gi, const ItemMeta& m) {
         if (a.first_compute && m.n0 == 0 && lane_id() == 0) a.first_compute[m.dest] = now_ticks();
-        gu_compute<D>(gi, xl, m.hrow, m.n0, m.nvalid, a.seq);
+        gu_compute<D>(gi, xl + m.row * XGeom<D>::N, m.hrow, m.n0, m.nvalid, a.seq);
         if (k == 0) stamp(a, kStampFirstData);
     };
     auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
@@ -866,8 +902,8 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
 #pragma unroll
         for (int i = 0; i < 4; ++i) cs[i] = red[lane + 64 * i];
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + lane, cs, U, pd);
-        if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
+        add_columns(a, slot, yacc, (int)(m.row * D + m.tile * kDnCols) + lane, cs, U, pd);
+        if (a.executions) count_execution(a, slot, m.unit, m.dest, T * nb);
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
     };
@@ -938,7 +974,7 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
     if (state != 1) return;
     if (total == 0 && a.core_count == 0) {
         // no rows at all: the reduction of nothing is zero
-        for (uint32_t c = lane; c < a.width; c += 64) {
+        for (uint32_t c = lane; c < a.width * a.batch; c += 64) {
             if (a.y32) a.y32[c] = 0.f;
             a.y[c] = 0;
         }
@@ -1040,9 +1076,9 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     // the down items (one workgroup alone takes both).
     const uint32_t gu_wgs = kSplitRoles && W >= 2 ? (W + 1) / 2 : 0;
     const WaveRole role{blockIdx.x * kWaves + wave, W * kWaves, gu_wgs * kWaves};
-    unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width;
+    unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width * a.batch;
     XPart<D> xp;
-    load_xpart<D>(a.x, xp);
+    load_x<D>(a.x, a.batch, xp, xl);
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
@@ -1090,7 +1126,7 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
         }
         if (u1 > u0) ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
     }
-    stage_xpart<D>(xp, xl, &sh.xcount);
+    stage_x<D>(xp, a.batch, xl, &sh.xcount);
     if (QUEUE) stamp(a, kStampQueueDone);
     check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
 }
@@ -1106,8 +1142,8 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
     const uint32_t t = threadIdx.x - 64, n = kThreads - 64;
     uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
     for (uint32_t i = t; i < a.slot_words; i += n) st_agent(other + i, 0u);
-    unsigned long long* other_acc = a.yacc + ((a.seq + 1) & 1) * a.width;
-    for (uint32_t i = t; i < a.width; i += n) st_agent_u64(other_acc + i, 0ull);
+    unsigned long long* other_acc = a.yacc + ((a.seq + 1) & 1) * a.width * a.batch;
+    for (uint32_t i = t; i < a.width * a.batch; i += n) st_agent_u64(other_acc + i, 0ull);
 }
 
 // Completion proof of a fused launch (replaces a per-launch event). Every worker
@@ -1154,7 +1190,9 @@ __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) 
         __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { return a.yacc + (a.seq & 1) * a.width; }
+__device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) {
+    return a.yacc + (a.seq & 1) * a.width * a.batch;
+}
 
 // ---------------------------------------------------------------------------------
 // Kernels. Persistent launches have gridDim.x = workers + 1; the last block mirrors.
@@ -1165,7 +1203,7 @@ __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) { re
 template <int D>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[XGeom<D>::N];
+    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1185,7 +1223,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs
 template <int D>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[XGeom<D>::N];
+    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1196,7 +1234,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, 
 template <int D>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[XGeom<D>::N];
+    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1293,7 +1331,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     e = hipLaunchKernel(v->stage_b, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
-    return hipLaunchKernel(v->reduce, dim3(p.width / kThreads), dim3(kThreads), rargs, 0, stream);
+    return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
 }
 
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,

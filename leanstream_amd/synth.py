@@ -117,6 +117,12 @@ CONFIGS = {
     "c2": LayerConfig("ministral8b_sparse_int4_mlp_d4096_f12288_a30_b1", 4096, 12288, 0.30, seed=0xC2),
     "c4": LayerConfig("llama70b_sparse_int4_mlp_d8192_f28672_a20_b1", 8192, 28672, 0.20, scale_lo=0.003,
                       scale_hi=0.015, seed=0xC4),
+    # batch 4: the same weights and active groups as the batch-1 entries (same seed); x
+    # row 0 is their x (the generator is counter-based)
+    "c4b4": LayerConfig("llama70b_sparse_int4_mlp_d8192_f28672_a20_b4", 8192, 28672, 0.20, batch=4,
+                        scale_lo=0.003, scale_hi=0.015, seed=0xC4),
+    "c1b4": LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25_b4", 1024, 4096, 0.25, batch=4,
+                        selection="permutation", seed=0xC1),
 }
 
 

@@ -53,8 +53,9 @@ class DeviceLayer:
         self.slot_capacity = max(1, k)
         self.y = torch.empty(cfg.batch * d, dtype=torch.float16, device=dev)
         self.y32 = torch.empty(cfg.batch * d, dtype=torch.float32, device=dev) if with_y32 else None
-        # h of each destination row: fp32 bits in the low word, launch sequence tag in the high word
-        self.hidden = torch.zeros(self.slot_capacity * G, dtype=torch.int64, device=dev)
+        # h of each destination row and batch row: fp32 bits in the low word, launch
+        # sequence tag in the high word ([slot][batch][G])
+        self.hidden = torch.zeros(self.slot_capacity * cfg.batch * G, dtype=torch.int64, device=dev)
         self.partial = torch.zeros(self.slot_capacity * d, dtype=torch.float32, device=dev)
         self.executions = torch.zeros(self.slot_capacity, dtype=torch.int32, device=dev) if diagnostics else None
         self.queue = ReadyQueue(queue_capacity if queue_capacity else max(1, k))
@@ -82,7 +83,8 @@ class DeviceLayer:
     def hidden_h(self):
         """h per destination row and neuron (fp32) from the tagged hidden buffer."""
         words = self.hidden.cpu().numpy().view(np.uint32).reshape(-1, 2)[:, 0]
-        return words.view(np.float32).reshape(self.slot_capacity, self.cfg.group_size)
+        h = words.view(np.float32).reshape(self.slot_capacity, self.cfg.batch, self.cfg.group_size)
+        return h[:, 0, :] if self.cfg.batch == 1 else h
 
     def host_copy(self):
         """Host (numpy) copies of copy 0: cache, scales, x."""
