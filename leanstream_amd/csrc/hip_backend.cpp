@@ -75,8 +75,8 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     int dev = 0;
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, &p.per_cu_fused);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, &p.per_cu_split);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, static_cast<int>(b.batch), &p.per_cu_fused);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(b.batch), &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
         e = hipErrorInvalidConfiguration;
     uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);

@@ -15,7 +15,7 @@ struct LaunchPlan {
 
 bool variant_available(int width);
 // Maximum co-resident workgroups per CU for the kernels of an entry point.
-hipError_t resident_workers(int width, int entry_point, int* per_cu);
+hipError_t resident_workers(int width, int entry_point, int batch, int* per_cu);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
 hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
 // Zeroes both ring slots, both accumulator buffers and the tagged h rows.

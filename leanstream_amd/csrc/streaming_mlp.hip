@@ -375,21 +375,34 @@ __device__ __forceinline__ float group_sum(float x) {
 // Finish a gate/up item: dot products, row reductions, activation. Publishes h of
 // neurons n0 .. n0 + nvalid - 1 into hrow, each word tagged with the launch sequence
 // (the word is its own ready flag).
-template <int D>
-__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, uint64_t* hrow, int n0, int nvalid,
-                                           uint32_t seq) {   // xl: this item's batch row
+// With NB > 1 the item's weights are dequantised once and multiplied with x of each of
+// the nb batch rows (xl: row 0; row b at xl + b N); h of row b goes to hrow + b G.
+template <int D, int NB>
+__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, uint64_t* hrow, uint32_t G, int n0,
+                                           int nvalid, uint32_t seq, uint32_t nb) {
     using Gm = GuGeom<D>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
-    float acc[Gm::RPL][2];
+    float acc[NB][Gm::RPL][2];
 #pragma unroll
-    for (int p = 0; p < Gm::RPL; ++p) acc[p][0] = acc[p][1] = 0.f;
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int p = 0; p < Gm::RPL; ++p) acc[b][p][0] = acc[b][p][1] = 0.f;
 #pragma unroll
     for (int k = 0; k < Gm::CPL; ++k) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const u32x4 xv = xl[(4 * k + g) * Gm::LPR + r];   // paired (stage_x)
-            const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+            uint32_t xw[NB][4];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                if (NB == 1 || (uint32_t)b < nb) {
+                    const u32x4 xv = xl[b * XGeom<D>::N + (4 * k + g) * Gm::LPR + r];   // paired (stage_x)
+                    xw[b][0] = xv.x;
+                    xw[b][1] = xv.y;
+                    xw[b][2] = xv.z;
+                    xw[b][3] = xv.w;
+                }
+            }
 #pragma unroll
             for (int p = 0; p < Gm::RPL; ++p) {
 #pragma unroll
@@ -401,23 +414,32 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, 
                     h2 w[4];
                     dequant8(words[g], s2, w);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) acc[p][proj] = dot2(w[q], as_h2(xw[q]), acc[p][proj]);
+                    for (int b = 0; b < NB; ++b) {
+                        if (NB == 1 || (uint32_t)b < nb) {
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) acc[b][p][proj] = dot2(w[q], as_h2(xw[b][q]), acc[b][p][proj]);
+                        }
+                    }
                 }
             }
         }
     }
 #pragma unroll
-    for (int p = 0; p < Gm::RPL; ++p) {
-        const float gsum = group_sum<Gm::LPR>(acc[p][0]);
-        const float usum = group_sum<Gm::LPR>(acc[p][1]);
-        const int nu = p * Gm::NPW + sub;
-        if (r == Gm::LPR - 1 && nu < nvalid) {
-            const float g = round_half(gsum);
-            const float u = round_half(usum);
-            const float sl = round_half(g / (1.0f + __expf(-g)));
-            const float h = round_half(sl * u);
-            __hip_atomic_store(hrow + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h), __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    for (int b = 0; b < NB; ++b) {
+        if (NB > 1 && (uint32_t)b >= nb) break;
+#pragma unroll
+        for (int p = 0; p < Gm::RPL; ++p) {
+            const float gsum = group_sum<Gm::LPR>(acc[b][p][0]);
+            const float usum = group_sum<Gm::LPR>(acc[b][p][1]);
+            const int nu = p * Gm::NPW + sub;
+            if (r == Gm::LPR - 1 && nu < nvalid) {
+                const float g = round_half(gsum);
+                const float u = round_half(usum);
+                const float sl = round_half(g / (1.0f + __expf(-g)));
+                const float h = round_half(sl * u);
+                __hip_atomic_store(hrow + b * G + n0 + nu, ((uint64_t)seq << 32) | __float_as_uint(h),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
 }
@@ -681,10 +703,12 @@ __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot
 // Item walk of one wave over units [u0, u1).
 // ---------------------------------------------------------------------------------
 
-// Batch unit (relative to u0) of item i: gate/up items [0, NG), ipu per batch unit; then
-// down items, T per batch unit, unit-major. Batch unit v is row v % batch of unit v / batch.
-__device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T) {
-    return i < NG ? i / ipu : (i - NG) / T;
+// Unit (relative to u0) of item i: gate/up items [0, NG), ipu per unit (each serves every
+// batch row); then down items, T per batch unit (unit u, row b is batch unit u nb + b).
+__device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T, uint32_t nb) {
+    if (i < NG) return i / ipu;
+    const uint32_t v = (i - NG) / T;
+    return nb == 1 ? v : v / nb;
 }
 
 // How the waves taking part share the items of a unit range: wave w of nw. With
@@ -758,8 +782,7 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
     word = 0;
     if (lane < 5 * count) {
         const uint32_t j = lane / 5, w = lane - 5 * j;
-        const uint32_t v = item_unit(il.item(k0 + j), il.NG, ipu, T);
-        const uint32_t g = u0 + (nb == 1 ? v : v / nb);
+        const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T, nb);
         word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
                                 : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
@@ -796,7 +819,7 @@ struct ItemMeta {
 // wait for another wave; down items wait for their unit's h (after every gate/up item
 // of this wave), so every h is eventually published. With FUSED, the U-th contribution
 // of a column writes the output (U = core + queue units, learnt from the epoch word).
-template <int D, bool FUSED>
+template <int D, bool FUSED, int NB>
 __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
                                               unsigned long long* yacc, XPart<D>& xp, u32x4* xl, Epoch& ep,
                                               uint32_t early, Pending& pd, uint32_t u0, uint32_t u1,
@@ -804,15 +827,15 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     using Gm = GuGeom<D>;
     constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
-    const uint32_t nb = a.batch;
-    const uint32_t nu = (u1 - u0) * nb;                  // batch units: every unit once per batch row
-    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per batch unit
+    const uint32_t nb = NB == 1 ? 1u : a.batch;
+    const uint32_t nu = u1 - u0;
+    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per unit (every batch row)
     const uint32_t NG = nu * ipu;
-    const ItemList il = make_items(role, NG, nu * T);
+    const ItemList il = make_items(role, NG, nu * nb * T);   // down items per batch unit
     const uint32_t K = il.K, KG = il.KG;   // items of this wave; the first KG are gate/up
     // Every exit stages this wave's part of x first (siblings may be waiting for it).
     auto leave = [&](bool r) -> bool {
-        stage_x<D>(xp, a.batch, xl, &sh.xcount);
+        stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
         return r;
     };
     if (!K) return leave(true);
@@ -822,7 +845,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     uint32_t word = 0, k0 = 0;
     if (!fetch_descs(a, slot, u0, need, il, 0, min(K, (uint32_t)kDescItems), ipu, T, nb, word)) return leave(false);
     // x was loaded before the descriptors, so (in-order completion) it is in too
-    stage_x<D>(xp, a.batch, xl, &sh.xcount);
+    stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     const int wave = wave_id();
     uint16_t* hs = sh.hs[wave];
     uint16_t* ss = sh.ss[wave];
@@ -848,9 +871,9 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         Unit u;
         if (!fetch_unit(k, u)) return false;
         const uint32_t i = il.item(k), rel = i / ipu;
-        m.row = nb == 1 ? 0u : rel % nb;
+        m.row = 0;
         m.dest = u.dest;
-        m.hrow = a.hbuf + ((size_t)u.dest * nb + m.row) * G;
+        m.hrow = a.hbuf + (size_t)u.dest * nb * G;   // row 0 of the destination's h rows
         m.n0 = (int)((i - rel * ipu) * Gm::NPI);
         m.nvalid = min(Gm::NPI, (int)G - m.n0);
         gu_issue<D>(u.grp, u.sc, m.n0, m.nvalid, gi);
@@ -874,7 +897,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     };
     auto compute_gu = [&](uint32_t k, const GuItem<D>& gi, const ItemMeta& m) {
         if (a.first_compute && m.n0 == 0 && lane_id() == 0) a.first_compute[m.dest] = now_ticks();
-        gu_compute<D>(gi, xl + m.row * XGeom<D>::N, m.hrow, m.n0, m.nvalid, a.seq);
+        gu_compute<D, NB>(gi, xl, m.hrow, G, m.n0, m.nvalid, a.seq, nb);
         if (k == 0) stamp(a, kStampFirstData);
     };
     auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
@@ -1068,7 +1091,7 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
 // four waves share (progressive path). Every range goes through the one call of
 // process_items below, so the item loop exists once in the kernel's code (one copy per
 // range kind would triple the code and raise the register count).
-template <int D, bool FUSED, bool CORE, bool QUEUE>
+template <int D, bool FUSED, bool CORE, bool QUEUE, int NB>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
     const uint32_t wave = wave_id();
@@ -1078,7 +1101,8 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     const WaveRole role{blockIdx.x * kWaves + wave, W * kWaves, gu_wgs * kWaves};
     unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width * a.batch;
     XPart<D> xp;
-    load_x<D>(a.x, a.batch, xp, xl);
+    const uint32_t xrows = NB == 1 ? 1u : a.batch;   // the NB = 1 kernels hold one row of x
+    load_x<D>(a.x, xrows, xp, xl);
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
@@ -1124,9 +1148,9 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
         } else {
             break;
         }
-        if (u1 > u0) ok = process_items<D, FUSED>(a, sh, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+        if (u1 > u0) ok = process_items<D, FUSED, NB>(a, sh, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
     }
-    stage_x<D>(xp, a.batch, xl, &sh.xcount);
+    stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     if (QUEUE) stamp(a, kStampQueueDone);
     check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
 }
@@ -1200,10 +1224,10 @@ __device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) {
 
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
-template <int D>
+template <int D, int NB>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
+    __shared__ u32x4 xl[NB * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1213,28 +1237,28 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs
         if (threadIdx.x < 64) await_workers(a, slot, gridDim.x - 1);
     } else {
         stamp(a, kStampEntry);
-        worker<D, true, true, true>(a, b, sh, xl, slot);
+        worker<D, true, true, true, NB>(a, b, sh, xl, slot);
         stamp(a, kStampExit);
         count_out(slot);
     }
 }
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
-template <int D>
+template <int D, int NB>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
+    __shared__ u32x4 xl[NB * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
-    worker<D, false, true, false>(a, b, sh, xl, slot);
+    worker<D, false, true, false, NB>(a, b, sh, xl, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
-template <int D>
+template <int D, int NB>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
-    __shared__ u32x4 xl[kMaxBatch * XGeom<D>::N];
+    __shared__ u32x4 xl[NB * XGeom<D>::N];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1243,7 +1267,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, 
         run_mirror(a, slot, pre);
         return;
     }
-    worker<D, false, false, true>(a, b, sh, xl, slot);
+    worker<D, false, false, true, NB>(a, b, sh, xl, slot);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
@@ -1276,16 +1300,20 @@ namespace {
 
 struct Variant {
     int width;
-    const void* fused;
-    const void* stage_a;
-    const void* stage_b;
+    const void* fused[2];     // [0] batch 1, [1] batch 2 .. kMaxBatch
+    const void* stage_a[2];
+    const void* stage_b[2];
     const void* reduce;
 };
 
 template <int D>
 Variant make_variant() {
-    return {D, reinterpret_cast<const void*>(&fused_layer_kernel<D>), reinterpret_cast<const void*>(&stage_a_kernel<D>),
-            reinterpret_cast<const void*>(&stage_b_kernel<D>), reinterpret_cast<const void*>(&reduce_kernel<D>)};
+    return {D,
+            {reinterpret_cast<const void*>(&fused_layer_kernel<D, 1>),
+             reinterpret_cast<const void*>(&fused_layer_kernel<D, kMaxBatch>)},
+            {reinterpret_cast<const void*>(&stage_a_kernel<D, 1>), reinterpret_cast<const void*>(&stage_a_kernel<D, kMaxBatch>)},
+            {reinterpret_cast<const void*>(&stage_b_kernel<D, 1>), reinterpret_cast<const void*>(&stage_b_kernel<D, kMaxBatch>)},
+            reinterpret_cast<const void*>(&reduce_kernel<D>)};
 }
 
 const Variant* find_variant(int width) {
@@ -1300,15 +1328,16 @@ const Variant* find_variant(int width) {
 
 bool variant_available(int width) { return find_variant(width) != nullptr; }
 
-hipError_t resident_workers(int width, int entry_point, int* per_cu) {
+hipError_t resident_workers(int width, int entry_point, int batch, int* per_cu) {
     const Variant* v = find_variant(width);
-    if (!v) return hipErrorInvalidValue;
-    const void* k = entry_point == kEntryFused ? v->fused : v->stage_b;
+    if (!v || batch < 1 || batch > (int)kMaxBatch) return hipErrorInvalidValue;
+    const int nb = batch > 1;
+    const void* k = entry_point == kEntryFused ? v->fused[nb] : v->stage_b[nb];
     int n = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kThreads, 0);
     if (e == hipSuccess && entry_point != kEntryFused) {
         int na = 0;
-        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&na, v->stage_a, kThreads, 0);
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&na, v->stage_a[nb], kThreads, 0);
         if (na < n) n = na;
     }
     *per_cu = n;
@@ -1320,15 +1349,17 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     if (!v || p.workers < 1) return hipErrorInvalidValue;
     MlpArgs a = args;
     Bounds b = bounds;
+    if (a.batch < 1 || a.batch > kMaxBatch) return hipErrorInvalidValue;
+    const int nb = a.batch > 1;
     void* kargs[] = {&a, &b};
     if (p.entry_point == kEntryFused)
-        return hipLaunchKernel(v->fused, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
+        return hipLaunchKernel(v->fused[nb], dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     hipError_t e = hipSuccess;
     if (a.core_count) {
-        e = hipLaunchKernel(v->stage_a, dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+        e = hipLaunchKernel(v->stage_a[nb], dim3(p.workers), dim3(kThreads), kargs, 0, stream);
         if (e != hipSuccess) return e;
     }
-    e = hipLaunchKernel(v->stage_b, dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
+    e = hipLaunchKernel(v->stage_b[nb], dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
     return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
