@@ -20,7 +20,12 @@ namespace leanstream::runtime {
 // (kAllResident asks for exactly that; the selector rejects 0 workers); every worker
 // takes a share of both the gate/up and the down-projection work; entry_point 0 = one
 // fused launch (core + ready queue + compact reduction), entry_point 1 = split launches
-// (stage A -> stage B -> reduction kernel).
+// (stage A -> stage B -> reduction kernel). group_batch selects how a launch consumes
+// positions published after it started: 0 = every wave takes its fixed stripe of the
+// queue's items and waits for each item's position to be published (a newly ready group
+// is computed by many waves at once); n > 0 = a workgroup claims up to n ready positions
+// at a time and its four waves compute them (the ready-pair claim of
+// backends/triton/persistent.py:77-86 for n = 2).
 inline constexpr uint32_t kAllResident = 1u << 16;
 inline constexpr KernelCandidate kHipCandidates[] = {
     {0, 256, "hip_fused_w256", 0, 0, 0, 0, 0},
@@ -28,8 +33,9 @@ inline constexpr KernelCandidate kHipCandidates[] = {
     {2, 1024, "hip_fused_w1024", 0, 0, 0, 0, 0},
     {3, 256, "hip_split_w256", 0, 0, 0, 0, 1},
     {4, kAllResident, "hip_split_resident", 0, 0, 0, 0, 1},
+    {5, kAllResident, "hip_fused_resident_pairs", 0, 0, 0, 2, 0},
 };
-inline constexpr uint32_t kHipCandidateCount = 5;
+inline constexpr uint32_t kHipCandidateCount = 6;
 inline constexpr KernelCandidate kHipDefault = kHipCandidates[1];
 inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexcept {
     return KernelSelector(offline_table, {kHipCandidates, kHipCandidateCount}, kHipDefault);

@@ -1,0 +1,52 @@
+// CopyEngines for HostStagingIO on MI355X (host -> device copies of packed groups).
+//
+// SdmaCopyEngine drives the SDMA copy engines directly through ROCr
+// (hsa_amd_memory_async_copy_on_engine, the routine hipMemcpyAsync itself ends in), one
+// completion signal per in-flight lane, lanes spread round robin over `engines` SDMA
+// engines. No HIP stream or hardware compute queue is involved, so a copy can never be
+// ordered behind the persistent consumer kernel that waits for it, and no copy ever needs
+// a compute unit.
+//
+// HipCopyEngine issues hipMemcpyAsync on `streams` side streams (default priority,
+// non-blocking with respect to the null stream), one event per lane. Streams share the
+// process's hardware queues (GPU_MAX_HW_QUEUES): a copy stream that shares one with the
+// stream running the consumer can leave copies queued behind that kernel until its
+// bounded waits expire, so keep streams + other streams of the process within that count.
+#pragma once
+#include "host_staging_io.h"
+
+namespace leanstream::runtime {
+
+class SdmaCopyEngine {
+public:
+    // `device` is the HIP device ordinal whose memory receives the copies; `lanes` >= the
+    // transport's qd; `engines` SDMA engines used round robin (1..16, clamped to the
+    // engines ROCr reports for host -> device). Throws std::runtime_error on failure.
+    SdmaCopyEngine(int device, uint32_t lanes, uint32_t engines);
+    ~SdmaCopyEngine();
+    SdmaCopyEngine(const SdmaCopyEngine&) = delete;
+    SdmaCopyEngine& operator=(const SdmaCopyEngine&) = delete;
+    CopyEngine view();
+    uint32_t engines() const;
+
+private:
+    struct Impl;
+    Impl* impl_ = nullptr;
+};
+
+class HipCopyEngine {
+public:
+    // `lanes` >= the transport's qd; `streams` copy streams used round robin (1..8).
+    // Throws std::runtime_error when a stream or event cannot be created.
+    HipCopyEngine(int device, uint32_t lanes, uint32_t streams);
+    ~HipCopyEngine();
+    HipCopyEngine(const HipCopyEngine&) = delete;
+    HipCopyEngine& operator=(const HipCopyEngine&) = delete;
+    CopyEngine view();
+
+private:
+    struct Impl;
+    Impl* impl_ = nullptr;
+};
+
+}  // namespace leanstream::runtime

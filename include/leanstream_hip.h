@@ -18,6 +18,11 @@
  *                                                  (backends/triton/mapped.cpp:9-30)
  *   ls_queue_*                                  <- ExecutionQueue (include/leanstream/execution_queue.h:19-34)
  *   ls_rank_groups                              <- top-k ranking of ls_predict (predictor/predictor_cpu.cpp:192-201)
+ *   ls_stream_create / _destroy / _run / _queue <- the end-to-end decode loop over Runtime / LayerStep
+ *                                                  (examples/end_to_end/main.cu:58-72) with the I/O
+ *                                                  transport replaced: HostStagingIO (pinned host store ->
+ *                                                  hipMemcpyAsync) instead of the O_DIRECT engine behind
+ *                                                  WeightManager (src/io/stream_io.h:45-65)
  *
  * Return values: 0 on success, a positive errno (EINVAL, ENOTSUP, ...) for rejected
  * arguments, or a positive hipError_t for a failed launch.
@@ -115,6 +120,57 @@ int ls_publisher_join(void* publisher);
 /* ---- group selection ---- */
 /* Top-k logical ids by (score descending, id ascending); -1 on non-finite scores. */
 int ls_rank_groups(const float* scores, uint32_t count, uint32_t k, int32_t* out);
+
+/* ---- streaming decode over host-staged layers ---- */
+/* Copy engines: SDMA engines driven directly (no HIP stream), or hipMemcpyAsync streams. */
+enum { LS_COPY_SDMA = 0, LS_COPY_HIP = 1 };
+/* Identical to leanstream::runtime::GroupLayout (file_offset = offset in the host store). */
+typedef struct ls_group_layout {
+    uint32_t logical_group, physical_group;
+    uint64_t file_offset;
+    uint32_t bytes, reserved;
+} ls_group_layout;
+
+typedef struct ls_stream_setup {
+    void* backend;            /* ls_hip_create handle, bound with staging = `staging` */
+    const void* host_store;   /* pinned host memory holding every layer's packed groups */
+    uint64_t host_bytes;
+    void* staging;            /* device arena: logical group g at g * staging_stride */
+    uint64_t staging_bytes;
+    uint64_t group_bytes, staging_stride;
+    uint32_t group_count;     /* logical groups per layer */
+    uint32_t layers;          /* Runtime layer contexts */
+    uint32_t qd;              /* copies in flight, 1..32 */
+    uint32_t copy_engine;     /* LS_COPY_SDMA or LS_COPY_HIP */
+    uint32_t copy_queues;     /* SDMA engines (1..16) or hipMemcpyAsync streams (1..8), round robin */
+    uint32_t mode;            /* LS_MODE_* */
+    int32_t device;
+} ls_stream_setup;
+
+typedef struct ls_stream_layer {
+    const ls_group_layout* layout; /* [group_count] */
+    const int32_t* rank;           /* update_prediction priority order */
+    uint32_t rank_count;
+    const int32_t* final_ids;      /* finalize order */
+    uint32_t final_count;
+    const uint64_t* arrival_ns;    /* optional [group_count]: earliest copy start after begin */
+    const void* input;             /* device fp16 x */
+    void* output;                  /* device fp16 y */
+} ls_stream_layer;
+
+/* NULL on invalid setup or allocation failure. */
+void* ls_stream_create(const ls_stream_setup* setup);
+void ls_stream_destroy(void* decoder);
+/* The decoder's ready queue (descriptors, publication order, control words). */
+int ls_stream_queue(void* decoder, ls_device_queue* out);
+/* Runs `count` layers in order on `stream` (Runtime layer id = (first_layer + i) % layers).
+ * times: optional [count][7] ns after the call's start: begin, after begin_layer, after
+ * update_prediction, after enqueue_compute, after finalize, completion observed, after
+ * commit. stamps: optional [count][group_count][3] ns after each layer's begin: admission,
+ * copy submission, copy completion. Stops at the first failing layer and returns its code
+ * (ETIMEDOUT when the kernel does not complete within timeout_ms). */
+int ls_stream_run(void* decoder, const ls_stream_layer* layers, uint32_t count, uint32_t first_layer, void* stream,
+                  uint64_t* times, uint64_t* stamps, int32_t timeout_ms);
 
 /* ---- synthetic workload generation on the device (counter-based splitmix64) ---- */
 int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream);

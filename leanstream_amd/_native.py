@@ -37,6 +37,28 @@ class LayerBuffers(C.Structure):
                 ("executions", p), ("first_compute", p), ("claim_log", p), ("stamps", p)]
 
 
+class GroupLayout(C.Structure):
+    """GroupLayout (include/leanstream/group_layout.h); file_offset = offset in the host store."""
+
+    _fields_ = [("logical_group", u32), ("physical_group", u32), ("file_offset", u64), ("bytes", u32),
+                ("reserved", u32)]
+
+
+class StreamSetup(C.Structure):
+    """ls_stream_setup (include/leanstream_hip.h)."""
+
+    _fields_ = [("backend", p), ("host_store", p), ("host_bytes", u64), ("staging", p), ("staging_bytes", u64),
+                ("group_bytes", u64), ("staging_stride", u64), ("group_count", u32), ("layers", u32), ("qd", u32),
+                ("copy_engine", u32), ("copy_queues", u32), ("mode", u32), ("device", i32)]
+
+
+class StreamLayer(C.Structure):
+    """ls_stream_layer (include/leanstream_hip.h)."""
+
+    _fields_ = [("layout", p), ("rank", p), ("rank_count", u32), ("final_ids", p), ("final_count", u32),
+                ("arrival_ns", p), ("input", p), ("output", p)]
+
+
 _SIGNATURES = [
     ("ls_hip_create", [], p),
     ("ls_hip_create_table", [p, u32, u32], p),
@@ -71,6 +93,10 @@ _SIGNATURES = [
     ("ls_publisher_start", [p, p, p, u32, u32, u32], p),
     ("ls_publisher_join", [p], C.c_int),
     ("ls_rank_groups", [p, u32, u32, p], C.c_int),
+    ("ls_stream_create", [p], p),
+    ("ls_stream_destroy", [p], None),
+    ("ls_stream_queue", [p, p], C.c_int),
+    ("ls_stream_run", [p, p, u32, u32, p, p, p, i32], C.c_int),
     ("ls_synth_bytes", [p, u64, u64, p], C.c_int),
     ("ls_synth_uniform_f16", [p, u64, u64, C.c_double, C.c_double, p], C.c_int),
     ("ls_synth_normal_f16", [p, u64, u64, p], C.c_int),

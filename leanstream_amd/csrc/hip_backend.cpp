@@ -147,6 +147,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     a.y = static_cast<uint16_t*>(output);
     a.epoch = epoch;
     a.batch_mode = mode == ConsumerMode::Progressive ? 0u : 1u;
+    a.claim_batch = c.group_batch;
     a.spin_limit = spin_limit_;
     auto hs = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;

@@ -101,6 +101,9 @@ struct MlpArgs {
     uint32_t epoch;
     uint32_t seq;                 // launch sequence number (selects the ring slot)
     uint32_t batch_mode;          // 1: wait for batch_epoch before consuming the queue
+    uint32_t claim_batch;         // progressive path: 0 = every wave takes its stripe of the queue
+                                  // positions, waiting for each to be published; n > 0 = workgroups
+                                  // claim up to n ready positions at a time
     uint32_t batch;               // rows of x / y (1 .. kMaxBatch)
     uint64_t spin_limit;          // bounded waits, in 100 MHz ticks
 };

@@ -761,22 +761,32 @@ __device__ __forceinline__ ItemList make_items(const WaveRole& r, uint32_t NG, u
 }
 
 // Descriptor words of items k0 .. k0 + count - 1 of this wave in one round trip: lane
-// 5 j + w holds word w of item k0 + j's unit. Queue positions are read from the mirror
-// once it has copied the first `need` of them.
-__device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t need,
+// 5 j + w holds word w of item k0 + j's unit. A queue position is read from the mirror
+// once the mirror has copied it: the wave waits until the mirrored ready count covers
+// the last position of the batch (`seen` is the count it last observed).
+__device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t& seen,
                                             const ItemList& il, uint32_t k0, uint32_t count, uint32_t ipu,
                                             uint32_t T, uint32_t nb, uint32_t& word) {
-    if (need) {
-        uint32_t ok = 1;
+    // units rise along each of the wave's two lists (gate/up, then down items), so the
+    // batch's last position is that of its last gate/up or its last down item
+    const uint32_t kl = k0 + count - 1;
+    uint32_t last = 0;
+    if (k0 < il.KG) last = item_unit(il.item(min(kl, il.KG - 1)), il.NG, ipu, T, nb);
+    if (kl >= il.KG) last = max(last, item_unit(il.item(kl), il.NG, ipu, T, nb));
+    const uint32_t g = u0 + last;
+    const uint32_t need = g >= a.core_count ? g - a.core_count + 1 : 0u;
+    if (need > seen) {
+        uint32_t ok = 1, ready = 0;
         if (lane_id() == 0) {
             Waiter wt(a.spin_limit);
-            while (ld_agent(slot + kSyncReady) < need) {
+            while ((ready = ld_agent(slot + kSyncReady)) < need) {
                 if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
                 if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
                 __builtin_amdgcn_s_sleep(1);
             }
         }
         if (!__builtin_amdgcn_readfirstlane(ok)) return false;
+        seen = __builtin_amdgcn_readfirstlane(ready);
     }
     const uint32_t lane = lane_id();
     word = 0;
@@ -839,11 +849,11 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         return r;
     };
     if (!K) return leave(true);
-    const uint32_t need = u1 > a.core_count ? u1 - a.core_count : 0;
+    uint32_t seen = 0;   // mirrored ready count this wave last observed
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
     uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, need, il, 0, min(K, (uint32_t)kDescItems), ipu, T, nb, word)) return leave(false);
+    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, nb, word)) return leave(false);
     // x was loaded before the descriptors, so (in-order completion) it is in too
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     const int wave = wave_id();
@@ -862,7 +872,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, need, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, nb, word))
+            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, nb, word))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -1046,8 +1056,8 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
     }
 }
 
-// Claim the next ready pair [head, min(head+2, ready)) (backends/triton/persistent.py:77-86),
-// against the mirrored ready count. Every wave of the workgroup takes part; `ok` is this
+// Claim the next ready positions [head, min(head + claim_batch, ready)) against the
+// mirrored ready count (claim_batch = 2: the ready pair of backends/triton/persistent.py:77-86). Every wave of the workgroup takes part; `ok` is this
 // wave's success so far. Returns the number of claimed positions (0 = leave, also when
 // any wave of the workgroup failed).
 __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total, bool ok) {
@@ -1064,7 +1074,7 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
             head = ld_agent(slot + kSyncClaimHead);
             if (head >= total) break;
             if (head < ready) {
-                const uint32_t end = min(head + 2u, min(ready, total));
+                const uint32_t end = min(head + a.claim_batch, min(ready, total));
                 uint32_t expected = head;
                 if (__hip_atomic_compare_exchange_strong(slot + kSyncClaimHead, &expected, end, __ATOMIC_RELAXED,
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
@@ -1086,9 +1096,10 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
 }
 
 // One persistent worker workgroup of a launch. Its waves walk their share of the resident
-// (core) units' items, then either their share of the queue's (all-ready fast path) or,
-// claiming ready pairs one at a time, the claimed pairs' items, which the workgroup's
-// four waves share (progressive path). Every range goes through the one call of
+// (core) units' items, then their share of the queue's (waiting for each position to be
+// published when the launch started before the queue was complete) or, with claim_batch
+// > 0 on the progressive path, the items of the ready positions the workgroup claims,
+// which its four waves share. Every range goes through the one call of
 // process_items below, so the item loop exists once in the kernel's code (one copy per
 // range kind would triple the code and raise the register count).
 template <int D, bool FUSED, bool CORE, bool QUEUE, int NB>
@@ -1128,7 +1139,10 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             for (int w = 1; w < kWaves; ++w)
                 if (sh.wpath[w] != path) path = 0;
             path = __builtin_amdgcn_readfirstlane(path);
-            if (path == 2) {
+            // All positions published before the launch (path 2), or published while it
+            // runs with striped consumption (path 1, claim_batch 0): every wave walks its
+            // stripe of the queue's items, waiting for each item's position as needed.
+            if (path == 2 || (path == 1 && a.claim_batch == 0)) {
                 u0 = a.core_count;
                 u1 = u0 + ep.total;
                 stage = kDone;

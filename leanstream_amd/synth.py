@@ -179,3 +179,51 @@ def descriptors(cfg, logical, source_kind=0, dest_base=0):
     out[:, 3] = dest_base + np.arange(len(logical))
     out[:, 4] = source_kind
     return out
+
+
+# ---------------------------------------------------------------- streaming decode step
+SEED_ARRIVAL = 6
+
+
+@dataclass(frozen=True)
+class StreamConfig:
+    """A decode step of `layers` sparse MLP layers of one shape whose active groups are
+    staged from pinned host memory. Layer l has its own weights, scales and N(0,1) group
+    scores (seed derived from `seed` and l); x is shared. In rank order, group i's bytes
+    reach the pinned store at the sum of i+1 exponential gaps of mean `arrival_mean_ns`."""
+
+    name: str
+    layer: LayerConfig
+    layers: int = 36
+    arrival_mean_ns: float = 5000.0
+    seed: int = 0xC3
+
+    def layer_config(self, l):
+        return LayerConfig(f"{self.layer.name}_l{l}", self.layer.width, self.layer.ffn, self.layer.active_frac,
+                           self.layer.group_size, self.layer.batch, self.layer.scale_lo, self.layer.scale_hi,
+                           "ranking", (self.seed * 1000003 + l) & 0xFFFFFFFFFFFFFFFF)
+
+    def x_config(self):
+        return self.layer_config(0)
+
+    def arrivals(self, l, rank):
+        """ns after the layer's begin at which each logical group may be copied (0 for
+        groups outside `rank`)."""
+        out = np.zeros(self.layer.groups, dtype=np.uint64)
+        if self.arrival_mean_ns <= 0:
+            return out
+        u = unit(self.layer_config(l).sub_seed(SEED_ARRIVAL), np.arange(len(rank), dtype=np.uint64))
+        gaps = -self.arrival_mean_ns * np.log1p(-u)
+        out[np.asarray(rank, dtype=np.int64)] = np.floor(np.cumsum(gaps) + 0.5).astype(np.uint64)
+        return out
+
+
+STREAMS = {
+    "c3": StreamConfig("streaming_decode_36x_sparse_int4_mlp_d1024_f4096_g64_a25_b1",
+                       LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25", 1024, 4096, 0.25)),
+}
+
+
+def stream_rank(sc, l):
+    """Active groups of layer l in rank order (top-k of its N(0,1) scores)."""
+    return active_groups(sc.layer_config(l))

@@ -135,3 +135,16 @@ def test_rank_groups_matches_oracle(seed):
     bad[3] = np.nan
     out = np.zeros(4, dtype=np.int32)
     assert lib.ls_rank_groups(bad.ctypes.data, len(bad), 4, out.ctypes.data) != 0
+
+
+def test_stream_create_rejects_invalid_setup():
+    """ls_stream_create validates its setup before touching the GPU."""
+    lib = _native.library()
+    assert not lib.ls_stream_create(None)
+    s = _native.StreamSetup()          # all zero: no backend, no store, no geometry
+    assert not lib.ls_stream_create(C.byref(s))
+    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 33, 0, 1, 1, 0)   # qd above 32
+    assert not lib.ls_stream_create(C.byref(s))
+    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 2, 1, 1, 0)    # unknown copy engine
+    assert not lib.ls_stream_create(C.byref(s))
+    assert lib.ls_stream_run(None, None, 0, 0, None, None, None, 1000) != 0
