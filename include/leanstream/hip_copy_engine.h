@@ -21,8 +21,10 @@ class SdmaCopyEngine {
 public:
     // `device` is the HIP device ordinal whose memory receives the copies; `lanes` >= the
     // transport's qd; `engines` SDMA engines used round robin (1..16, clamped to the
-    // engines ROCr reports for host -> device). Throws std::runtime_error on failure.
-    SdmaCopyEngine(int device, uint32_t lanes, uint32_t engines);
+    // engines ROCr reports for host -> device); `chunk_bytes` > 0 cuts a group into
+    // pieces of that size on successive engines (one engine moves a few GB/s, so pieces
+    // shorten a group's latency). Throws std::runtime_error on failure.
+    SdmaCopyEngine(int device, uint32_t lanes, uint32_t engines, uint64_t chunk_bytes = 0);
     ~SdmaCopyEngine();
     SdmaCopyEngine(const SdmaCopyEngine&) = delete;
     SdmaCopyEngine& operator=(const SdmaCopyEngine&) = delete;

@@ -143,6 +143,7 @@ typedef struct ls_stream_setup {
     uint32_t qd;              /* copies in flight, 1..32 */
     uint32_t copy_engine;     /* LS_COPY_SDMA or LS_COPY_HIP */
     uint32_t copy_queues;     /* SDMA engines (1..16) or hipMemcpyAsync streams (1..8), round robin */
+    uint32_t copy_chunk;      /* SDMA: bytes per copy piece (0 = one copy per group) */
     uint32_t mode;            /* LS_MODE_* */
     int32_t device;
 } ls_stream_setup;

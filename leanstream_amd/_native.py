@@ -49,7 +49,7 @@ class StreamSetup(C.Structure):
 
     _fields_ = [("backend", p), ("host_store", p), ("host_bytes", u64), ("staging", p), ("staging_bytes", u64),
                 ("group_bytes", u64), ("staging_stride", u64), ("group_count", u32), ("layers", u32), ("qd", u32),
-                ("copy_engine", u32), ("copy_queues", u32), ("mode", u32), ("device", i32)]
+                ("copy_engine", u32), ("copy_queues", u32), ("copy_chunk", u32), ("mode", u32), ("device", i32)]
 
 
 class StreamLayer(C.Structure):

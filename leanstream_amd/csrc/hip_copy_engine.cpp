@@ -14,6 +14,7 @@ struct SdmaCopyEngine::Impl {
     hsa_agent_t gpu{}, cpu{};
     std::vector<hsa_signal_t> signals;            // one per lane, 0 = copy complete
     std::vector<hsa_amd_sdma_engine_id_t> ids;    // engines used round robin
+    uint64_t chunk = 0;                           // bytes per SDMA copy (0 = one copy per group)
     uint32_t next = 0;
     bool hsa = false;
 
@@ -51,16 +52,29 @@ struct SdmaCopyEngine::Impl {
         if (hsa) hsa_shut_down();
     }
 
+    // A group is cut into pieces of `chunk` bytes on successive engines; every piece's
+    // completion decrements the lane's signal, which starts at the piece count.
     static int submit(void* c, uint32_t lane, void* dst, const void* src, uint64_t bytes) {
         Impl& m = *static_cast<Impl*>(c);
         if (lane >= m.signals.size()) return EINVAL;
-        hsa_signal_store_relaxed(m.signals[lane], 1);
-        const hsa_amd_sdma_engine_id_t id = m.ids[m.next++ % m.ids.size()];
-        const hsa_status_t st = hsa_amd_memory_async_copy_on_engine(dst, m.gpu, src, m.cpu, bytes, 0, nullptr,
-                                                                    m.signals[lane], id, false);
-        if (st != HSA_STATUS_SUCCESS) {
-            hsa_signal_store_relaxed(m.signals[lane], 0);
-            return EIO;
+        const uint64_t piece = m.chunk && m.chunk < bytes ? m.chunk : bytes;
+        const uint64_t pieces = (bytes + piece - 1) / piece;
+        const hsa_signal_t sig = m.signals[lane];
+        hsa_signal_store_relaxed(sig, static_cast<hsa_signal_value_t>(pieces));
+        for (uint64_t i = 0; i < pieces; ++i) {
+            const uint64_t off = i * piece, n = bytes - off < piece ? bytes - off : piece;
+            const hsa_amd_sdma_engine_id_t id = m.ids[m.next++ % m.ids.size()];
+            const hsa_status_t st =
+                hsa_amd_memory_async_copy_on_engine(static_cast<uint8_t*>(dst) + off, m.gpu,
+                                                    static_cast<const uint8_t*>(src) + off, m.cpu, n, 0, nullptr, sig,
+                                                    id, false);
+            if (st != HSA_STATUS_SUCCESS) {
+                // retire the pieces never issued, let the issued ones land, then fail
+                hsa_signal_subtract_relaxed(sig, static_cast<hsa_signal_value_t>(pieces - i));
+                while (hsa_signal_load_scacquire(sig) != 0) {
+                }
+                return EIO;
+            }
         }
         return 0;
     }
@@ -72,8 +86,10 @@ struct SdmaCopyEngine::Impl {
     }
 };
 
-SdmaCopyEngine::SdmaCopyEngine(int device, uint32_t lanes, uint32_t engines) : impl_(new Impl) {
+SdmaCopyEngine::SdmaCopyEngine(int device, uint32_t lanes, uint32_t engines, uint64_t chunk_bytes)
+    : impl_(new Impl) {
     Impl& m = *impl_;
+    m.chunk = chunk_bytes;
     auto fail = [&](const char* what) {
         delete impl_;
         impl_ = nullptr;

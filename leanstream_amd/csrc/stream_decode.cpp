@@ -81,7 +81,7 @@ struct StreamDecoder {
         cache_slots.assign(n, -1);
         StagingConfig sc;
         if (s.copy_engine == LS_COPY_SDMA) {
-            sdma.reset(new SdmaCopyEngine(s.device, s.qd, s.copy_queues));
+            sdma.reset(new SdmaCopyEngine(s.device, s.qd, s.copy_queues, s.copy_chunk));
             sc.engine = sdma->view();
         } else {
             copies.reset(new HipCopyEngine(s.device, s.qd, s.copy_queues));

@@ -956,8 +956,10 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
 // ---------------------------------------------------------------------------------
 // Queue protocol (LeanStream kernels/streaming_mlp.cu:47-79, backends/triton/persistent.py:32-92):
 // wait for the layer epoch (or an error), optionally for batch publication, decide once
-// per launch between the all-ready fast path and the claim path, then consume published
-// positions in order.
+// per launch between the all-ready fast path and the progressive path (positions
+// published while the launch runs), then consume published positions in order: on the
+// progressive path every wave waits for the positions of its own stripe of items, or
+// (claim_batch > 0) workgroups claim ready positions.
 //
 // On MI355X the queue lives in host memory behind PCIe, where concurrent reads from
 // hundreds of workgroups are served one after another. So exactly one workgroup of
@@ -1132,7 +1134,7 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             if (!QUEUE) break;
             ok = ok && await_epoch(a, slot, ep, early);
             stamp(a, kStampEpoch);
-            // One decision for the whole workgroup (the claim path synchronises its waves).
+            // One decision for the whole workgroup (claiming synchronises its waves).
             if (lane_id() == 0) sh.wpath[wave] = ok && ep.total ? ep.path : 0u;
             __syncthreads();
             uint32_t path = sh.wpath[0];

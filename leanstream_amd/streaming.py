@@ -3,8 +3,8 @@
 Every layer's packed groups live in one pinned host store (layer l, physical group p
 at byte (l * groups + p) * group_bytes, the file offset of its GroupLayout). Per layer,
 the native loop drives Runtime / LayerStep / WeightManager with HostStagingIO: the
-ranked groups are copied into the device staging arena with hipMemcpyAsync as they
-arrive, and each completion publishes READY to the persistent consumer that was
+ranked groups are copied into the device staging arena as they arrive (SDMA engines
+driven directly, or hipMemcpyAsync on side streams), and each completion publishes READY to the persistent consumer that was
 pre-enqueued for the layer. Scales of every layer stay in HBM (physical row
 l * groups + p); x is shared by the layers, each layer writes its own y row.
 """
@@ -26,8 +26,8 @@ def _check(rc, what):
 
 
 class StreamingDecode:
-    def __init__(self, sc, layers=None, qd=24, copy_engine=COPY_SDMA, copy_queues=8, mode=MODE_PROGRESSIVE,
-                 arrivals=True):
+    def __init__(self, sc, layers=None, qd=24, copy_engine=COPY_SDMA, copy_queues=8, copy_chunk=0,
+                 mode=MODE_PROGRESSIVE, arrivals=True):
         import torch
 
         self.torch = torch
@@ -96,7 +96,7 @@ class StreamingDecode:
             e.input = self.x.data_ptr()
             e.output = self.y.data_ptr() + l * cfg.batch * d * 2
         self.setup = StreamSetup(self.backend.context, self.host.data_ptr(), self.host.numel(), self.staging.data_ptr(),
-                                 self.staging.numel(), gb, gb, n, L, qd, copy_engine, copy_queues, mode,
+                                 self.staging.numel(), gb, gb, n, L, qd, copy_engine, copy_queues, copy_chunk, mode,
                                  torch.cuda.current_device())
         torch.cuda.synchronize()
         self.handle = lib.ls_stream_create(C.byref(self.setup))

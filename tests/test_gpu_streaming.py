@@ -111,18 +111,24 @@ def test_streamed_layer_bit_identical_to_resident_layer(torch_gpu):
 
 
 def test_streamed_layers_without_arrival_delay(torch_gpu):
-    """Copies issued as soon as admitted, through hipMemcpyAsync instead of direct SDMA:
-    same outputs as with delays."""
+    """Copies issued as soon as admitted, through hipMemcpyAsync instead of direct SDMA,
+    or cut into pieces over 16 SDMA engines: same outputs as with delays."""
     torch = torch_gpu
     sc = synth.STREAMS["c3"]
-    log(f"case: streamed decode {sc.name} layers=3 no arrival delay, hipMemcpyAsync on 1 stream, qd 4")
+    log(f"case: streamed decode {sc.name} layers=3 no arrival delay: hipMemcpyAsync on 1 stream with qd 4; "
+        f"24 KB SDMA pieces on 16 engines")
     a = StreamingDecode(sc, layers=3)
     b = StreamingDecode(sc, layers=3, arrivals=False, qd=4, copy_engine=COPY_HIP, copy_queues=1)
+    c = StreamingDecode(sc, layers=3, arrivals=False, copy_queues=16, copy_chunk=24576)   # 4 pieces per group
     try:
         a.run()
         b.run()
+        c.run()
         torch.cuda.synchronize()
-        assert np.array_equal(a.y.cpu().numpy().view(np.uint16), b.y.cpu().numpy().view(np.uint16))
+        want = a.y.cpu().numpy().view(np.uint16)
+        assert np.array_equal(want, b.y.cpu().numpy().view(np.uint16))
+        assert np.array_equal(want, c.y.cpu().numpy().view(np.uint16))
     finally:
         a.close()
         b.close()
+        c.close()

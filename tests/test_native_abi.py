@@ -143,8 +143,8 @@ def test_stream_create_rejects_invalid_setup():
     assert not lib.ls_stream_create(None)
     s = _native.StreamSetup()          # all zero: no backend, no store, no geometry
     assert not lib.ls_stream_create(C.byref(s))
-    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 33, 0, 1, 1, 0)   # qd above 32
+    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 33, 0, 1, 0, 1, 0)   # qd above 32
     assert not lib.ls_stream_create(C.byref(s))
-    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 2, 1, 1, 0)    # unknown copy engine
+    s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 2, 1, 0, 1, 0)    # unknown copy engine
     assert not lib.ls_stream_create(C.byref(s))
     assert lib.ls_stream_run(None, None, 0, 0, None, None, None, 1000) != 0
