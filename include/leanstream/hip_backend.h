@@ -47,7 +47,8 @@ inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexc
 struct HipLayerBuffers {
     uint32_t width = 0;            // d, multiple of 256 (256..8192)
     uint32_t group_size = 0;       // G neurons per group
-    uint32_t batch = 1;            // tokens per call (1 .. 4)
+    uint32_t batch = 1;            // tokens per call: 1 .. 4, or 5 .. 32 for the dense matrix-core path
+                                   // (group_size 64, core descriptors only, x bf16 [batch][d])
     uint32_t slot_capacity = 0;    // destination rows (>= core + queue capacity)
     uint32_t cache_groups = 0;     // slots in the cache arena
     uint32_t staging_groups = 0;   // slots in the staging arena

@@ -177,6 +177,7 @@ int ls_stream_run(void* decoder, const ls_stream_layer* layers, uint32_t count, 
 int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream);
 int ls_synth_uniform_f16(void* dst, uint64_t count, uint64_t seed, double lo, double hi, void* stream);
 int ls_synth_normal_f16(void* dst, uint64_t count, uint64_t seed, void* stream);
+int ls_synth_normal_bf16(void* dst, uint64_t count, uint64_t seed, void* stream);
 
 #ifdef __cplusplus
 }

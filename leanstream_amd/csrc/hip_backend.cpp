@@ -22,6 +22,9 @@ struct HipBackend::Impl {
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
     void* owned_partial = nullptr;
+    uint16_t* h16 = nullptr;     // dense path: fp16 h rows
+    float* dpart = nullptr;      // dense path: down-projection partial rows
+    bool dense = false;          // batch > kMaxBatch: every launch takes the matrix-core path
     uint32_t* done = nullptr;    // host-coherent: sequence of the last finished launch
     uint32_t last_seq = 0;       // sequence of the last enqueued launch (0: none)
     bool needs_clear = true;
@@ -35,12 +38,16 @@ struct HipBackend::Impl {
         if (yacc) (void)hipFree(yacc);
         if (owned_hidden) (void)hipFree(owned_hidden);
         if (owned_partial) (void)hipFree(owned_partial);
+        if (h16) (void)hipFree(h16);
+        if (dpart) (void)hipFree(dpart);
         if (status) (void)hipHostFree(status);
         if (done) (void)hipHostFree(done);
         sync = nullptr;
         qmirror = nullptr;
         yacc = nullptr;
         owned_hidden = owned_partial = nullptr;
+        h16 = nullptr;
+        dpart = nullptr;
         status = nullptr;
         done = nullptr;
         bound = false;
@@ -57,32 +64,41 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (!b.width || b.width % 256 || !b.group_size || b.group_size > 256 || !b.slot_capacity || !b.physical_groups ||
         !b.scales || (b.cache_groups && !b.cache) || (b.staging_groups && !b.staging))
         return EINVAL;
-    if (!b.batch || b.batch > lsamd::kMaxBatch) return ENOTSUP;
+    if (!b.batch || b.batch > lsamd::kMaxDenseBatch) return ENOTSUP;
+    // batch > kMaxBatch: the dense matrix-core path (64-neuron groups, core units only)
+    const bool dense = b.batch > lsamd::kMaxBatch;
+    if (dense && b.group_size != 64) return ENOTSUP;
     if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
     if (!lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
     p.buf = b;
+    p.dense = dense;
+    const uint32_t rows = dense ? 1u : b.batch;   // the batch-1..4 kernels' h rows and accumulators
     const uint32_t units_cap = b.slot_capacity + b.queue_capacity;
     p.slot_words = lsamd::sync_slot_words(units_cap);
     hipError_t e = hipMalloc(&p.sync, sizeof(uint32_t) * 2 * p.slot_words);
     if (e == hipSuccess) e = hipMalloc(&p.qmirror, sizeof(uint32_t) * 5 * std::max<uint32_t>(1, b.queue_capacity));
-    if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * b.batch);
+    if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * rows);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
     if (e == hipSuccess && !b.hidden)
-        e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * b.batch * b.group_size);
+        e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * rows * b.group_size);
+    if (e == hipSuccess && dense)
+        e = hipMalloc(&p.h16, sizeof(uint16_t) * 32 * b.slot_capacity * b.group_size);
+    if (e == hipSuccess && dense)
+        e = hipMalloc(&p.dpart, sizeof(float) * lsamd::kDenseSplits * 32 * b.width);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
     int dev = 0;
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, static_cast<int>(b.batch), &p.per_cu_fused);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(b.batch), &p.per_cu_split);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, static_cast<int>(rows), &p.per_cu_fused);
+    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(rows), &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
         e = hipErrorInvalidConfiguration;
     uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
     if (e == hipSuccess)
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * b.batch, hbuf,
-                              b.slot_capacity * b.batch * b.group_size, nullptr);
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * rows, hbuf,
+                              b.slot_capacity * rows * b.group_size, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         p.release();
@@ -113,6 +129,9 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.slot_words = p.slot_words;
     a.units_cap = units_cap;
     a.slot_capacity = b.slot_capacity;
+    a.h16 = p.h16;
+    a.dpart = p.dpart;
+    a.dsplits = dense ? lsamd::kDenseSplits : 0u;
     p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
     slices_ = b.width / lsamd::kDnCols;
     max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused) - 1;
@@ -153,9 +172,10 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     hipError_t e = hipSuccess;
     // h words are tagged with the launch sequence. A clear (after a failed launch, and
     // before the sequence wraps) zeroes every tag, so no stored tag can match a later one.
+    const uint32_t rows = p.dense ? 1u : p.buf.batch;
     if (p.needs_clear || p.seq == UINT32_MAX) {
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * p.buf.batch, a.hbuf,
-                              p.buf.slot_capacity * p.buf.batch * p.buf.group_size, hs);
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * rows, a.hbuf,
+                              p.buf.slot_capacity * rows * p.buf.group_size, hs);
         if (e != hipSuccess) return static_cast<int>(e);
         p.needs_clear = false;
     }
@@ -165,7 +185,9 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     a.seq = p.seq;
     a.done = p.done;
     const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(workers), entry};
-    e = lsamd::launch_layer(plan, a, p.bounds, hs);
+    // Batch 5..32: the dense matrix-core path computes the core units (the queue is not
+    // consumed: a dense layer's groups are all resident).
+    e = p.dense ? lsamd::launch_dense(a, p.bounds, hs) : lsamd::launch_layer(plan, a, p.bounds, hs);
     last_candidate_ = static_cast<int>(c.id);
     if (e != hipSuccess) {
         p.needs_clear = true;  // a partial launch may have left a ring slot dirty

@@ -44,6 +44,8 @@ constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
 constexpr uint32_t kDnCols = 256;  // columns of one down-projection item (two scale blocks)
 constexpr uint32_t kMaxBatch = 4;  // batch rows of one launch (x of every row is kept in LDS)
+constexpr uint32_t kMaxDenseBatch = 32;   // batch rows of the dense (matrix-core) path
+constexpr uint32_t kDenseSplits = 16;     // unit splits of its down projection
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
@@ -104,7 +106,11 @@ struct MlpArgs {
     uint32_t claim_batch;         // progressive path: 0 = every wave takes its stripe of the queue
                                   // positions, waiting for each to be published; n > 0 = workgroups
                                   // claim up to n ready positions at a time
-    uint32_t batch;               // rows of x / y (1 .. kMaxBatch)
+    uint32_t batch;               // rows of x / y (1 .. kMaxBatch; dense path: kMaxBatch + 1 .. kMaxDenseBatch)
+    // dense path (batch > kMaxBatch): x is bf16 [batch][d]
+    uint16_t* h16;                // fp16 h rows [32][slot_capacity * G]
+    float* dpart;                 // fp32 down-projection partial rows [dsplits][32][d]
+    uint32_t dsplits;
     uint64_t spin_limit;          // bounded waits, in 100 MHz ticks
 };
 

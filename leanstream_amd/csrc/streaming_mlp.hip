@@ -1310,6 +1310,192 @@ __global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long 
 }
 
 // ---------------------------------------------------------------------------------
+// Dense batched path (batch 5 .. 32, every group a resident core unit): matrix cores.
+//
+// Per batch row the arithmetic is the batch-1 path's: w = fp16(q * scale) exactly, fp32
+// sums of exact products, fp16 roundings of g, u, silu and h, fp32 sum of h * w_down.
+// The products run on v_mfma_f32_32x32x16_f16: the dequantised weights and h are fp16
+// values by definition, and bf16 x converts to fp16 exactly (8 significant bits; only
+// |x| < 2^-17 rounds, by less than 2^-25), so every product is exact in fp32 and only the
+// summation order differs. The 32 MFMA rows are the batch rows (rows >= batch are zero).
+//
+// MFMA fragment layout (v_mfma_f32_32x32x16_f16, checked on gfx950): lane l holds
+// A[row l % 32][k 8 (l / 32) + i] and B[k 8 (l / 32) + i][col l % 32], i < 8; result
+// element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]. Which k a slot stands for is
+// free as long as A and B agree, so each lane feeds the MFMA from its own contiguous loads.
+//
+// Three launches: gate/up (h rows in fp16), down projection (fp32 partial rows per split
+// of the units), reduction (fixed split order, then the completion word).
+// ---------------------------------------------------------------------------------
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kDenseCols = 128;    // down-projection columns per workgroup (32 per wave)
+constexpr int kDensePitch = 72;    // fp16 per LDS row: 64 neurons + 8 (rows stay 16-byte aligned)
+
+__device__ __forceinline__ _Float16 bf16_to_f16(uint32_t bits) {
+    return (_Float16)__builtin_bit_cast(float, bits << 16);
+}
+
+__device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Gate/up of one 32-neuron half of one unit for all batch rows. Wave w reduces the
+// quarter [w D/4, (w+1) D/4) of the input; the four partial tiles meet in LDS. Lane l
+// (neuron 32 half + l % 32, row l % 32 of x) loads 32 consecutive columns per step:
+// 16 bytes of each weight row and 64 bytes of x.
+__global__ __launch_bounds__(kThreads) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
+    __shared__ float red[kWaves][2][16][64];
+    const uint32_t D = a.width, G = a.group_size;
+    const uint32_t unit = blockIdx.x >> 1, half = blockIdx.x & 1;
+    if (blockIdx.x == 0) {   // the next launch's ring slot (this one's was cleared before it)
+        uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
+        for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
+    }
+    const Unit u = resolve(a, b, a.core[unit], (int)D);
+    const int lane = lane_id();
+    const uint32_t w = wave_id();
+    const uint32_t n = half * 32 + (lane & 31), hh = lane >> 5, row = lane & 31;
+    f32x16 cg = {}, cu = {};
+    if (u.ok) {
+        const uint8_t* wg = u.grp + (size_t)(n * 3) * (D / 2);
+        const uint8_t* wu = wg + D / 2;
+        const uint16_t* sg = u.sc + (size_t)(n * 3) * (D / 128);
+        const uint16_t* su = sg + D / 128;
+        const uint16_t* xr = a.x + (size_t)row * D;
+        const bool xok = row < a.batch;
+        const uint32_t kq = D / kWaves;
+        for (uint32_t t = 0; t < kq / 64; ++t) {
+            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+            const u32x4 qg = ld_stream16(wg + k0 / 2), qu = ld_stream16(wu + k0 / 2);
+            const uint16_t sgb = sg[k0 / 128], sub = su[k0 / 128];
+            u32x4 xv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                xv[q] = xok ? *reinterpret_cast<const u32x4*>(xr + k0 + 8 * q) : u32x4{0u, 0u, 0u, 0u};
+            const h2 sg2 = {half_bits(sgb), half_bits(sgb)}, su2 = {half_bits(sub), half_bits(sub)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                h2 wgv[4], wuv[4];
+                dequant8(qg[j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
+                dequant8(qu[j], su2, wuv);
+                h8 xa, bg, bu;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {   // slot 2 i = column i, slot 2 i + 1 = column i + 4
+                    xa[2 * i] = bf16_to_f16((xv[j][i >> 1] >> (16 * (i & 1))) & 0xffffu);
+                    xa[2 * i + 1] = bf16_to_f16((xv[j][(i + 4) >> 1] >> (16 * (i & 1))) & 0xffffu);
+                    bg[2 * i] = wgv[i].x;
+                    bg[2 * i + 1] = wgv[i].y;
+                    bu[2 * i] = wuv[i].x;
+                    bu[2 * i + 1] = wuv[i].y;
+                }
+                cg = mfma32(xa, bg, cg);
+                cu = mfma32(xa, bu, cu);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        red[w][0][i][lane] = cg[i];
+        red[w][1][i][lane] = cu[i];
+    }
+    __syncthreads();
+    const uint32_t hstride = a.slot_capacity * G;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t e = threadIdx.x + kThreads * r, i = e >> 6, l = e & 63;
+        float gsum = 0.f, usum = 0.f;
+#pragma unroll
+        for (int v = 0; v < kWaves; ++v) {   // fixed order: deterministic
+            gsum += red[v][0][i][l];
+            usum += red[v][1][i][l];
+        }
+        const uint32_t tk = 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        if (u.ok && tk < a.batch) {
+            const float g = round_half(gsum);
+            const float up = round_half(usum);
+            const float sl = round_half(g / (1.0f + __expf(-g)));
+            a.h16[(size_t)tk * hstride + u.dest * G + half * 32 + (l & 31)] =
+                __builtin_bit_cast(uint16_t, (_Float16)(sl * up));
+        }
+    }
+    if (threadIdx.x == 0) {
+        if (!u.ok) {
+            __hip_atomic_fetch_or(a.status, kStatusBadDescriptor, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else if (half == 0 && a.executions) {
+            __hip_atomic_fetch_add(a.executions + u.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
+// Down projection of 128 columns over one split of the units. Per unit the workgroup
+// dequantises the 64 x 128 weight tile into LDS transposed (column-major, so a lane's
+// eight k slots are eight neurons of its column: one 16-byte LDS read) and stages the
+// unit's h rows; wave w then runs four MFMAs for columns 32 w .. 32 w + 31.
+__global__ __launch_bounds__(kThreads) void dense_down_kernel(MlpArgs a, Bounds b) {
+    __shared__ alignas(16) _Float16 wl[kDenseCols][kDensePitch];
+    __shared__ alignas(16) _Float16 hl[32][kDensePitch];
+    const uint32_t D = a.width, G = a.group_size;
+    const uint32_t tiles = D / kDenseCols;
+    const uint32_t ct = blockIdx.x % tiles, split = blockIdx.x / tiles;
+    const uint32_t c0 = ct * kDenseCols;
+    const uint32_t per = (a.core_count + a.dsplits - 1) / a.dsplits;
+    const uint32_t u0 = split * per, u1 = min(a.core_count, u0 + per);
+    const uint32_t t = threadIdx.x;
+    const int lane = lane_id();
+    const uint32_t w = wave_id();
+    const uint32_t nn = t >> 2, cc = t & 3;   // weight tile: neuron, 32-column chunk
+    const uint32_t hr = t >> 3, hp = t & 7;   // h tile: batch row, 8-neuron part
+    const uint32_t hstride = a.slot_capacity * G;
+    f32x16 acc = {};
+    for (uint32_t un = u0; un < u1; ++un) {
+        const Unit u = resolve(a, b, a.core[un], (int)D);
+        if (!u.ok) continue;   // uniform across the workgroup; reported by the gate/up kernel
+        const u32x4 q = ld_stream16(u.grp + (size_t)(nn * 3 + 2) * (D / 2) + (c0 + 32 * cc) / 2);
+        const uint16_t sb = u.sc[(size_t)(nn * 3 + 2) * (D / 128) + c0 / 128];
+        const u32x4 hv = hr < a.batch ? *reinterpret_cast<const u32x4*>(a.h16 + (size_t)hr * hstride + u.dest * G + 8 * hp)
+                                      : u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();   // the previous unit's tiles are read
+        const h2 s2 = {half_bits(sb), half_bits(sb)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h2 wv[4];
+            dequant8(q[j], s2, wv);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wl[32 * cc + 8 * j + i][nn] = wv[i].x;
+                wl[32 * cc + 8 * j + i + 4][nn] = wv[i].y;
+            }
+        }
+        *reinterpret_cast<u32x4*>(&hl[hr][8 * hp]) = hv;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const h8 ha = *reinterpret_cast<const h8*>(&hl[lane & 31][16 * j + 8 * (lane >> 5)]);
+            const h8 wb = *reinterpret_cast<const h8*>(&wl[32 * w + (lane & 31)][16 * j + 8 * (lane >> 5)]);
+            acc = mfma32(ha, wb, acc);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t tk = 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+        if (tk < a.batch) a.dpart[((size_t)split * 32 + tk) * D + c0 + 32 * w + (lane & 31)] = acc[i];
+    }
+}
+
+// Sum of the splits in a fixed order, fp16 rounding, completion word.
+__global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * D + column
+    const uint32_t tk = idx / a.width, col = idx - tk * a.width;
+    float v = 0.f;
+    for (uint32_t s = 0; s < a.dsplits; ++s) v += a.dpart[((size_t)s * 32 + tk) * a.width + col];
+    if (a.y32) a.y32[idx] = v;
+    a.y[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
+    finish_launch(a, a.sync + (a.seq & 1) * a.slot_words);
+}
+
+// ---------------------------------------------------------------------------------
 // Host-side launch dispatch over the compiled (width, neurons-per-item) variants.
 // ---------------------------------------------------------------------------------
 namespace {
@@ -1379,6 +1565,29 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
     return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
+}
+
+hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t stream) {
+    MlpArgs a = args;
+    Bounds b = bounds;
+    if (a.group_size != 64 || a.width % 256 || a.batch <= kMaxBatch || a.batch > kMaxDenseBatch || !a.dsplits ||
+        !a.h16 || !a.dpart)
+        return hipErrorInvalidValue;
+    void* kargs[] = {&a, &b};
+    hipError_t e = hipSuccess;
+    if (a.core_count) {
+        e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_gate_up_kernel), dim3(2 * a.core_count),
+                            dim3(kThreads), kargs, 0, stream);
+        if (e == hipSuccess)
+            e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_down_kernel),
+                                dim3(a.width / kDenseCols * a.dsplits), dim3(kThreads), kargs, 0, stream);
+    } else {
+        a.dsplits = 0;   // nothing to sum: y = 0
+    }
+    if (e != hipSuccess) return e;
+    void* rargs[] = {&a};
+    return hipLaunchKernel(reinterpret_cast<const void*>(&dense_reduce_kernel), dim3(a.batch * a.width / kThreads),
+                           dim3(kThreads), rargs, 0, stream);
 }
 
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,

@@ -5,7 +5,7 @@
 // on (seed, i), so a host mirror (leanstream_amd/synth.py) produces the same bytes.
 //   bytes:    little-endian bytes of value(seed, i) for word i (uniform INT4 nibbles)
 //   uniform:  lo + (hi - lo) * u, u = (value >> 11) * 2^-53, rounded double -> fp16 (RNE)
-//   normal:   Irwin-Hall: sum of 12 uniforms (sequential double adds) - 6 -> fp16 (RNE)
+//   normal:   Irwin-Hall: sum of 12 uniforms (sequential double adds) - 6 -> fp16 or bf16 (RNE)
 // The double -> fp16 rounding is done in integer arithmetic (no double rounding).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -67,6 +67,35 @@ __global__ void synth_uniform_kernel(uint16_t* dst, uint64_t count, uint64_t see
         dst[i] = f64_to_f16_bits(lo + (hi - lo) * stream_unit(seed, i));
 }
 
+// Round-to-nearest-even conversion of a double to bfloat16 bits (finite, normal range:
+// the generator's values are in [-6, 6]; zero maps to +0).
+__host__ __device__ inline uint16_t f64_to_bf16_bits(double d) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, d);
+    const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
+    const int exp = (int)((b >> 52) & 0x7ff);
+    if (exp == 0) return sign;
+    const uint64_t mant = b & 0xFFFFFFFFFFFFFull;
+    int e = exp - 1023 + 127;
+    uint32_t m = (uint32_t)(mant >> 45);
+    const uint64_t rem = mant & ((1ull << 45) - 1), half = 1ull << 44;
+    if (rem > half || (rem == half && (m & 1u))) ++m;
+    if (m == 128u) {
+        m = 0;
+        ++e;
+    }
+    if (e >= 255) return sign | 0x7f80u;
+    if (e <= 0) return sign;
+    return sign | (uint16_t)(e << 7) | (uint16_t)m;
+}
+
+__global__ void synth_normal_bf16_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
+        double acc = 0.0;
+        for (int k = 0; k < 12; ++k) acc += stream_unit(seed, 12 * i + k);
+        dst[i] = f64_to_bf16_bits(acc - 6.0);
+    }
+}
+
 __global__ void synth_normal_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
     for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
         double acc = 0.0;
@@ -97,6 +126,14 @@ int ls_synth_uniform_f16(void* dst, uint64_t count, uint64_t seed, double lo, do
     if (!count) return 0;
     hipLaunchKernelGGL(lsamd::synth_uniform_kernel, dim3(lsamd::grid_for(count)), dim3(256), 0, (hipStream_t)stream,
                        (uint16_t*)dst, count, seed, lo, hi);
+    return (int)hipPeekAtLastError();
+}
+
+int ls_synth_normal_bf16(void* dst, uint64_t count, uint64_t seed, void* stream) {
+    if (!dst && count) return EINVAL;
+    if (!count) return 0;
+    hipLaunchKernelGGL(lsamd::synth_normal_bf16_kernel, dim3(lsamd::grid_for(count)), dim3(256), 0,
+                       (hipStream_t)stream, (uint16_t*)dst, count, seed);
     return (int)hipPeekAtLastError();
 }
 

@@ -55,6 +55,37 @@ def normal_f16(n, seed):
     return normal_f64(n, seed).astype(np.float16)
 
 
+def f64_to_bf16_bits(v):
+    """Round-to-nearest-even double -> bfloat16 bits (the device generator's conversion)."""
+    b = np.asarray(v, dtype=np.float64).view(np.uint64)
+    sign = (b >> np.uint64(48)) & np.uint64(0x8000)
+    exp = ((b >> np.uint64(52)) & np.uint64(0x7FF)).astype(np.int64)
+    mant = b & np.uint64(0xFFFFFFFFFFFFF)
+    e = exp - 1023 + 127
+    m = (mant >> np.uint64(45)).astype(np.int64)
+    rem = mant & np.uint64((1 << 45) - 1)
+    half = np.uint64(1 << 44)
+    m = m + ((rem > half) | ((rem == half) & (m % 2 == 1))).astype(np.int64)
+    carry = m == 128
+    m = np.where(carry, 0, m)
+    e = e + carry
+    out = sign.astype(np.int64) | (np.clip(e, 0, 255) << 7) | m
+    out = np.where(e >= 255, sign.astype(np.int64) | 0x7F80, out)
+    out = np.where((exp == 0) | (e <= 0), sign.astype(np.int64), out)
+    return out.astype(np.uint16)
+
+
+def normal_bf16(n, seed):
+    """bfloat16 bits of the Irwin-Hall normal stream."""
+    return f64_to_bf16_bits(normal_f64(n, seed))
+
+
+def bf16_to_f16(bits):
+    """bf16 bits -> fp16 (through fp32, round to nearest even): what the dense kernels feed
+    the matrix cores; exact unless |x| < 2^-17."""
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float16)
+
+
 def permutation(n, seed):
     """Fisher-Yates driven by the stream: j = value(i) mod (i + 1), i from n-1 down."""
     perm = np.arange(n, dtype=np.int64)
@@ -84,6 +115,7 @@ class LayerConfig:
     scale_hi: float = 0.02
     selection: str = "ranking"   # "ranking" (N(0,1) scores, top-k) | "permutation" | "all"
     seed: int = 0x1EA5_5EED
+    x_dtype: str = "f16"         # "f16" | "bf16" (the dense batched path)
 
     @property
     def groups(self):
@@ -123,6 +155,12 @@ CONFIGS = {
                         scale_lo=0.003, scale_hi=0.015, seed=0xC4),
     "c1b4": LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25_b4", 1024, 4096, 0.25, batch=4,
                         selection="permutation", seed=0xC1),
+    # dense batched fallback: every group active, batch 32, bf16 x (matrix-core path)
+    "c5": LayerConfig("dense_int4_mlp_d4096_f14336_g64_b32", 4096, 14336, 1.0, batch=32, selection="all",
+                      x_dtype="bf16", seed=0xC5),
+    # the same path at the d_model 1024 shape, 16 of 64 groups (quick parity case)
+    "c1d32": LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25_b32", 1024, 4096, 0.25, batch=32,
+                         selection="permutation", x_dtype="bf16", seed=0xC1),
 }
 
 
@@ -157,13 +195,16 @@ class HostLayer:
     cfg: LayerConfig
     cache: np.ndarray = field(repr=False)    # uint8 [groups * group_bytes]
     scales: np.ndarray = field(repr=False)   # float16 [groups * scale_words]
-    x: np.ndarray = field(repr=False)        # float16 [batch * width]
+    x: np.ndarray = field(repr=False)        # float16 [batch * width] (bf16 x: its exact fp16 value)
 
 
 def host_layer(cfg):
     cache = fill_bytes(cfg.groups * cfg.group_bytes, cfg.sub_seed(SEED_W))
     scales = uniform_f16(cfg.groups * cfg.scale_words, cfg.sub_seed(SEED_S), cfg.scale_lo, cfg.scale_hi)
-    x = normal_f16(cfg.batch * cfg.width, cfg.sub_seed(SEED_X))
+    if cfg.x_dtype == "bf16":
+        x = bf16_to_f16(normal_bf16(cfg.batch * cfg.width, cfg.sub_seed(SEED_X)))
+    else:
+        x = normal_f16(cfg.batch * cfg.width, cfg.sub_seed(SEED_X))
     return HostLayer(cfg, cache, scales, x)
 
 

@@ -37,8 +37,8 @@ class DeviceLayer:
             _check(lib.ls_synth_uniform_f16(self.scales.data_ptr() + 2 * c * n * cfg.scale_words, n * cfg.scale_words,
                                             cfg.sub_seed(synth.SEED_S) + c * 0x1000, cfg.scale_lo, cfg.scale_hi,
                                             stream), "synth scales")
-        _check(lib.ls_synth_normal_f16(self.x.data_ptr(), cfg.batch * d, cfg.sub_seed(synth.SEED_X), stream),
-               "synth x")
+        synth_x = lib.ls_synth_normal_bf16 if cfg.x_dtype == "bf16" else lib.ls_synth_normal_f16
+        _check(synth_x(self.x.data_ptr(), cfg.batch * d, cfg.sub_seed(synth.SEED_X), stream), "synth x")
         self.logical = synth.active_groups(cfg) if logical is None else np.asarray(logical, dtype=np.int64)
         k = len(self.logical)
         self.k = k

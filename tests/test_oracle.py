@@ -186,3 +186,26 @@ def test_ranking_ties_break_by_id():
 def test_ranking_rejects_nonfinite():
     with pytest.raises(ValueError):
         oracle.rank(np.array([1.0, np.nan], dtype=np.float32), 1)
+
+
+def test_f64_to_bf16_round_to_nearest_even():
+    """The bf16 conversion of the dense path's x generator: known answers (values checked
+    against torch's conversion), then correct rounding against both neighbours on a sample
+    of the generator's own values (torch rounds double -> float -> bf16 and can differ at
+    the float midpoint; this conversion rounds once)."""
+    v = np.array([0.0, 1.0, -1.0, 1.00390625, 1.005859375, 1.0078125, 3.14159, -5.99, 1e-3, 1.001953125])
+    want = np.array([0, 16256, 49024, 16256, 16257, 16257, 16457, 49344, 14979, 16256], dtype=np.uint16)
+    assert np.array_equal(synth.f64_to_bf16_bits(v), want)
+    x = synth.normal_f64(20000, 0x5EED)
+    q = synth.f64_to_bf16_bits(x)
+    as_f64 = lambda b: (b.astype(np.uint32) << np.uint32(16)).view(np.float32).astype(np.float64)
+    val = as_f64(q)
+    up, down = as_f64(q + np.uint16(1)), as_f64(q - np.uint16(1))   # neighbours in magnitude
+    err = np.abs(val - x)
+    assert np.all(err <= np.abs(up - x)) and np.all(err <= np.abs(down - x))
+    ties = (err == np.abs(up - x)) | (err == np.abs(down - x))
+    assert np.all(q[ties] % 2 == 0)
+    # bf16 -> fp16 is exact for these magnitudes
+    f16 = synth.bf16_to_f16(q).astype(np.float64)
+    big = np.abs(val) >= 2.0 ** -17
+    assert np.array_equal(f16[big], val[big])
