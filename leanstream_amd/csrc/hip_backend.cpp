@@ -24,6 +24,7 @@ struct HipBackend::Impl {
     void* owned_partial = nullptr;
     uint16_t* h16 = nullptr;     // dense path: fp16 h rows
     float* dpart = nullptr;      // dense path: down-projection partial rows
+    uint16_t* x16 = nullptr;     // dense path: x converted to paired fp16
     bool dense = false;          // batch > kMaxBatch: every launch takes the matrix-core path
     uint32_t* done = nullptr;    // host-coherent: sequence of the last finished launch
     uint32_t last_seq = 0;       // sequence of the last enqueued launch (0: none)
@@ -40,6 +41,7 @@ struct HipBackend::Impl {
         if (owned_partial) (void)hipFree(owned_partial);
         if (h16) (void)hipFree(h16);
         if (dpart) (void)hipFree(dpart);
+        if (x16) (void)hipFree(x16);
         if (status) (void)hipHostFree(status);
         if (done) (void)hipHostFree(done);
         sync = nullptr;
@@ -48,6 +50,7 @@ struct HipBackend::Impl {
         owned_hidden = owned_partial = nullptr;
         h16 = nullptr;
         dpart = nullptr;
+        x16 = nullptr;
         status = nullptr;
         done = nullptr;
         bound = false;
@@ -67,7 +70,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (!b.batch || b.batch > lsamd::kMaxDenseBatch) return ENOTSUP;
     // batch > kMaxBatch: the dense matrix-core path (64-neuron groups, core units only)
     const bool dense = b.batch > lsamd::kMaxBatch;
-    if (dense && b.group_size != 64) return ENOTSUP;
+    if (dense && (b.group_size != 64 || !lsamd::dense_available(static_cast<int>(b.width)))) return ENOTSUP;
     if (b.slot_capacity > lsamd::kMaxRowsReduced) return EINVAL;  // count field of the accumulators
     if (!lsamd::variant_available(static_cast<int>(b.width))) return ENOTSUP;
     p.buf = b;
@@ -85,6 +88,9 @@ int HipBackend::bind(const HipLayerBuffers& b) {
         e = hipMalloc(&p.h16, sizeof(uint16_t) * 32 * b.slot_capacity * b.group_size);
     if (e == hipSuccess && dense)
         e = hipMalloc(&p.dpart, sizeof(float) * lsamd::kDenseSplits * 32 * b.width);
+    if (e == hipSuccess && dense) e = hipMalloc(&p.x16, sizeof(uint16_t) * 32 * b.width);
+    // h rows >= batch stay zero: the dense down projection reads all 32 rows
+    if (e == hipSuccess && dense) e = hipMemset(p.h16, 0, sizeof(uint16_t) * 32 * b.slot_capacity * b.group_size);
     if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
@@ -131,6 +137,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.slot_capacity = b.slot_capacity;
     a.h16 = p.h16;
     a.dpart = p.dpart;
+    a.x16 = p.x16;
     a.dsplits = dense ? lsamd::kDenseSplits : 0u;
     p.bounds = {b.cache_groups, b.staging_groups, b.physical_groups};
     slices_ = b.width / lsamd::kDnCols;

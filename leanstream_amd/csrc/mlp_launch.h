@@ -20,6 +20,7 @@ hipError_t resident_workers(int width, int entry_point, int batch, int* per_cu);
 hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
 // Dense batched path (batch > kMaxBatch, core units only): gate/up -> down -> reduction.
 hipError_t launch_dense(const MlpArgs&, const Bounds&, hipStream_t);
+bool dense_available(int width);   // widths the dense (batch > kMaxBatch) path is compiled for
 // Zeroes both ring slots, both accumulator buffers and the tagged h rows.
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
                       uint32_t hwords, hipStream_t);

@@ -248,6 +248,12 @@ template <int D>
 __device__ __forceinline__ void stage_x(XPart<D>& xp, uint32_t batch, u32x4* xl, uint32_t* count) {
     using Xg = XGeom<D>;
     if (xp.staged) return;
+    // The pairing below must not be hoisted above the wave's first descriptor loads (the
+    // compiler would, to share it between the call sites): it waits for x, and the
+    // descriptors would then be requested only after x arrived. The empty asm pins the
+    // registers here; its memory clobber keeps the loads issued before it ahead of it.
+#pragma unroll
+    for (int j = 0; j < Xg::PER; ++j) asm volatile("" : "+v"(xp.v[j]) : : "memory");
 #pragma unroll
     for (int j = 0; j < Xg::PER; ++j) {
         const int i = threadIdx.x + j * kThreads;
@@ -618,6 +624,9 @@ __device__ __forceinline__ bool await_epoch(const MlpArgs& a, uint32_t* slot, Ep
     uint32_t word = 0;
     if (lane_id() == 0) {
         word = early;
+        // kept here: decoded earlier, the word would make the wave wait for every load
+        // issued before it (x, the descriptors) at the kernel's start
+        asm volatile("" : "+v"(word) : : "memory");
         Waiter wt(a.spin_limit);
         while (!(word & 3u)) {
             if (ld_agent(slot + kSyncAbort)) { word = 2; break; }
@@ -1324,14 +1333,17 @@ __global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long 
 // element i is C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32]. Which k a slot stands for is
 // free as long as A and B agree, so each lane feeds the MFMA from its own contiguous loads.
 //
-// Three launches: gate/up (h rows in fp16), down projection (fp32 partial rows per split
-// of the units), reduction (fixed split order, then the completion word).
+// Four launches: x conversion (bf16 -> paired fp16, once per layer), gate/up (h rows in
+// fp16), down projection (fp32 partial rows per split of the units), reduction (fixed
+// split order, then the completion word).
 // ---------------------------------------------------------------------------------
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kDenseCols = 128;    // down-projection columns per workgroup (32 per wave)
 constexpr int kDensePitch = 72;    // fp16 per LDS row: 64 neurons + 8 (rows stay 16-byte aligned)
+constexpr int kDenseGuWaves = 8;   // gate/up waves per workgroup, each reduces D / 8 columns
+constexpr int kDensePrefetch = 8;  // units whose down-tile loads are in flight per workgroup
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint32_t bits) {
     return (_Float16)__builtin_bit_cast(float, bits << 16);
@@ -1341,17 +1353,51 @@ __device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Workgroup barrier ordering LDS traffic only. __syncthreads() is a release/acquire at
+// workgroup scope over all memory, so it waits for every global load of the wave still
+// in flight (s_waitcnt vmcnt(0)); the prefetched loads of later units must stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// x (bf16 [batch][D]) -> x16 (fp16 [32][D]) in dequant8's pairing: within each 8-column
+// group the slots hold columns (0, 4, 1, 5, 2, 6, 3, 7), so one 16-byte load of x16 is
+// the MFMA A fragment matching a dequantised weight word. Rows >= batch are zero. Once
+// per layer, so the gate/up workgroups share one conversion instead of each redoing it.
+__global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
+    const uint32_t D = a.width, groups = D / 8;
+    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * groups + group
+    const uint32_t row = idx / groups, grp = idx - row * groups;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < a.batch) v = *reinterpret_cast<const u32x4*>(a.x + (size_t)row * D + 8 * grp);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    h8 o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o[2 * i] = bf16_to_f16((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+        o[2 * i + 1] = bf16_to_f16((w[(i + 4) >> 1] >> (16 * (i & 1))) & 0xffffu);
+    }
+    *reinterpret_cast<h8*>(a.x16 + (size_t)row * D + 8 * grp) = o;
+}
+
 // Gate/up of one 32-neuron half of one unit for all batch rows. Wave w reduces the
-// quarter [w D/4, (w+1) D/4) of the input; the four partial tiles meet in LDS. Lane l
-// (neuron 32 half + l % 32, row l % 32 of x) loads 32 consecutive columns per step:
-// 16 bytes of each weight row and 64 bytes of x.
-__global__ __launch_bounds__(kThreads) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
-    __shared__ float red[kWaves][2][16][64];
-    const uint32_t D = a.width, G = a.group_size;
+// eighth [w D/8, (w+1) D/8) of the input in NI steps of 64 columns; the eight partial
+// tiles meet in LDS. Lane l (neuron 32 half + l % 32, row l % 32 of x) takes 32
+// consecutive columns per step: 16 bytes of each weight row and 64 bytes of x16. All NI
+// steps' weight loads are issued before the first MFMA (NI <= 16: at most 128 registers),
+// so a wave keeps its whole share of the weights in flight.
+template <int NI>
+__global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
+    __shared__ float red[kDenseGuWaves][2][16][64];
+    constexpr uint32_t D = NI * 64 * kDenseGuWaves;
+    constexpr uint32_t kq = D / kDenseGuWaves;
+    const uint32_t G = a.group_size;
     const uint32_t unit = blockIdx.x >> 1, half = blockIdx.x & 1;
     if (blockIdx.x == 0) {   // the next launch's ring slot (this one's was cleared before it)
         uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-        for (uint32_t i = threadIdx.x; i < a.slot_words; i += kThreads) st_agent(other + i, 0u);
+        for (uint32_t i = threadIdx.x; i < a.slot_words; i += blockDim.x) st_agent(other + i, 0u);
     }
     const Unit u = resolve(a, b, a.core[unit], (int)D);
     const int lane = lane_id();
@@ -1363,28 +1409,34 @@ __global__ __launch_bounds__(kThreads) void dense_gate_up_kernel(MlpArgs a, Boun
         const uint8_t* wu = wg + D / 2;
         const uint16_t* sg = u.sc + (size_t)(n * 3) * (D / 128);
         const uint16_t* su = sg + D / 128;
-        const uint16_t* xr = a.x + (size_t)row * D;
-        const bool xok = row < a.batch;
-        const uint32_t kq = D / kWaves;
-        for (uint32_t t = 0; t < kq / 64; ++t) {
-            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
-            const u32x4 qg = ld_stream16(wg + k0 / 2), qu = ld_stream16(wu + k0 / 2);
-            const uint16_t sgb = sg[k0 / 128], sub = su[k0 / 128];
-            u32x4 xv[4];
+        const _Float16* xr = reinterpret_cast<const _Float16*>(a.x16) + (size_t)row * D;
+        u32x4 qg[NI], qu[NI];
+        uint32_t sgv[NI], suv[NI];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                xv[q] = xok ? *reinterpret_cast<const u32x4*>(xr + k0 + 8 * q) : u32x4{0u, 0u, 0u, 0u};
-            const h2 sg2 = {half_bits(sgb), half_bits(sgb)}, su2 = {half_bits(sub), half_bits(sub)};
+        for (int t = 0; t < NI; ++t) {
+            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+            qg[t] = ld_stream16(wg + k0 / 2);
+            qu[t] = ld_stream16(wu + k0 / 2);
+            sgv[t] = sg[k0 / 128];
+            suv[t] = su[k0 / 128];
+        }
+        // keep every load above ahead of the first MFMA (the scheduler would otherwise
+        // sink them next to their uses, leaving two or three in flight per wave)
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NI; ++t) {
+            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+            const h2 sg2 = {half_bits((uint16_t)sgv[t]), half_bits((uint16_t)sgv[t])};
+            const h2 su2 = {half_bits((uint16_t)suv[t]), half_bits((uint16_t)suv[t])};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                const h8 xa = *reinterpret_cast<const h8*>(xr + k0 + 8 * j);   // paired (dense_x_kernel)
                 h2 wgv[4], wuv[4];
-                dequant8(qg[j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
-                dequant8(qu[j], su2, wuv);
-                h8 xa, bg, bu;
+                dequant8(qg[t][j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
+                dequant8(qu[t][j], su2, wuv);
+                h8 bg, bu;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {   // slot 2 i = column i, slot 2 i + 1 = column i + 4
-                    xa[2 * i] = bf16_to_f16((xv[j][i >> 1] >> (16 * (i & 1))) & 0xffffu);
-                    xa[2 * i + 1] = bf16_to_f16((xv[j][(i + 4) >> 1] >> (16 * (i & 1))) & 0xffffu);
+                for (int i = 0; i < 4; ++i) {
                     bg[2 * i] = wgv[i].x;
                     bg[2 * i + 1] = wgv[i].y;
                     bu[2 * i] = wuv[i].x;
@@ -1403,11 +1455,11 @@ __global__ __launch_bounds__(kThreads) void dense_gate_up_kernel(MlpArgs a, Boun
     __syncthreads();
     const uint32_t hstride = a.slot_capacity * G;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const uint32_t e = threadIdx.x + kThreads * r, i = e >> 6, l = e & 63;
+    for (int r = 0; r < 1024 / (64 * kDenseGuWaves); ++r) {
+        const uint32_t e = threadIdx.x + 64 * kDenseGuWaves * r, i = e >> 6, l = e & 63;
         float gsum = 0.f, usum = 0.f;
 #pragma unroll
-        for (int v = 0; v < kWaves; ++v) {   // fixed order: deterministic
+        for (int v = 0; v < kDenseGuWaves; ++v) {   // fixed order: deterministic
             gsum += red[v][0][i][l];
             usum += red[v][1][i][l];
         }
@@ -1429,53 +1481,85 @@ __global__ __launch_bounds__(kThreads) void dense_gate_up_kernel(MlpArgs a, Boun
     }
 }
 
+// One unit's share of a down-projection workgroup's loads: thread t's 16 bytes of the
+// 64 x 128 weight tile (neuron t / 4, columns 32 (t % 4) ..), the tile's scale of that
+// neuron, and 16 bytes of the unit's h rows (batch row t / 8, neurons 8 (t % 8) ..).
+struct DenseDnLoad {
+    u32x4 q, hv;
+    uint32_t sb;
+    bool ok;
+};
+
+// Branch-free, so that the compiler can count the loads in flight and wait for exactly
+// one unit's: a position past the split re-reads the split's first unit, and an invalid
+// descriptor reads the partial-row buffer (at least 2048 d bytes, more than a group's
+// 96 d), both with ok = false. h rows >= batch are zero (cleared at bind).
+__device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b, uint32_t un, uint32_t u0,
+                                               uint32_t u1, uint32_t c0, DenseDnLoad& L) {
+    const uint32_t D = a.width, G = a.group_size, t = threadIdx.x;
+    const uint32_t nn = t >> 2, cc = t & 3, hr = t >> 3, hp = t & 7;
+    const bool in = un < u1;
+    const Unit u = resolve(a, b, a.core[in ? un : u0], (int)D);
+    L.ok = in && u.ok;   // an invalid descriptor is reported by the gate/up kernel
+    const uint8_t* grp = u.ok ? u.grp : reinterpret_cast<const uint8_t*>(a.dpart);
+    const uint16_t* sc = u.ok ? u.sc : reinterpret_cast<const uint16_t*>(a.dpart);
+    L.q = ld_stream16(grp + (size_t)(nn * 3 + 2) * (D / 2) + (c0 + 32 * cc) / 2);
+    L.sb = sc[(size_t)(nn * 3 + 2) * (D / 128) + c0 / 128];
+    L.hv = *reinterpret_cast<const u32x4*>(a.h16 + (size_t)hr * a.slot_capacity * G + u.dest * G + 8 * hp);
+}
+
 // Down projection of 128 columns over one split of the units. Per unit the workgroup
 // dequantises the 64 x 128 weight tile into LDS transposed (column-major, so a lane's
 // eight k slots are eight neurons of its column: one 16-byte LDS read) and stages the
-// unit's h rows; wave w then runs four MFMAs for columns 32 w .. 32 w + 31.
+// unit's h rows; wave w then runs four MFMAs for columns 32 w .. 32 w + 31. The loads of
+// the next kDensePrefetch units are in flight while a unit is computed.
 __global__ __launch_bounds__(kThreads) void dense_down_kernel(MlpArgs a, Bounds b) {
     __shared__ alignas(16) _Float16 wl[kDenseCols][kDensePitch];
     __shared__ alignas(16) _Float16 hl[32][kDensePitch];
-    const uint32_t D = a.width, G = a.group_size;
+    const uint32_t D = a.width;
     const uint32_t tiles = D / kDenseCols;
     const uint32_t ct = blockIdx.x % tiles, split = blockIdx.x / tiles;
     const uint32_t c0 = ct * kDenseCols;
     const uint32_t per = (a.core_count + a.dsplits - 1) / a.dsplits;
-    const uint32_t u0 = split * per, u1 = min(a.core_count, u0 + per);
+    const uint32_t u0 = min(a.core_count, split * per), u1 = min(a.core_count, u0 + per);
     const uint32_t t = threadIdx.x;
     const int lane = lane_id();
     const uint32_t w = wave_id();
     const uint32_t nn = t >> 2, cc = t & 3;   // weight tile: neuron, 32-column chunk
     const uint32_t hr = t >> 3, hp = t & 7;   // h tile: batch row, 8-neuron part
-    const uint32_t hstride = a.slot_capacity * G;
     f32x16 acc = {};
-    for (uint32_t un = u0; un < u1; ++un) {
-        const Unit u = resolve(a, b, a.core[un], (int)D);
-        if (!u.ok) continue;   // uniform across the workgroup; reported by the gate/up kernel
-        const u32x4 q = ld_stream16(u.grp + (size_t)(nn * 3 + 2) * (D / 2) + (c0 + 32 * cc) / 2);
-        const uint16_t sb = u.sc[(size_t)(nn * 3 + 2) * (D / 128) + c0 / 128];
-        const u32x4 hv = hr < a.batch ? *reinterpret_cast<const u32x4*>(a.h16 + (size_t)hr * hstride + u.dest * G + 8 * hp)
-                                      : u32x4{0u, 0u, 0u, 0u};
-        __syncthreads();   // the previous unit's tiles are read
-        const h2 s2 = {half_bits(sb), half_bits(sb)};
+    DenseDnLoad buf[kDensePrefetch];
+    if (u0 < u1) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h2 wv[4];
-            dequant8(q[j], s2, wv);
+    for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue(a, b, u0 + s, u0, u1, c0, buf[s]);
+    for (uint32_t base = u0; base < u1; base += kDensePrefetch) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wl[32 * cc + 8 * j + i][nn] = wv[i].x;
-                wl[32 * cc + 8 * j + i + 4][nn] = wv[i].y;
+        for (int s = 0; s < kDensePrefetch; ++s) {
+            if (buf[s].ok) {   // uniform across the workgroup
+                lds_barrier();   // the previous unit's tiles are read
+                const h2 s2 = {half_bits((uint16_t)buf[s].sb), half_bits((uint16_t)buf[s].sb)};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    h2 wv[4];
+                    dequant8(buf[s].q[j], s2, wv);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        wl[32 * cc + 8 * j + i][nn] = wv[i].x;
+                        wl[32 * cc + 8 * j + i + 4][nn] = wv[i].y;
+                    }
+                }
+                *reinterpret_cast<u32x4*>(&hl[hr][8 * hp]) = buf[s].hv;
+                lds_barrier();
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const h8 ha = *reinterpret_cast<const h8*>(&hl[lane & 31][16 * j + 8 * (lane >> 5)]);
+                    const h8 wb = *reinterpret_cast<const h8*>(&wl[32 * w + (lane & 31)][16 * j + 8 * (lane >> 5)]);
+                    acc = mfma32(ha, wb, acc);
+                }
             }
+            dense_dn_issue(a, b, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
         }
-        *reinterpret_cast<u32x4*>(&hl[hr][8 * hp]) = hv;
-        __syncthreads();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const h8 ha = *reinterpret_cast<const h8*>(&hl[lane & 31][16 * j + 8 * (lane >> 5)]);
-            const h8 wb = *reinterpret_cast<const h8*>(&wl[32 * w + (lane & 31)][16 * j + 8 * (lane >> 5)]);
-            acc = mfma32(ha, wb, acc);
-        }
+    }
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -1489,7 +1573,15 @@ __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
     const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * D + column
     const uint32_t tk = idx / a.width, col = idx - tk * a.width;
     float v = 0.f;
-    for (uint32_t s = 0; s < a.dsplits; ++s) v += a.dpart[((size_t)s * 32 + tk) * a.width + col];
+    if (a.dsplits == kDenseSplits) {   // every split's load in flight at once
+        float p[kDenseSplits];
+#pragma unroll
+        for (uint32_t s = 0; s < kDenseSplits; ++s) p[s] = a.dpart[((size_t)s * 32 + tk) * a.width + col];
+#pragma unroll
+        for (uint32_t s = 0; s < kDenseSplits; ++s) v += p[s];
+    } else {
+        for (uint32_t s = 0; s < a.dsplits; ++s) v += a.dpart[((size_t)s * 32 + tk) * a.width + col];
+    }
     if (a.y32) a.y32[idx] = v;
     a.y[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
     finish_launch(a, a.sync + (a.seq & 1) * a.slot_words);
@@ -1567,17 +1659,36 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
 }
 
+namespace {
+const void* dense_gate_up_for(uint32_t width) {
+    switch (width) {
+        case 512: return reinterpret_cast<const void*>(&dense_gate_up_kernel<1>);
+        case 1024: return reinterpret_cast<const void*>(&dense_gate_up_kernel<2>);
+        case 2048: return reinterpret_cast<const void*>(&dense_gate_up_kernel<4>);
+        case 4096: return reinterpret_cast<const void*>(&dense_gate_up_kernel<8>);
+        case 8192: return reinterpret_cast<const void*>(&dense_gate_up_kernel<16>);
+        default: return nullptr;
+    }
+}
+}  // namespace
+
+bool dense_available(int width) { return width > 0 && dense_gate_up_for((uint32_t)width) != nullptr; }
+
 hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t stream) {
     MlpArgs a = args;
     Bounds b = bounds;
-    if (a.group_size != 64 || a.width % 256 || a.batch <= kMaxBatch || a.batch > kMaxDenseBatch || !a.dsplits ||
-        !a.h16 || !a.dpart)
+    const void* gate_up = dense_gate_up_for(a.width);
+    if (a.group_size != 64 || !gate_up || a.batch <= kMaxBatch || a.batch > kMaxDenseBatch || !a.dsplits ||
+        !a.h16 || !a.dpart || !a.x16)
         return hipErrorInvalidValue;
     void* kargs[] = {&a, &b};
+    void* rargs[] = {&a};
     hipError_t e = hipSuccess;
     if (a.core_count) {
-        e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_gate_up_kernel), dim3(2 * a.core_count),
-                            dim3(kThreads), kargs, 0, stream);
+        e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_x_kernel), dim3(32 * a.width / 8 / kThreads),
+                            dim3(kThreads), rargs, 0, stream);
+        if (e == hipSuccess)
+            e = hipLaunchKernel(gate_up, dim3(2 * a.core_count), dim3(64 * kDenseGuWaves), kargs, 0, stream);
         if (e == hipSuccess)
             e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_down_kernel),
                                 dim3(a.width / kDenseCols * a.dsplits), dim3(kThreads), kargs, 0, stream);
@@ -1585,7 +1696,6 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
         a.dsplits = 0;   // nothing to sum: y = 0
     }
     if (e != hipSuccess) return e;
-    void* rargs[] = {&a};
     return hipLaunchKernel(reinterpret_cast<const void*>(&dense_reduce_kernel), dim3(a.batch * a.width / kThreads),
                            dim3(kThreads), rargs, 0, stream);
 }

@@ -35,6 +35,19 @@ def compare(y32, ref, what):
     return rel, mx
 
 
+def check_h(h, ref_h, what):
+    """The intermediate h rows (fp16 values) against the oracle's. Gate/up dequantise exactly
+    as LeanStream does (fp16(q*s) per weight), so only the fp32 summation order differs and
+    fewer than 1% of the neurons may land on the other side of an fp16 rounding boundary of
+    gate, up, silu or h; the rows also meet the stated relative L2 tolerance."""
+    h = np.asarray(h, dtype=np.float64)
+    ref_h = np.asarray(ref_h, dtype=np.float64)
+    rel = np.linalg.norm(h - ref_h) / max(np.linalg.norm(ref_h), 1e-30)
+    flips = np.mean(h != ref_h)
+    log(f"  {what}: rel_l2={rel:.3e}, {flips * 100:.3f}% of neurons differ (fp16 rounding-boundary flips)")
+    assert flips < 0.01 and rel <= REL_L2, (flips, rel)
+
+
 def f16_ulps(a16, b16):
     a = np.asarray(a16, dtype=np.float16).view(np.int16).astype(np.int32)
     b = np.asarray(b16, dtype=np.float16).view(np.int16).astype(np.int32)
@@ -86,10 +99,7 @@ def test_core_layer_matches_oracle(torch_gpu, key):
     log(f"  fp16 output: max {ulps.max()} ulp, {np.mean(ulps > 0) * 100:.2f}% differ")
     # the fp16 output is the round-to-nearest of y32
     assert np.array_equal(layer.y.cpu().numpy().view(np.uint16), y32.astype(np.float16).view(np.uint16))
-    h = layer.hidden_h()
-    hdiff = np.abs(h - ref["h"]) > 0
-    log(f"  h: {hdiff.mean() * 100:.3f}% of neurons differ (fp16 rounding-boundary flips)")
-    assert hdiff.mean() < 0.01
+    check_h(layer.hidden_h(), ref["h"], "h")
     assert np.all(layer.executions.cpu().numpy() == 1)
     layer.close()
 
@@ -117,9 +127,7 @@ def test_batch_layer_matches_oracle(torch_gpu, key):
                            cfg.group_size, threads=8)
         compare(y32[b], ref["y32"], f"{cfg.name} row {b}")
         assert np.array_equal(y16[b].view(np.uint16), y32[b].astype(np.float16).view(np.uint16))
-        hdiff = np.abs(h[:, b, :] - ref["h"]) > 0
-        log(f"  row {b} h: {hdiff.mean() * 100:.3f}% of neurons differ (fp16 rounding-boundary flips)")
-        assert hdiff.mean() < 0.01
+        check_h(h[:, b, :], ref["h"], f"row {b} h")
     assert np.all(layer.executions.cpu().numpy() == 1)
     single = DeviceLayer(synth.CONFIGS[key.replace("b4", "")])
     single.seal_empty_queue(1)
