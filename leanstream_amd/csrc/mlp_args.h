@@ -110,7 +110,7 @@ struct MlpArgs {
     // dense path (batch > kMaxBatch): x is bf16 [batch][d]
     uint16_t* h16;                // fp16 h rows [32][slot_capacity * G]
     float* dpart;                 // fp32 down-projection partial rows [dsplits][32][d]
-    uint16_t* x16;                // x as fp16 [32][d] in dequant8's column pairing (rows >= batch zero)
+    uint16_t* x16;                // x as fp16 MFMA A fragments, 32 rows x d (dense_x_kernel; rows >= batch zero)
     uint32_t dsplits;
     uint64_t spin_limit;          // bounded waits, in 100 MHz ticks
 };

@@ -89,6 +89,9 @@ __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
 __device__ __forceinline__ u32x4 ld_stream16(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
+// A plain (L2-retained) 16-byte load, for weight lines that are consumed by several
+// instructions (a streaming load may drop the line after its first piece is read).
+__device__ __forceinline__ u32x4 ld_cached16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ u32x2 ld_stream8(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
@@ -1340,10 +1343,11 @@ __global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kDenseCols = 128;    // down-projection columns per workgroup (32 per wave)
+constexpr int kDenseCols = 256;    // down-projection columns per workgroup: whole 128-byte weight lines
+constexpr int kDenseDnWaves = kDenseCols / 32;   // 32 columns per wave
 constexpr int kDensePitch = 72;    // fp16 per LDS row: 64 neurons + 8 (rows stay 16-byte aligned)
 constexpr int kDenseGuWaves = 8;   // gate/up waves per workgroup, each reduces D / 8 columns
-constexpr int kDensePrefetch = 8;  // units whose down-tile loads are in flight per workgroup
+constexpr int kDensePrefetch = 6;  // units whose down-tile loads are in flight per workgroup (9 loads each)
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint32_t bits) {
     return (_Float16)__builtin_bit_cast(float, bits << 16);
@@ -1362,10 +1366,18 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// x (bf16 [batch][D]) -> x16 (fp16 [32][D]) in dequant8's pairing: within each 8-column
-// group the slots hold columns (0, 4, 1, 5, 2, 6, 3, 7), so one 16-byte load of x16 is
-// the MFMA A fragment matching a dequantised weight word. Rows >= batch are zero. Once
-// per layer, so the gate/up workgroups share one conversion instead of each redoing it.
+// x (bf16 [batch][D]) -> x16: fp16 MFMA A fragments in dequant8's pairing. Within each
+// 8-column group the slots hold columns (0, 4, 1, 5, 2, 6, 3, 7), so one 16-byte piece
+// is the A fragment matching a dequantised weight word. The pieces are stored in the
+// order the gate/up waves load them: fragment f = 4 (c / 64) + (c % 32) / 8 holds, for
+// lane l, row l % 32 and columns 64 (c / 64) + 32 (l / 32) + 8 ((c % 32) / 8) .. + 7 at
+// byte 1024 f + 16 l, so every x load of a wave reads one contiguous kilobyte. Rows >=
+// batch are zero. Once per layer, shared by every gate/up workgroup.
+__device__ __forceinline__ uint32_t x16_piece(uint32_t row, uint32_t c) {   // 16-byte piece index
+    const uint32_t f = 4 * (c / 64) + (c % 32) / 8, l = row + 32 * ((c % 64) / 32);
+    return 64 * f + l;
+}
+
 __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
     const uint32_t D = a.width, groups = D / 8;
     const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * groups + group
@@ -1379,7 +1391,7 @@ __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
         o[2 * i] = bf16_to_f16((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
         o[2 * i + 1] = bf16_to_f16((w[(i + 4) >> 1] >> (16 * (i & 1))) & 0xffffu);
     }
-    *reinterpret_cast<h8*>(a.x16 + (size_t)row * D + 8 * grp) = o;
+    reinterpret_cast<h8*>(a.x16)[x16_piece(row, 8 * grp)] = o;
 }
 
 // Gate/up of one 32-neuron half of one unit for all batch rows. Wave w reduces the
@@ -1390,7 +1402,7 @@ __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
 // so a wave keeps its whole share of the weights in flight.
 template <int NI>
 __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
-    __shared__ float red[kDenseGuWaves][2][16][64];
+    __shared__ float red[kDenseGuWaves / 2][2][16][64];   // 32 KB: two workgroups per CU fit
     constexpr uint32_t D = NI * 64 * kDenseGuWaves;
     constexpr uint32_t kq = D / kDenseGuWaves;
     const uint32_t G = a.group_size;
@@ -1409,14 +1421,25 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         const uint8_t* wu = wg + D / 2;
         const uint16_t* sg = u.sc + (size_t)(n * 3) * (D / 128);
         const uint16_t* su = sg + D / 128;
-        const _Float16* xr = reinterpret_cast<const _Float16*>(a.x16) + (size_t)row * D;
+        const u32x4* xf = reinterpret_cast<const u32x4*>(a.x16);
+        // x16 of step t (four 16-byte fragments per lane, each wave-contiguous) is loaded
+        // two steps ahead, from a ring of three; steps 0 and 1 go out before the weights.
+        // Loads complete in issue order, so each step waits only for what it uses.
+        u32x4 xq[3][4];
+        auto issue_x = [&](int t, u32x4 (&dst)[4]) {
+            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dst[j] = xf[x16_piece(row, k0 + 8 * j)];
+        };
+        issue_x(0, xq[0]);
+        if (NI > 1) issue_x(1, xq[1]);
         u32x4 qg[NI], qu[NI];
         uint32_t sgv[NI], suv[NI];
 #pragma unroll
         for (int t = 0; t < NI; ++t) {
             const uint32_t k0 = w * kq + 64 * t + 32 * hh;
-            qg[t] = ld_stream16(wg + k0 / 2);
-            qu[t] = ld_stream16(wu + k0 / 2);
+            qg[t] = ld_cached16(wg + k0 / 2);   // a row's 128-byte line serves four steps
+            qu[t] = ld_cached16(wu + k0 / 2);
             sgv[t] = sg[k0 / 128];
             suv[t] = su[k0 / 128];
         }
@@ -1425,12 +1448,13 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int t = 0; t < NI; ++t) {
-            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+            if (t + 2 < NI) issue_x(t + 2, xq[(t + 2) % 3]);
+            __builtin_amdgcn_sched_barrier(0);
             const h2 sg2 = {half_bits((uint16_t)sgv[t]), half_bits((uint16_t)sgv[t])};
             const h2 su2 = {half_bits((uint16_t)suv[t]), half_bits((uint16_t)suv[t])};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const h8 xa = *reinterpret_cast<const h8*>(xr + k0 + 8 * j);   // paired (dense_x_kernel)
+                const h8 xa = __builtin_bit_cast(h8, xq[t % 3][j]);   // paired (dense_x_kernel)
                 h2 wgv[4], wuv[4];
                 dequant8(qg[t][j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
                 dequant8(qu[t][j], su2, wuv);
@@ -1447,10 +1471,22 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
             }
         }
     }
+    // Fixed-order sum of the eight partial tiles: wave w + 4 into wave w, then waves 0..3.
+    constexpr uint32_t HW = kDenseGuWaves / 2;
+    if (w >= HW) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        red[w][0][i][lane] = cg[i];
-        red[w][1][i][lane] = cu[i];
+        for (int i = 0; i < 16; ++i) {
+            red[w - HW][0][i][lane] = cg[i];
+            red[w - HW][1][i][lane] = cu[i];
+        }
+    }
+    __syncthreads();
+    if (w < HW) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            red[w][0][i][lane] += cg[i];
+            red[w][1][i][lane] += cu[i];
+        }
     }
     __syncthreads();
     const uint32_t hstride = a.slot_capacity * G;
@@ -1459,7 +1495,7 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         const uint32_t e = threadIdx.x + 64 * kDenseGuWaves * r, i = e >> 6, l = e & 63;
         float gsum = 0.f, usum = 0.f;
 #pragma unroll
-        for (int v = 0; v < kDenseGuWaves; ++v) {   // fixed order: deterministic
+        for (int v = 0; v < (int)HW; ++v) {   // fixed order: deterministic
             gsum += red[v][0][i][l];
             usum += red[v][1][i][l];
         }
@@ -1481,12 +1517,14 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
     }
 }
 
-// One unit's share of a down-projection workgroup's loads: thread t's 16 bytes of the
-// 64 x 128 weight tile (neuron t / 4, columns 32 (t % 4) ..), the tile's scale of that
-// neuron, and 16 bytes of the unit's h rows (batch row t / 8, neurons 8 (t % 8) ..).
+// One unit's share of a down-projection workgroup's loads. Thread t covers rows
+// 4 (t / 32) .. + 3 and columns 8 (t % 32) .. + 7 of the unit's 64 x 256 weight tile: one
+// 4-byte load per row (a wave's 32 lanes read a row's whole 128-byte line), that row's
+// scale for the columns' block, and 8 bytes of the unit's h rows (batch row t / 16,
+// neurons 4 (t % 16) ..).
 struct DenseDnLoad {
-    u32x4 q, hv;
-    uint32_t sb;
+    uint32_t q[4], sb[4];
+    u32x2 hv;
     bool ok;
 };
 
@@ -1497,24 +1535,37 @@ struct DenseDnLoad {
 __device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b, uint32_t un, uint32_t u0,
                                                uint32_t u1, uint32_t c0, DenseDnLoad& L) {
     const uint32_t D = a.width, G = a.group_size, t = threadIdx.x;
-    const uint32_t nn = t >> 2, cc = t & 3, hr = t >> 3, hp = t & 7;
+    const uint32_t nq = t >> 5, o = t & 31, hr = t >> 4, hp = t & 15;
     const bool in = un < u1;
     const Unit u = resolve(a, b, a.core[in ? un : u0], (int)D);
     L.ok = in && u.ok;   // an invalid descriptor is reported by the gate/up kernel
     const uint8_t* grp = u.ok ? u.grp : reinterpret_cast<const uint8_t*>(a.dpart);
     const uint16_t* sc = u.ok ? u.sc : reinterpret_cast<const uint16_t*>(a.dpart);
-    L.q = ld_stream16(grp + (size_t)(nn * 3 + 2) * (D / 2) + (c0 + 32 * cc) / 2);
-    L.sb = sc[(size_t)(nn * 3 + 2) * (D / 128) + c0 / 128];
-    L.hv = *reinterpret_cast<const u32x4*>(a.h16 + (size_t)hr * a.slot_capacity * G + u.dest * G + 8 * hp);
+    const uint32_t col = c0 + 8 * o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const uint32_t n = 4 * nq + r;
+        L.q[r] = *reinterpret_cast<const uint32_t*>(grp + (size_t)(n * 3 + 2) * (D / 2) + col / 2);
+        L.sb[r] = sc[(size_t)(n * 3 + 2) * (D / 128) + col / 128];
+    }
+    L.hv = *reinterpret_cast<const u32x2*>(a.h16 + (size_t)hr * a.slot_capacity * G + u.dest * G + 4 * hp);
 }
 
-// Down projection of 128 columns over one split of the units. Per unit the workgroup
-// dequantises the 64 x 128 weight tile into LDS transposed (column-major, so a lane's
-// eight k slots are eight neurons of its column: one 16-byte LDS read) and stages the
-// unit's h rows; wave w then runs four MFMAs for columns 32 w .. 32 w + 31. The loads of
-// the next kDensePrefetch units are in flight while a unit is computed.
-__global__ __launch_bounds__(kThreads) void dense_down_kernel(MlpArgs a, Bounds b) {
-    __shared__ alignas(16) _Float16 wl[kDenseCols][kDensePitch];
+// LDS position (in halves) of the 8-neuron granule gr of tile column col: rows of 64
+// neurons, granules XOR-swizzled by bits 3..5 of the column so that the 8-byte writes of
+// one instruction (32 columns 8 apart) and the MFMA's 16-byte reads spread over the banks.
+__device__ __forceinline__ uint32_t dn_tile_pos(uint32_t col, uint32_t gr) {
+    return col * 64 + 8 * (gr ^ ((col >> 3) & 7));
+}
+
+// Down projection of 256 columns over one split of the units. Per unit the workgroup
+// dequantises the 64 x 256 weight tile into LDS transposed (column-major, 8-neuron
+// granules, so a lane's eight k slots are eight neurons of its column: one 16-byte LDS
+// read) and stages the unit's h rows; wave w then runs four MFMAs for columns
+// 32 w .. 32 w + 31. The loads of the next kDensePrefetch units are in flight while a
+// unit is computed.
+__global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs a, Bounds b) {
+    __shared__ alignas(16) _Float16 wl[kDenseCols * 64];
     __shared__ alignas(16) _Float16 hl[32][kDensePitch];
     const uint32_t D = a.width;
     const uint32_t tiles = D / kDenseCols;
@@ -1525,41 +1576,49 @@ __global__ __launch_bounds__(kThreads) void dense_down_kernel(MlpArgs a, Bounds 
     const uint32_t t = threadIdx.x;
     const int lane = lane_id();
     const uint32_t w = wave_id();
-    const uint32_t nn = t >> 2, cc = t & 3;   // weight tile: neuron, 32-column chunk
-    const uint32_t hr = t >> 3, hp = t & 7;   // h tile: batch row, 8-neuron part
+    const uint32_t nq = t >> 5, o = t & 31;    // weight tile: 4-row group, 8-column group
+    const uint32_t hr = t >> 4, hp = t & 15;   // h tile: batch row, 4-neuron part
     f32x16 acc = {};
     DenseDnLoad buf[kDensePrefetch];
     if (u0 < u1) {
 #pragma unroll
-    for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue(a, b, u0 + s, u0, u1, c0, buf[s]);
-    for (uint32_t base = u0; base < u1; base += kDensePrefetch) {
+        for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue(a, b, u0 + s, u0, u1, c0, buf[s]);
+        for (uint32_t base = u0; base < u1; base += kDensePrefetch) {
 #pragma unroll
-        for (int s = 0; s < kDensePrefetch; ++s) {
-            if (buf[s].ok) {   // uniform across the workgroup
-                lds_barrier();   // the previous unit's tiles are read
-                const h2 s2 = {half_bits((uint16_t)buf[s].sb), half_bits((uint16_t)buf[s].sb)};
+            for (int s = 0; s < kDensePrefetch; ++s) {
+                if (buf[s].ok) {   // uniform across the workgroup
+                    // dequantise the four rows (pairs (column k, column k + 4) per row)
+                    h2 v[4][4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    h2 wv[4];
-                    dequant8(buf[s].q[j], s2, wv);
+                    for (int r = 0; r < 4; ++r) {
+                        const h2 s2 = {half_bits((uint16_t)buf[s].sb[r]), half_bits((uint16_t)buf[s].sb[r])};
+                        dequant8(buf[s].q[r], s2, v[r]);
+                    }
+                    lds_barrier();   // the previous unit's tiles are read
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        wl[32 * cc + 8 * j + i][nn] = wv[i].x;
-                        wl[32 * cc + 8 * j + i + 4][nn] = wv[i].y;
+                    for (int c = 0; c < 8; ++c) {   // column 8 o + c: rows 4 nq .. 4 nq + 3
+                        const int k = c & 3;
+                        const bool hi = c >= 4;
+                        const h2 r01 = {hi ? v[0][k].y : v[0][k].x, hi ? v[1][k].y : v[1][k].x};
+                        const h2 r23 = {hi ? v[2][k].y : v[2][k].x, hi ? v[3][k].y : v[3][k].x};
+                        const uint32_t col = 8 * o + c;
+                        *reinterpret_cast<u32x2*>(wl + dn_tile_pos(col, nq >> 1) + 4 * (nq & 1)) =
+                            u32x2{__builtin_bit_cast(uint32_t, r01), __builtin_bit_cast(uint32_t, r23)};
+                    }
+                    *reinterpret_cast<u32x2*>(&hl[hr][4 * hp]) = buf[s].hv;
+                    lds_barrier();
+                    const uint32_t col = 32 * w + (lane & 31);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t gr = 2 * j + (lane >> 5);
+                        const h8 ha = *reinterpret_cast<const h8*>(&hl[lane & 31][8 * gr]);
+                        const h8 wb = *reinterpret_cast<const h8*>(wl + dn_tile_pos(col, gr));
+                        acc = mfma32(ha, wb, acc);
                     }
                 }
-                *reinterpret_cast<u32x4*>(&hl[hr][8 * hp]) = buf[s].hv;
-                lds_barrier();
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const h8 ha = *reinterpret_cast<const h8*>(&hl[lane & 31][16 * j + 8 * (lane >> 5)]);
-                    const h8 wb = *reinterpret_cast<const h8*>(&wl[32 * w + (lane & 31)][16 * j + 8 * (lane >> 5)]);
-                    acc = mfma32(ha, wb, acc);
-                }
+                dense_dn_issue(a, b, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
             }
-            dense_dn_issue(a, b, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
         }
-    }
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -1691,7 +1750,7 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
             e = hipLaunchKernel(gate_up, dim3(2 * a.core_count), dim3(64 * kDenseGuWaves), kargs, 0, stream);
         if (e == hipSuccess)
             e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_down_kernel),
-                                dim3(a.width / kDenseCols * a.dsplits), dim3(kThreads), kargs, 0, stream);
+                                dim3(a.width / kDenseCols * a.dsplits), dim3(64 * kDenseDnWaves), kargs, 0, stream);
     } else {
         a.dsplits = 0;   // nothing to sum: y = 0
     }
