@@ -1434,14 +1434,31 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         issue_x(0, xq[0]);
         if (NI > 1) issue_x(1, xq[1]);
         u32x4 qg[NI], qu[NI];
-        uint32_t sgv[NI], suv[NI];
 #pragma unroll
         for (int t = 0; t < NI; ++t) {
             const uint32_t k0 = w * kq + 64 * t + 32 * hh;
             qg[t] = ld_cached16(wg + k0 / 2);   // a row's 128-byte line serves four steps
             qu[t] = ld_cached16(wu + k0 / 2);
-            sgv[t] = sg[k0 / 128];
-            suv[t] = su[k0 / 128];
+        }
+        // The wave's K range covers SB consecutive scale blocks of each row (step t uses
+        // block t / 2): one 8-byte load per projection row where SB is a multiple of 4.
+        constexpr int SB = NI >= 2 ? NI / 2 : 1;
+        uint32_t sgv[SB], suv[SB];
+        const uint32_t b0 = NI >= 2 ? w * SB : w / 2;
+        if constexpr (SB % 4 == 0) {
+#pragma unroll
+            for (int i = 0; i < SB; i += 4) {
+                const u32x2 gv = *reinterpret_cast<const u32x2*>(sg + b0 + i);
+                const u32x2 uv = *reinterpret_cast<const u32x2*>(su + b0 + i);
+                sgv[i] = gv.x & 0xffffu; sgv[i + 1] = gv.x >> 16; sgv[i + 2] = gv.y & 0xffffu; sgv[i + 3] = gv.y >> 16;
+                suv[i] = uv.x & 0xffffu; suv[i + 1] = uv.x >> 16; suv[i + 2] = uv.y & 0xffffu; suv[i + 3] = uv.y >> 16;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < SB; ++i) {
+                sgv[i] = sg[b0 + i];
+                suv[i] = su[b0 + i];
+            }
         }
         // keep every load above ahead of the first MFMA (the scheduler would otherwise
         // sink them next to their uses, leaving two or three in flight per wave)
@@ -1450,8 +1467,9 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         for (int t = 0; t < NI; ++t) {
             if (t + 2 < NI) issue_x(t + 2, xq[(t + 2) % 3]);
             __builtin_amdgcn_sched_barrier(0);
-            const h2 sg2 = {half_bits((uint16_t)sgv[t]), half_bits((uint16_t)sgv[t])};
-            const h2 su2 = {half_bits((uint16_t)suv[t]), half_bits((uint16_t)suv[t])};
+            const int sb = NI >= 2 ? t / 2 : 0;   // constant after unrolling
+            const h2 sg2 = {half_bits((uint16_t)sgv[sb]), half_bits((uint16_t)sgv[sb])};
+            const h2 su2 = {half_bits((uint16_t)suv[sb]), half_bits((uint16_t)suv[sb])};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const h8 xa = __builtin_bit_cast(h8, xq[t % 3][j]);   // paired (dense_x_kernel)
