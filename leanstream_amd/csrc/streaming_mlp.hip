@@ -51,6 +51,10 @@ constexpr int kWgPerCu = 2;          // resident workgroups per CU (register bud
 constexpr int kDnRows = 64;          // rows of one down-item pass: 8 row groups x 8 rows
 constexpr int kDescItems = 12;       // item descriptors fetched per round trip (5 words each)
 constexpr bool kSplitRoles = false;  // all-ready path: gate/up and down items on different workgroups
+#ifndef LS_GU_HALVES
+#define LS_GU_HALVES 1
+#endif
+constexpr bool kGuHalves = LS_GU_HALVES;  // one-pass gate/up items are loaded in two halves (GuHalf)
 static_assert(kDnCols == 256, "a down item is two scale blocks wide");
 
 // ---------------------------------------------------------------------------------
@@ -133,6 +137,15 @@ __device__ __forceinline__ void dequant8(uint32_t word, h2 s, h2 out[4]) {
 }
 
 __device__ __forceinline__ float dot2(h2 a, h2 b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+
+// Waits until every vector memory load this wave issued has returned (s_waitcnt vmcnt(0);
+// expcnt and lgkmcnt at their maxima). The scheduling barriers keep the loads after it
+// from being hoisted above the wait.
+__device__ __forceinline__ void wait_vector_loads() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // ---------------------------------------------------------------------------------
 // bounded waiting
@@ -301,6 +314,22 @@ struct GuItem {
     uint32_t s[GuGeom<D>::RPL][2][GuGeom<D>::CPL];   // fp16 bits (32-bit registers)
 };
 
+// Halves of a gate/up item, loaded one after the other: H = 1 is the first half, H = 2
+// the second, H = 0 the whole item. Items of several passes split by pass, one-pass items
+// (D >= 8192) by chunk. A wave issues the second half when the first has landed and
+// computes the first while the second streams, so only half an item's arithmetic is
+// left once the layer's last weight bytes arrive.
+template <int D, int H>
+struct GuHalf {
+    using Gm = GuGeom<D>;
+    static constexpr bool BY_PASS = Gm::RPL >= 2;
+    static constexpr int P0 = (H == 2 && BY_PASS) ? Gm::RPL / 2 : 0;
+    static constexpr int P1 = (H == 1 && BY_PASS) ? Gm::RPL / 2 : Gm::RPL;
+    static constexpr int K0 = (H == 2 && !BY_PASS) ? Gm::CPL / 2 : 0;
+    static constexpr int K1 = (H == 1 && !BY_PASS) ? Gm::CPL / 2 : Gm::CPL;
+    static_assert(BY_PASS || Gm::CPL >= 2, "an item splits by pass or by chunk");
+};
+
 // A wave-uniform pointer, in scalar registers: loads then take a scalar base plus a
 // 32-bit per-lane offset (the values are uniform; the compiler cannot always prove it).
 template <class T>
@@ -312,20 +341,21 @@ __device__ __forceinline__ T* uniform_ptr(T* p) {
 
 // Issue every load of a gate/up item: neurons n0 .. n0 + nvalid - 1 of the unit whose
 // packed bytes start at grp and scale rows at sc; pass p covers neurons n0 + p NPW + sub.
-// A full item (every neuron valid) needs no per-lane guard.
-template <int D>
+// A full item (every neuron valid) needs no per-lane guard. H selects the half (GuHalf).
+template <int D, int H>
 __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc, int n0, int nvalid, GuItem<D>& L) {
     using Gm = GuGeom<D>;
+    using Hf = GuHalf<D, H>;
     const int lane = lane_id();
     const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
     if (nvalid == Gm::NPI) {
 #pragma unroll
-        for (int p = 0; p < Gm::RPL; ++p) {
+        for (int p = Hf::P0; p < Hf::P1; ++p) {
             const uint8_t* row = uniform_ptr(grp + (size_t)(n0 + p * Gm::NPW) * (3 * D / 2));
             const uint16_t* srow = uniform_ptr(sc + (size_t)(n0 + p * Gm::NPW) * 3 * Gm::BLOCKS);
             const uint32_t wo = (uint32_t)sub * (3 * D / 2) + 16 * r, so = (uint32_t)sub * 3 * Gm::BLOCKS + (r >> 2);
 #pragma unroll
-            for (int k = 0; k < Gm::CPL; ++k) {
+            for (int k = Hf::K0; k < Hf::K1; ++k) {
                 L.w[p][0][k] = ld_stream16(row + wo + 16 * Gm::LPR * k);
                 L.w[p][1][k] = ld_stream16(row + wo + 16 * Gm::LPR * k + D / 2);
                 L.s[p][0][k] = srow[so + (Gm::LPR / 4) * k];
@@ -335,14 +365,14 @@ __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc,
         return;
     }
 #pragma unroll
-    for (int p = 0; p < Gm::RPL; ++p) {
+    for (int p = Hf::P0; p < Hf::P1; ++p) {
         const int nu = p * Gm::NPW + sub;
         const bool ok = nu < nvalid;
         const int n = n0 + (ok ? nu : 0);
         const uint8_t* row = grp + (size_t)n * (3 * D / 2);
         const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
 #pragma unroll
-        for (int k = 0; k < Gm::CPL; ++k) {
+        for (int k = Hf::K0; k < Hf::K1; ++k) {
             const int chunk = r + Gm::LPR * k;
             if (ok) {
                 L.w[p][0][k] = ld_stream16(row + 16 * chunk);
@@ -386,19 +416,16 @@ __device__ __forceinline__ float group_sum(float x) {
 // (the word is its own ready flag).
 // With NB > 1 the item's weights are dequantised once and multiplied with x of each of
 // the nb batch rows (xl: row 0; row b at xl + b N); h of row b goes to hrow + b G.
-template <int D, int NB>
-__device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, uint64_t* hrow, uint32_t G, int n0,
-                                           int nvalid, uint32_t seq, uint32_t nb) {
+// gu_dots adds the dot products of half H of the item (GuHalf) into acc; gu_finish
+// reduces and publishes.
+template <int D, int NB, int H>
+__device__ __forceinline__ void gu_dots(const GuItem<D>& L, const u32x4* xl, uint32_t nb,
+                                        float (&acc)[NB][GuGeom<D>::RPL][2]) {
     using Gm = GuGeom<D>;
-    const int lane = lane_id();
-    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
-    float acc[NB][Gm::RPL][2];
+    using Hf = GuHalf<D, H>;
+    const int r = lane_id() % Gm::LPR;
 #pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int p = 0; p < Gm::RPL; ++p) acc[b][p][0] = acc[b][p][1] = 0.f;
-#pragma unroll
-    for (int k = 0; k < Gm::CPL; ++k) {
+    for (int k = Hf::K0; k < Hf::K1; ++k) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             uint32_t xw[NB][4];
@@ -413,7 +440,7 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, 
                 }
             }
 #pragma unroll
-            for (int p = 0; p < Gm::RPL; ++p) {
+            for (int p = Hf::P0; p < Hf::P1; ++p) {
 #pragma unroll
                 for (int proj = 0; proj < 2; ++proj) {
                     const _Float16 sv = half_bits((uint16_t)L.s[p][proj][k]);
@@ -433,6 +460,14 @@ __device__ __forceinline__ void gu_compute(const GuItem<D>& L, const u32x4* xl, 
             }
         }
     }
+}
+
+template <int D, int NB>
+__device__ __forceinline__ void gu_finish(float (&acc)[NB][GuGeom<D>::RPL][2], uint64_t* hrow, uint32_t G, int n0,
+                                          int nvalid, uint32_t seq, uint32_t nb) {
+    using Gm = GuGeom<D>;
+    const int lane = lane_id();
+    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         if (NB > 1 && (uint32_t)b >= nb) break;
@@ -881,6 +916,14 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     // resident waves, which keeps the registers per wave low and leaves the loads of every
     // other wave to hide this one's compute. Gate/up items
     // come first in every wave's list.
+    // Gate/up items in two halves only at batch 1 where an item is one pass (D >= 8192):
+    // such layers give every wave several items, and the second half's loads overlap
+    // the first half's arithmetic (d=8192, 90 groups: 26.3 -> 26.0 us). With several
+    // passes per item (D <= 4096, at most one or two items per wave) the whole item stays
+    // in flight: halving the bytes in flight cost more than the overlap gained (d=4096,
+    // 58 groups: 14.4 -> 14.9 us); at batch 4 (four dot products per dequantised pair)
+    // the halves were 0.2 us slower.
+    constexpr bool halves = kGuHalves && NB == 1 && !GuHalf<D, 1>::BY_PASS;
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
@@ -898,7 +941,12 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         m.hrow = a.hbuf + (size_t)u.dest * nb * G;   // row 0 of the destination's h rows
         m.n0 = (int)((i - rel * ipu) * Gm::NPI);
         m.nvalid = min(Gm::NPI, (int)G - m.n0);
-        gu_issue<D>(u.grp, u.sc, m.n0, m.nvalid, gi);
+        m.grp = u.grp;
+        m.sc = u.sc;
+        if constexpr (halves)
+            gu_issue<D, 1>(u.grp, u.sc, m.n0, m.nvalid, gi);
+        else
+            gu_issue<D, 0>(u.grp, u.sc, m.n0, m.nvalid, gi);
         return true;
     };
     auto issue_dn = [&](uint32_t k, DnItem& di, ItemMeta& m) -> bool {
@@ -917,9 +965,22 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         if (FUSED && !ep.known && lane_id() == 0) early = ld_agent(slot + kSyncEpoch);
         return true;
     };
-    auto compute_gu = [&](uint32_t k, const GuItem<D>& gi, const ItemMeta& m) {
+    auto compute_gu = [&](uint32_t k, GuItem<D>& gi, const ItemMeta& m) {
         if (a.first_compute && m.n0 == 0 && lane_id() == 0) a.first_compute[m.dest] = now_ticks();
-        gu_compute<D, NB>(gi, xl, m.hrow, G, m.n0, m.nvalid, a.seq, nb);
+        float acc[NB][Gm::RPL][2];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int p = 0; p < Gm::RPL; ++p) acc[b][p][0] = acc[b][p][1] = 0.f;
+        if constexpr (halves) {
+            wait_vector_loads();   // the first half has landed: the second goes out now
+            gu_issue<D, 2>(m.grp, m.sc, m.n0, m.nvalid, gi);
+            gu_dots<D, NB, 1>(gi, xl, nb, acc);
+            gu_dots<D, NB, 2>(gi, xl, nb, acc);
+        } else {
+            gu_dots<D, NB, 0>(gi, xl, nb, acc);
+        }
+        gu_finish<D, NB>(acc, m.hrow, G, m.n0, m.nvalid, a.seq, nb);
         if (k == 0) stamp(a, kStampFirstData);
     };
     auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
