@@ -198,7 +198,7 @@ struct GuGeom {
 };
 
 // x (every batch row) is shared by the workgroup through LDS, as (k, k+4) fp16 pairs to
-// match dequant8, in the order gu_compute reads it: block (k, g) of lane r (words
+// match dequant8, in the order gu_dots reads it: block (k, g) of lane r (words
 // 4g .. 4g+3 of its chunk k, x columns 32 (r + LPR k) + 8g .. + 7) of row b at
 // xl[b N + (4k + g) LPR + r], so a wave's 64 lanes read 1 KB of consecutive LDS per block.
 // Each wave loads a quarter of row 0 as raw 16-byte pieces into registers at its start,
