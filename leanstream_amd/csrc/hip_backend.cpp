@@ -1,7 +1,7 @@
 // HipBackend: the MI355X ComputeBackend for the streaming sparse INT4 MLP.
 // Cold path (bind): validation, geometry choice, occupancy query, device sync state.
 // Hot path (enqueue): O(1) candidate selection + one (fused) or three (split) launches
-// + one completion event, all on the caller's stream.
+// on the caller's stream; completion is proven by the kernels' own host-coherent words.
 #include "leanstream/hip_backend.h"
 #include <hip/hip_runtime_api.h>
 #include <algorithm>
@@ -17,7 +17,7 @@ struct HipBackend::Impl {
     lsamd::Bounds bounds{};
     uint32_t* sync = nullptr;
     uint32_t* qmirror = nullptr;  // device copy of published queue descriptors
-    unsigned long long* yacc = nullptr;  // packed fixed-point column accumulators [2][d]
+    unsigned long long* yacc = nullptr;  // packed fixed-point column accumulators [2][rows][d][kAccStride]
     uint32_t slot_words = 0;
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
@@ -80,7 +80,7 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     p.slot_words = lsamd::sync_slot_words(units_cap);
     hipError_t e = hipMalloc(&p.sync, sizeof(uint32_t) * 2 * p.slot_words);
     if (e == hipSuccess) e = hipMalloc(&p.qmirror, sizeof(uint32_t) * 5 * std::max<uint32_t>(1, b.queue_capacity));
-    if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * rows);
+    if (e == hipSuccess) e = hipMalloc(&p.yacc, sizeof(long long) * 2 * b.width * rows * lsamd::kAccStride);
     if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&p.status), 64, hipHostMallocCoherent | hipHostMallocMapped);
     if (e == hipSuccess && !b.hidden)
         e = hipMalloc(&p.owned_hidden, sizeof(uint64_t) * b.slot_capacity * rows * b.group_size);
@@ -97,13 +97,16 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     int dev = 0;
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntryFused, static_cast<int>(rows), &p.per_cu_fused);
-    if (e == hipSuccess) e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(rows), &p.per_cu_split);
+    const int gs = static_cast<int>(b.group_size);
+    if (e == hipSuccess)
+        e = lsamd::resident_workers(b.width, lsamd::kEntryFused, static_cast<int>(rows), gs, &p.per_cu_fused);
+    if (e == hipSuccess)
+        e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(rows), gs, &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
         e = hipErrorInvalidConfiguration;
     uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
     if (e == hipSuccess)
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * rows, hbuf,
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * rows * lsamd::kAccStride, hbuf,
                               b.slot_capacity * rows * b.group_size, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -181,7 +184,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     // before the sequence wraps) zeroes every tag, so no stored tag can match a later one.
     const uint32_t rows = p.dense ? 1u : p.buf.batch;
     if (p.needs_clear || p.seq == UINT32_MAX) {
-        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * rows, a.hbuf,
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * rows * lsamd::kAccStride, a.hbuf,
                               p.buf.slot_capacity * rows * p.buf.group_size, hs);
         if (e != hipSuccess) return static_cast<int>(e);
         p.needs_clear = false;

@@ -42,6 +42,10 @@ constexpr long long kAccBias = 1ll << 39;
 constexpr unsigned long long kAccOne = 1ull << 52;
 constexpr unsigned long long kAccValueMask = kAccOne - 1;
 constexpr uint32_t kMaxRowsReduced = 4095;
+// 64-bit words between consecutive column accumulators. Dense (1): a wave's 64-column
+// atomic instruction is four line requests; one line per column made it 64 requests and
+// a Ministral-8B layer twice as slow (the atomics are bound by request count).
+constexpr uint32_t kAccStride = 1;
 constexpr uint32_t kDnCols = 256;  // columns of one down-projection item (two scale blocks)
 constexpr uint32_t kMaxBatch = 4;  // batch rows of one launch (x of every row is kept in LDS)
 constexpr uint32_t kMaxDenseBatch = 32;   // batch rows of the dense (matrix-core) path
@@ -49,12 +53,21 @@ constexpr uint32_t kDenseSplits = 16;     // unit splits of its down projection
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
-// Phase stamps written by thread 0 of each worker when MlpArgs::stamps is set.
+// Phase stamps (100 MHz clock) written by lane 0 of every wave when MlpArgs::stamps is
+// set: stamps[(block * 4 + wave) * kStampSlots + phase]; 0 = the wave never got there.
 constexpr uint32_t kStampSlots = 32;
 enum StampPhase : uint32_t {
-    kStampEntry = 0, kStampXLoaded = 1, kStampCoreDone = 2, kStampEpoch = 3, kStampQueueDone = 4,
-    kStampFirstData = 5,   // first gate/up item computed (wave 0)
-    kStampDnComputed = 8,  // first down item computed (wave 0)
+    kStampEntry = 0,
+    kStampDescs = 1,         // the wave's first descriptors have arrived
+    kStampCoreDone = 2, kStampEpoch = 3, kStampQueueDone = 4,
+    kStampFirstData = 5,     // first item's weights have landed (staged walk)
+    kStampFirstDone = 6,     // first gate/up item computed, h published
+    kStampSecondData = 7,    // second item's weights have landed (staged walk)
+    kStampHReady = 8,        // first down item: h of its unit complete
+    kStampDnComputed = 9,    // first down item computed (atomics issued next)
+    kStampDrained = 10,      // last column additions returned
+    kStampMirrorEpoch = 12,  // mirror: epoch word published
+    kStampMirrorDone = 13,   // mirror: every worker counted out
     kStampExit = 31,
 };
 
@@ -82,7 +95,8 @@ struct MlpArgs {
     const uint16_t* scales;       // fp16 [(physical*G + n)*3 + proj][d/128]
     uint64_t* hbuf;               // [slot][batch][G] h = fp16(silu(g)*u) as fp32 bits | launch seq << 32
     float* partial;               // unused by the fixed-point reduction (kept in the buffer block)
-    unsigned long long* yacc;     // [2][batch][d] packed accumulators (see kAccOne), buffer (seq & 1) per launch
+    unsigned long long* yacc;     // [2][batch][d][kAccStride] packed accumulators (see kAccOne), buffer (seq & 1)
+                                  // per launch
     uint16_t* y;                  // fp16 [batch][d]
     float* y32;                   // optional fp32 [batch][d] pre-rounding output
     uint32_t* executions;         // optional per-destination execution counters

@@ -14,8 +14,9 @@ struct LaunchPlan {
 };
 
 bool variant_available(int width);
-// Maximum co-resident workgroups per CU for the kernels of an entry point.
-hipError_t resident_workers(int width, int entry_point, int batch, int* per_cu);
+// Maximum co-resident workgroups per CU for the kernels of an entry point (the kernel
+// family depends on the batch and, at batch 1, on the group size).
+hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
 hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
 // Dense batched path (batch > kMaxBatch, core units only): gate/up -> down -> reduction.

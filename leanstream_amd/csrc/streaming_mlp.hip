@@ -157,7 +157,8 @@ struct Waiter {
 };
 
 __device__ __forceinline__ void stamp(const MlpArgs& a, uint32_t k) {
-    if (a.stamps && threadIdx.x == 0 && k < kStampSlots) a.stamps[blockIdx.x * kStampSlots + k] = now_ticks();
+    if (a.stamps && (threadIdx.x & 63) == 0 && k < kStampSlots)
+        a.stamps[(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kStampSlots + k] = now_ticks();
 }
 
 __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, uint32_t bit) {
@@ -643,7 +644,6 @@ __device__ __forceinline__ Unit resolve(const MlpArgs& a, const Bounds& b, ExecD
 struct Shared {
     alignas(16) uint16_t hs[kWaves][kDnRows];
     alignas(16) uint16_t ss[kWaves][2 * kDnRows];
-    alignas(16) float red[kWaves][kDnCols];   // a down item's column sums, re-dealt for the atomics
     uint32_t word[8];
     uint32_t wpath[kWaves];
     uint32_t wfail[kWaves];
@@ -695,6 +695,11 @@ __device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned
     a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+// The accumulator buffer of this launch (two alternate between consecutive launches).
+__device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) {
+    return a.yacc + (size_t)(a.seq & 1) * a.width * a.batch * kAccStride;
+}
+
 // One contribution of a column value: round(v * 2^20) biased by 2^39, count 1 in the
 // top field. Out-of-range values are clipped and reported.
 __device__ __forceinline__ unsigned long long acc_term(const MlpArgs& a, uint32_t* slot, float value) {
@@ -731,7 +736,8 @@ __device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, un
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned long long t = acc_term(a, slot, c[i]);
-        n[i] = __hip_atomic_fetch_add(yacc + col + 64 * i, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t;
+        n[i] = __hip_atomic_fetch_add(yacc + (size_t)(col + 64 * i) * kAccStride, t, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) + t;
     }
     check_pending(a, pd, U);
 #pragma unroll
@@ -877,7 +883,7 @@ struct ItemMeta {
 // of this wave), so every h is eventually published. With FUSED, the U-th contribution
 // of a column writes the output (U = core + queue units, learnt from the epoch word).
 template <int D, bool FUSED, int NB>
-__device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint32_t* slot, const Bounds& b,
+__device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x4* stage, uint32_t* slot, const Bounds& b,
                                               unsigned long long* yacc, XPart<D>& xp, u32x4* xl, Epoch& ep,
                                               uint32_t early, Pending& pd, uint32_t u0, uint32_t u1,
                                               const WaveRole& role) {
@@ -1002,7 +1008,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
         // re-deal through LDS: lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds
         // columns l + 64 i
         const int lane = lane_id();
-        float* red = sh.red[wave];
+        float* red = reinterpret_cast<float*>(stage) + wave * kDnCols;
         *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
@@ -1022,6 +1028,327 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, uint
     for (uint32_t k = KG; k < K; ++k) {
         if (!issue_dn(k, di, m)) return false;
         if (!compute_dn(k, di, m)) return false;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------------
+// Staged item walk (64-neuron groups, batch 1). Every item is 8 KB of weights -- a gate/up
+// item's RPL x 2 x CPL 16-byte pieces per lane, or a down item's 8 row pieces per lane --
+// plus one 256-byte block of its scales, and is loaded into one of the wave's two LDS
+// slots with global_load_lds, which takes no registers. A wave keeps two items in
+// flight: item k + 1 streams in while item k is computed. At the Ministral-8B shape
+// (at most one gate/up and one down item per wave) every byte of the layer is requested
+// as soon as the wave's descriptors arrive, so the layer's HBM stream is one phase.
+//
+// Each item is exactly kStageOps load instructions, all into LDS (the compiler tracks no
+// register result of them), so `s_waitcnt vmcnt(kStageOps)` before computing item k waits
+// for item k and everything issued before it, and leaves item k + 1 in flight.
+// ---------------------------------------------------------------------------------
+constexpr uint32_t kStagedGroup = 64;              // neurons per group of the staged kernels
+// Widths whose staged kernels keep two workgroups per CU (slots + x + Shared <= 80 KB).
+constexpr bool staged_width(int width) { return width <= 4096; }
+constexpr int kSlotVecs = 512;                     // 16-byte weight pieces of one item
+constexpr int kSlotStride = kSlotVecs + 16;        // + 256 bytes of scales
+constexpr int kStageOps = 9;                       // load instructions per item
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// 16 / 4 bytes per lane into LDS: lane l's piece lands at block + 16 l (4 l). Weights are
+// read once: non-temporal.
+__device__ __forceinline__ void lds_load16(const void* g, u32x4* block) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr)block, 16, 0, 2);
+}
+__device__ __forceinline__ void lds_load4(const void* g, u32x4* block) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr)block, 4, 0, 0);
+}
+
+// vmcnt(N) with the other counters at their maxima; the scheduling barriers keep the LDS
+// reads of the awaited item below it.
+template <int N>
+__device__ __forceinline__ void wait_loads_but() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+    __builtin_amdgcn_sched_barrier(0);
+}
+// Waits until piece group j (of GROUPS, two loads each, issued after the item's scale
+// block) has landed: at most 2 (GROUPS - 1 - j) of the item's loads are outstanding.
+template <int GROUPS>
+__device__ __forceinline__ void constexpr_wait_group(int j) {
+    static_assert(GROUPS == 4, "gate/up items are four piece groups");
+    switch (j) {
+        case 0: wait_loads_but<6>(); break;
+        case 1: wait_loads_but<4>(); break;
+        case 2: wait_loads_but<2>(); break;
+        default: wait_loads_but<0>(); break;
+    }
+}
+
+// lgkmcnt(0): this wave's LDS reads of a slot are complete before new pieces land in it.
+__device__ __forceinline__ void wait_lds_reads() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Gate/up item: neurons n0 .. n0 + NPI - 1 of the unit at grp / sc. Piece (p, proj, k) of
+// lane l lands at slot[((p 2 + proj) CPL + k) 64 + l]; the scale block holds, per neuron,
+// its B gate then its B up scales (B = D / 128: NPI x 2B fp16 = 256 bytes), lane l loading
+// the l-th 32-bit word. Issue order: the scale block, then piece groups j = k RPL + p
+// (gate piece, up piece), the order in which gu_dots_staged consumes them, so group j has
+// landed once at most 2 (groups - 1 - j) of the item's loads are outstanding.
+template <int D>
+__device__ __forceinline__ void gu_stage(const uint8_t* grp, const uint16_t* sc, int n0, u32x4* sl) {
+    using Gm = GuGeom<D>;
+    constexpr int B = D / 128;
+    static_assert(Gm::NPI * B == 64, "one 32-bit scale word per lane");
+    static_assert(2 * Gm::RPL * Gm::CPL + 1 == kStageOps, "an item is kStageOps loads");
+    const int lane = lane_id();
+    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+    const uint16_t* srow = uniform_ptr(sc + (size_t)n0 * 3 * B);
+    lds_load4(srow + (uint32_t)(lane / B) * 3 * B + 2 * (lane % B), sl + kSlotVecs);
+    const uint32_t wo = (uint32_t)sub * (3 * D / 2) + 16 * r;
+#pragma unroll
+    for (int k = 0; k < Gm::CPL; ++k) {
+#pragma unroll
+        for (int p = 0; p < Gm::RPL; ++p) {
+            const uint8_t* row = uniform_ptr(grp + (size_t)(n0 + p * Gm::NPW) * (3 * D / 2));
+            lds_load16(row + wo + 16 * Gm::LPR * k, sl + ((p * 2 + 0) * Gm::CPL + k) * 64);
+            lds_load16(row + wo + 16 * Gm::LPR * k + D / 2, sl + ((p * 2 + 1) * Gm::CPL + k) * 64);
+        }
+    }
+}
+
+// Down item: tile `tile` (256 columns) of the unit's 64 rows. Lane 8 g + dc's piece j is
+// row 8 g + j, columns 32 dc .. 32 dc + 31, at slot[j 64 + l]; the scale block holds the
+// tile's two scales of row l in word l.
+template <int D>
+__device__ __forceinline__ void dn_stage(const uint8_t* grp, const uint16_t* sc, int tile, u32x4* sl) {
+    constexpr int B = D / 128;
+    constexpr int RB = 3 * D / 2;
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const uint16_t* srow = uniform_ptr(sc + 2 * B + 2 * tile);
+    lds_load4(srow + (uint32_t)lane * 3 * B, sl + kSlotVecs);
+    const uint8_t* base = uniform_ptr(grp + D + tile * (kDnCols / 2));
+    const uint32_t wo = (uint32_t)(8 * g) * RB + dc * 16;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lds_load16(base + wo + j * RB, sl + j * 64);
+}
+
+// gu_dots of a staged item (batch 1): the same arithmetic, pieces and scales from LDS,
+// consumed group by group as they land (the item is the newest load of the wave, or loads
+// issued after it are stores). `last` runs once the final group has landed, before it is
+// computed (the wave issues its next item there).
+template <int D, class Last>
+__device__ __forceinline__ void gu_dots_staged(const u32x4* sl, const u32x4* xl, float (&acc)[1][GuGeom<D>::RPL][2],
+                                               Last&& last) {
+    using Gm = GuGeom<D>;
+    constexpr int B = D / 128;
+    constexpr int GROUPS = Gm::RPL * Gm::CPL;
+    const int lane = lane_id();
+    const int r = lane % Gm::LPR, sub = lane / Gm::LPR;
+    const uint16_t* scl = reinterpret_cast<const uint16_t*>(sl + kSlotVecs);
+#pragma unroll
+    for (int k = 0; k < Gm::CPL; ++k) {
+        uint32_t xw[4][4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const u32x4 xv = xl[(4 * k + g) * Gm::LPR + r];   // paired (stage_x)
+            xw[g][0] = xv.x;
+            xw[g][1] = xv.y;
+            xw[g][2] = xv.z;
+            xw[g][3] = xv.w;
+        }
+#pragma unroll
+        for (int p = 0; p < Gm::RPL; ++p) {
+            constexpr_wait_group<GROUPS>(k * Gm::RPL + p);
+            if (k * Gm::RPL + p == GROUPS - 1) last();
+            u32x4 v[2];
+            h2 s2[2];
+#pragma unroll
+            for (int proj = 0; proj < 2; ++proj) {
+                v[proj] = sl[((p * 2 + proj) * Gm::CPL + k) * 64 + lane];
+                const _Float16 sv = half_bits(scl[(p * Gm::NPW + sub) * 2 * B + proj * B + ((r + Gm::LPR * k) >> 2)]);
+                s2[proj] = h2{sv, sv};
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+#pragma unroll
+                for (int proj = 0; proj < 2; ++proj) {
+                    const uint32_t words[4] = {v[proj].x, v[proj].y, v[proj].z, v[proj].w};
+                    h2 w[4];
+                    dequant8(words[g], s2[proj], w);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) acc[0][p][proj] = dot2(w[q], as_h2(xw[g][q]), acc[0][p][proj]);
+                }
+            }
+            // the group's products are computed here, before the next group's wait (the
+            // compiler would otherwise sink them below the last wait)
+            asm volatile("" : "+v"(acc[0][p][0]), "+v"(acc[0][p][1]));
+        }
+    }
+}
+
+// dn_accumulate of a staged item: row pieces and scales from LDS, h from `h` (row lane).
+__device__ __forceinline__ void dn_accumulate_staged(const u32x4* sl, uint64_t h, uint16_t* hs, uint16_t* ss,
+                                                     float acc[32]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const uint32_t s = reinterpret_cast<const uint32_t*>(sl + kSlotVecs)[lane];
+    hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)h));   // exact: h is fp16
+    ss[lane] = (uint16_t)s;
+    ss[kDnRows + lane] = (uint16_t)(s >> 16);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + kDnRows * (dc >> 2) + 8 * g);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const u32x4 wa = sl[(2 * p) * 64 + lane], wb = sl[(2 * p + 1) * 64 + lane];
+        const h2 hab = as_h2(hw[p]), sab = as_h2(sw[p]);
+        const uint32_t xa[4] = {wa.x, wa.y, wa.z, wa.w}, xb[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h2 w[4];
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);   // columns 8q + 4..7
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
+        }
+    }
+}
+
+// This wave's items of units [u0, u1) through its two LDS slots (stage: kWaves x 2 slots).
+// Same item lists, waits and reduction as process_items.
+template <int D, bool FUSED>
+__device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& sh, u32x4* stage, uint32_t* slot,
+                                                     const Bounds& b, unsigned long long* yacc, XPart<D>& xp,
+                                                     u32x4* xl, Epoch& ep, uint32_t early, Pending& pd, uint32_t u0,
+                                                     uint32_t u1, const WaveRole& role) {
+    using Gm = GuGeom<D>;
+    constexpr uint32_t T = D / kDnCols;
+    constexpr uint32_t G = kStagedGroup;
+    constexpr uint32_t ipu = G / Gm::NPI;   // gate/up items per unit
+    const uint32_t nu = u1 - u0;
+    const uint32_t NG = nu * ipu;
+    const ItemList il = make_items(role, NG, nu * T);
+    const uint32_t K = il.K, KG = il.KG;
+    auto leave = [&](bool r) -> bool {
+        stage_x<D>(xp, 1u, xl, &sh.xcount);
+        return r;
+    };
+    if (!K) return leave(true);
+    uint32_t seen = 0, word = 0, k0 = 0;
+    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, 1u, word)) return leave(false);
+    if (a.stamps) {
+        asm volatile("" : : "v"(word));   // the stamp waits for the descriptors
+        stamp(a, kStampDescs);
+    }
+    stage_x<D>(xp, 1u, xl, &sh.xcount);
+    const int wave = wave_id();
+    const int lane = lane_id();
+    uint16_t* hs = sh.hs[wave];
+    uint16_t* ss = sh.ss[wave];
+    u32x4* const sl0 = stage + (2 * wave) * kSlotStride;
+    u32x4* const sl1 = sl0 + kSlotStride;
+    ItemMeta m0, m1;
+    uint32_t U = 0;
+    bool have_u = !FUSED;
+
+    auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
+        if (k - k0 >= (uint32_t)kDescItems) {
+            k0 = k;
+            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, 1u, word))
+                return false;
+        }
+        return unit_of(a, slot, b, word, k - k0, D, u);
+    };
+    auto issue = [&](uint32_t k, u32x4* sl, ItemMeta& m) -> bool {
+        Unit u;
+        if (!fetch_unit(k, u)) return false;
+        wait_lds_reads();   // the slot's previous item is no longer being read
+        m.grp = u.grp;
+        m.sc = u.sc;
+        m.dest = u.dest;
+        m.hrow = a.hbuf + (size_t)u.dest * G;
+        if (k < KG) {
+            const uint32_t i = il.item(k), rel = i / ipu;
+            m.n0 = (int)((i - rel * ipu) * Gm::NPI);
+            gu_stage<D>(u.grp, u.sc, m.n0, sl);
+        } else {
+            const uint32_t d = il.item(k) - NG, rel = d / T;
+            m.unit = u0 + rel;
+            m.tile = d - rel * T;
+            dn_stage<D>(u.grp, u.sc, (int)m.tile, sl);
+        }
+        return true;
+    };
+    // next: issues the wave's next item once this one's last piece group has landed
+    auto compute_gu = [&](uint32_t k, const u32x4* sl, const ItemMeta& m, auto&& next) -> bool {
+        if (k == 0 && !wait_x(a, slot, &sh.xcount)) return false;
+        if (a.first_compute && m.n0 == 0 && lane == 0) a.first_compute[m.dest] = now_ticks();
+        float acc[1][Gm::RPL][2];
+#pragma unroll
+        for (int p = 0; p < Gm::RPL; ++p) acc[0][p][0] = acc[0][p][1] = 0.f;
+        bool ok = true;
+        gu_dots_staged<D>(sl, xl, acc, [&]() {
+            if (k < 2) stamp(a, k == 0 ? kStampFirstData : kStampSecondData);
+            ok = next();
+        });
+        if (!ok) return false;
+        gu_finish<D, 1>(acc, m.hrow, G, m.n0, Gm::NPI, a.seq, 1u);
+        if (k == 0) stamp(a, kStampFirstDone);
+        return true;
+    };
+    auto compute_dn = [&](uint32_t k, u32x4* sl, const ItemMeta& m) -> bool {
+        if (!have_u) {
+            if (!await_epoch(a, slot, ep, early)) return false;
+            U = a.core_count + ep.total;
+            have_u = true;
+        }
+        DnItem it;
+        it.h = ld_agent_u64(uniform_ptr(m.hrow) + lane);
+        if (!dn_wait_h(a, slot, m.hrow, (int)G, 0, it)) return false;
+        if (k == KG) stamp(a, kStampHReady);
+        float acc[32];
+#pragma unroll
+        for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+        dn_accumulate_staged(sl, it.h, hs, ss, acc);
+        float cs[4];
+        dn_reduce(acc, cs);
+        // re-deal through the slot just consumed (its pieces are in registers by now):
+        // lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds columns l + 64 i
+        float* red = reinterpret_cast<float*>(sl);
+        *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cs[i] = red[lane + 64 * i];
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + lane, cs, U, pd);
+        if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
+        if (k == KG) stamp(a, kStampDnComputed);
+        return true;
+    };
+    // Item k sits in slot sl. A gate/up item is computed group by group as its pieces
+    // land; item k + 1 goes out into the other slot once item k has landed, and streams
+    // while item k's last group (gate/up) or the whole down item is computed.
+    auto step = [&](uint32_t k, u32x4* sl, ItemMeta& m, u32x4* nsl, ItemMeta& nm) -> bool {
+        auto next = [&]() -> bool { return k + 1 >= K || issue(k + 1, nsl, nm); };
+        // a down item after the wave's last gate/up item waits until that item is computed:
+        // its bytes are not needed before h, and issued earlier they compete with the
+        // gate/up bytes still streaming, which h waits for
+        if (k + 1 == KG) return compute_gu(k, sl, m, [] { return true; }) && next();
+        if (k < KG) return compute_gu(k, sl, m, next);
+        wait_loads_but<0>();
+        if (k < 2) stamp(a, k == 0 ? kStampFirstData : kStampSecondData);
+        return next() && compute_dn(k, sl, m);
+    };
+    if (!issue(0, sl0, m0)) return false;
+    for (uint32_t k = 0; k < K; k += 2) {
+        if (!step(k, sl0, m0, sl1, m1)) return false;
+        if (k + 1 < K && !step(k + 1, sl1, m1, sl0, m0)) return false;
     }
     return true;
 }
@@ -1076,6 +1403,7 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
         uint32_t path = 0;
         if (state == 1 && total) path = ld_sys(&a.control->ready_count) >= total ? 2u : 1u;
         st_agent(slot + kSyncEpoch, pack_epoch(state, path, state == 1 ? total : 0u));
+        stamp(a, kStampMirrorEpoch);
     }
     state = wave_bcast(state);
     total = wave_bcast(total);
@@ -1177,15 +1505,16 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
 // which its four waves share. Every range goes through the one call of
 // process_items below, so the item loop exists once in the kernel's code (one copy per
 // range kind would triple the code and raise the register count).
-template <int D, bool FUSED, bool CORE, bool QUEUE, int NB>
-__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, uint32_t* slot) {
+template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, bool STAGED>
+__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, u32x4* stage,
+                                       uint32_t* slot) {
     const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
     const uint32_t wave = wave_id();
     // Roles by workgroup: the first gu_wgs workgroups take the gate/up items, the others
     // the down items (one workgroup alone takes both).
     const uint32_t gu_wgs = kSplitRoles && W >= 2 ? (W + 1) / 2 : 0;
     const WaveRole role{blockIdx.x * kWaves + wave, W * kWaves, gu_wgs * kWaves};
-    unsigned long long* yacc = a.yacc + (a.seq & 1) * a.width * a.batch;
+    unsigned long long* yacc = launch_acc(a);
     XPart<D> xp;
     const uint32_t xrows = NB == 1 ? 1u : a.batch;   // the NB = 1 kernels hold one row of x
     load_x<D>(a.x, xrows, xp, xl);
@@ -1195,14 +1524,14 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
     bool ok = true;
     enum : uint32_t { kCore, kDecide, kClaim, kDone };
-    uint32_t stage = CORE ? kCore : kDecide;
+    uint32_t phase = CORE ? kCore : kDecide;
     for (;;) {
         uint32_t u0 = 0, u1 = 0, e = early;
         WaveRole r = role;
-        if (stage == kCore) {
+        if (phase == kCore) {
             u1 = a.core_count;
-            stage = kDecide;
-        } else if (stage == kDecide) {
+            phase = kDecide;
+        } else if (phase == kDecide) {
             stamp(a, kStampCoreDone);
             if (!QUEUE) break;
             ok = ok && await_epoch(a, slot, ep, early);
@@ -1220,14 +1549,14 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             if (path == 2 || (path == 1 && a.claim_batch == 0)) {
                 u0 = a.core_count;
                 u1 = u0 + ep.total;
-                stage = kDone;
+                phase = kDone;
             } else if (path == 1) {
-                stage = kClaim;
+                phase = kClaim;
                 continue;
             } else {
                 break;
             }
-        } else if (stage == kClaim) {
+        } else if (phase == kClaim) {
             const uint32_t got = claim_pair(a, sh, slot, ep.total, ok);
             if (!got) break;
             u0 = a.core_count + __builtin_amdgcn_readfirstlane(sh.word[5]);
@@ -1237,11 +1566,20 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
         } else {
             break;
         }
-        if (u1 > u0) ok = process_items<D, FUSED, NB>(a, sh, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+        if (u1 > u0) {
+            if constexpr (STAGED)
+                ok = process_items_staged<D, FUSED>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+            else
+                ok = process_items<D, FUSED, NB>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+        }
     }
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     if (QUEUE) stamp(a, kStampQueueDone);
     check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
+    if (a.stamps) {
+        drain_vmem();
+        stamp(a, kStampDrained);
+    }
 }
 
 // The mirror workgroup: wave 0 mirrors the queue while waves 1..3 clear what the next
@@ -1255,8 +1593,8 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
     const uint32_t t = threadIdx.x - 64, n = kThreads - 64;
     uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
     for (uint32_t i = t; i < a.slot_words; i += n) st_agent(other + i, 0u);
-    unsigned long long* other_acc = a.yacc + ((a.seq + 1) & 1) * a.width * a.batch;
-    for (uint32_t i = t; i < a.width * a.batch; i += n) st_agent_u64(other_acc + i, 0ull);
+    unsigned long long* other_acc = a.yacc + (size_t)((a.seq + 1) & 1) * a.width * a.batch * kAccStride;
+    for (uint32_t i = t; i < a.width * a.batch; i += n) st_agent_u64(other_acc + (size_t)i * kAccStride, 0ull);
 }
 
 // Completion proof of a fused launch (replaces a per-launch event). Every worker
@@ -1265,9 +1603,12 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
 // than an eighth of the increments), and leaves at once. The mirror workgroup, after
 // mirroring the queue, polls the eight counters; when every worker is out it stores the
 // launch sequence into the host-coherent completion word. All reads of the launch's
-// weights and all writes of its outputs are complete by then.
+// weights and all writes of its outputs are complete by then. (One host store per launch:
+// a sign-off per workgroup into host memory made every launch wait for hundreds of PCIe
+// writes at its end.)
 __device__ __forceinline__ void count_out(uint32_t* slot) {
-    __syncthreads();   // the barrier waits for the workgroup's outstanding stores and atomics
+    drain_vmem();      // this wave's loads have returned, its stores and atomics are acknowledged
+    __syncthreads();   // every wave of the workgroup has drained
     if (threadIdx.x == 0)
         (void)__hip_atomic_fetch_add(slot + kSyncExitGroups + (blockIdx.x % 8u) * kLine, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -1286,6 +1627,7 @@ __device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, 
         }
         __builtin_amdgcn_s_sleep(1);
     }
+    stamp(a, kStampMirrorDone);
     if (lane == 0) __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
@@ -1303,20 +1645,26 @@ __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) 
         __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ unsigned long long* launch_acc(const MlpArgs& a) {
-    return a.yacc + (a.seq & 1) * a.width * a.batch;
-}
 
 // ---------------------------------------------------------------------------------
 // Kernels. Persistent launches have gridDim.x = workers + 1; the last block mirrors.
 // ---------------------------------------------------------------------------------
 
+// LDS of a persistent workgroup beyond Shared and x: the staged kernels' item slots
+// (kWaves x 2), or the other kernels' per-wave re-deal rows of the down items.
+template <bool STAGED>
+struct StageArea {
+    static constexpr int VECS = STAGED ? 2 * kWaves * kSlotStride : kWaves * kDnCols / 4;
+};
+
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
-template <int D, int NB>
+template <int D, int NB, bool STAGED>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs a, Bounds b) {
+    static_assert(!STAGED || NB == 1, "the staged walk serves batch 1");
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
+    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1326,28 +1674,30 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs
         if (threadIdx.x < 64) await_workers(a, slot, gridDim.x - 1);
     } else {
         stamp(a, kStampEntry);
-        worker<D, true, true, true, NB>(a, b, sh, xl, slot);
+        worker<D, true, true, true, NB, STAGED>(a, b, sh, xl, stage, slot);
         stamp(a, kStampExit);
         count_out(slot);
     }
 }
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
-template <int D, int NB>
+template <int D, int NB, bool STAGED>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
+    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
-    worker<D, false, true, false, NB>(a, b, sh, xl, slot);
+    worker<D, false, true, false, NB, STAGED>(a, b, sh, xl, stage, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
-template <int D, int NB>
+template <int D, int NB, bool STAGED>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, Bounds b) {
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
+    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
     if (threadIdx.x == 0) sh.xcount = 0;
     __syncthreads();
@@ -1356,7 +1706,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, 
         run_mirror(a, slot, pre);
         return;
     }
-    worker<D, false, false, true, NB>(a, b, sh, xl, slot);
+    worker<D, false, false, true, NB, STAGED>(a, b, sh, xl, stage, slot);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
@@ -1364,7 +1714,8 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, 
 template <int D>
 __global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
     const int col = blockIdx.x * kThreads + threadIdx.x;
-    const unsigned long long w = __hip_atomic_load(launch_acc(a) + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long w =
+        __hip_atomic_load(launch_acc(a) + (size_t)col * kAccStride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     write_output(a, col, w, (uint32_t)(w >> 52));
     finish_launch(a, a.sync + (a.seq & 1) * a.slot_words);   // last kernel of the split launch sequence
 }
@@ -1374,7 +1725,7 @@ __global__ __launch_bounds__(kThreads) void reduce_kernel(MlpArgs a) {
 // a sequence number the next launches use.
 __global__ void clear_sync_kernel(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns,
                                   uint64_t* hbuf, uint32_t hwords) {
-    // `columns` covers both accumulator buffers
+    // `columns` covers both accumulator buffers, padding included
     const uint32_t stride = gridDim.x * blockDim.x;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < words; i += stride) st_agent(sync + i, 0u);
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < columns; i += stride) st_agent_u64(yacc + i, 0ull);
@@ -1732,20 +2083,52 @@ namespace {
 
 struct Variant {
     int width;
-    const void* fused[2];     // [0] batch 1, [1] batch 2 .. kMaxBatch
-    const void* stage_a[2];
-    const void* stage_b[2];
+    // [0] batch 1, [1] batch 2 .. kMaxBatch, [2] batch 1 with 64-neuron groups (staged)
+    const void* fused[3];
+    const void* stage_a[3];
+    const void* stage_b[3];
     const void* reduce;
+};
+
+// Staged kernels exist only for the widths where they fit two workgroups per CU.
+template <int D, template <int, int, bool> class K>
+const void* staged_kernel() {
+    if constexpr (staged_width(D))
+        return reinterpret_cast<const void*>(K<D, 1, true>::fn);
+    else
+        return nullptr;
+}
+
+template <int D, int NB, bool STAGED>
+struct FusedK {
+    static constexpr auto fn = &fused_layer_kernel<D, NB, STAGED>;
+};
+template <int D, int NB, bool STAGED>
+struct StageAK {
+    static constexpr auto fn = &stage_a_kernel<D, NB, STAGED>;
+};
+template <int D, int NB, bool STAGED>
+struct StageBK {
+    static constexpr auto fn = &stage_b_kernel<D, NB, STAGED>;
 };
 
 template <int D>
 Variant make_variant() {
     return {D,
-            {reinterpret_cast<const void*>(&fused_layer_kernel<D, 1>),
-             reinterpret_cast<const void*>(&fused_layer_kernel<D, kMaxBatch>)},
-            {reinterpret_cast<const void*>(&stage_a_kernel<D, 1>), reinterpret_cast<const void*>(&stage_a_kernel<D, kMaxBatch>)},
-            {reinterpret_cast<const void*>(&stage_b_kernel<D, 1>), reinterpret_cast<const void*>(&stage_b_kernel<D, kMaxBatch>)},
+            {reinterpret_cast<const void*>(&fused_layer_kernel<D, 1, false>),
+             reinterpret_cast<const void*>(&fused_layer_kernel<D, kMaxBatch, false>), staged_kernel<D, FusedK>()},
+            {reinterpret_cast<const void*>(&stage_a_kernel<D, 1, false>),
+             reinterpret_cast<const void*>(&stage_a_kernel<D, kMaxBatch, false>), staged_kernel<D, StageAK>()},
+            {reinterpret_cast<const void*>(&stage_b_kernel<D, 1, false>),
+             reinterpret_cast<const void*>(&stage_b_kernel<D, kMaxBatch, false>), staged_kernel<D, StageBK>()},
             reinterpret_cast<const void*>(&reduce_kernel<D>)};
+}
+
+// Kernel family of a launch: 0 batch 1, 1 batch 2 .. kMaxBatch, 2 staged (batch 1,
+// 64-neuron groups, widths where two workgroups' slots fit a CU's LDS).
+int family(int width, int batch, int group_size) {
+    if (batch > 1) return 1;
+    return group_size == (int)kStagedGroup && staged_width(width) ? 2 : 0;
 }
 
 const Variant* find_variant(int width) {
@@ -1760,10 +2143,10 @@ const Variant* find_variant(int width) {
 
 bool variant_available(int width) { return find_variant(width) != nullptr; }
 
-hipError_t resident_workers(int width, int entry_point, int batch, int* per_cu) {
+hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu) {
     const Variant* v = find_variant(width);
     if (!v || batch < 1 || batch > (int)kMaxBatch) return hipErrorInvalidValue;
-    const int nb = batch > 1;
+    const int nb = family(width, batch, group_size);
     const void* k = entry_point == kEntryFused ? v->fused[nb] : v->stage_b[nb];
     int n = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kThreads, 0);
@@ -1782,7 +2165,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     MlpArgs a = args;
     Bounds b = bounds;
     if (a.batch < 1 || a.batch > kMaxBatch) return hipErrorInvalidValue;
-    const int nb = a.batch > 1;
+    const int nb = family(p.width, (int)a.batch, (int)a.group_size);
     void* kargs[] = {&a, &b};
     if (p.entry_point == kEntryFused)
         return hipLaunchKernel(v->fused[nb], dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
