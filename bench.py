@@ -91,6 +91,24 @@ def traffic_from_profiles(workload_name):
     return None
 
 
+def host_cpu():
+    """(logical CPUs of the host, CPU model string)."""
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return os.cpu_count() or 1, model
+
+
+# The GPU box gives one GPU's job a share of 16 host CPUs (OMP_NUM_THREADS there): the
+# baseline's thread pool stays within that share whatever the host's CPU count.
+CPU_SHARE = 16
+
+
 def cpu_baseline(cfg, budget_s):
     """The oracle (CPU restatement of the reference arithmetic) timed on the host cores."""
     import numpy as np
@@ -102,7 +120,9 @@ def cpu_baseline(cfg, budget_s):
 
     hl = synth.host_layer(cfg)
     rows = synth.descriptors(cfg, synth.active_groups(cfg))
-    threads = max(1, min(16, os.cpu_count() or 1))
+    host_cpus, model = host_cpu()
+    share = int(os.environ.get("OMP_NUM_THREADS", CPU_SHARE) or CPU_SHARE)
+    threads = max(1, min(share, host_cpus))
     out = {}
     for label, nthreads, share in (("all", threads, 0.7), ("one", 1, 0.3)):
         t_end = time.perf_counter() + budget_s * share
@@ -121,10 +141,12 @@ def cpu_baseline(cfg, budget_s):
         "unit": "us/layer",
         "cores": t_all,
         "kind": "port",
-        "sample": f"{n_all} full layers ({cfg.name}) with {t_all} OpenMP threads; single thread: {us_one:.0f} us/layer "
-                  f"over {n_one} layers",
+        "sample": f"{n_all} full layers ({cfg.name}) with {t_all} OpenMP threads (the job's CPU share of a "
+                  f"{host_cpus}-CPU host); single thread: {us_one:.0f} us/layer over {n_one} layers",
         "gbs": round(cfg.algorithmic_bytes() / us_all / 1e3, 2),
         "single_thread_us": round(us_one, 1),
+        "host_cpus": host_cpus,
+        "cpu_model": model,
     }
 
 

@@ -42,8 +42,8 @@ inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexc
 }
 
 // Geometry and caller-owned device buffers of one layer family (same shapes for every
-// layer the backend serves). Pointers are device addresses; hidden/partial may be
-// null, in which case bind() allocates them (cold path).
+// layer the backend serves). Pointers are device addresses; hidden may be null, in
+// which case bind() allocates it (cold path).
 struct HipLayerBuffers {
     uint32_t width = 0;            // d, multiple of 256 (256..8192)
     uint32_t group_size = 0;       // G neurons per group
@@ -58,11 +58,13 @@ struct HipLayerBuffers {
     const void* staging = nullptr; // packed groups [staging_groups][G][3][d/2]
     const void* scales = nullptr;  // fp16 [physical_groups*G][3][d/128]
     void* hidden = nullptr;        // u64 [slot_capacity][batch][G]: fp32 bits of h | launch sequence << 32
-    void* partial = nullptr;       // reserved (the reduction accumulates in backend-owned fixed point)
+    void* partial = nullptr;       // reserved, unused: the reduction accumulates in backend-owned fixed point
     void* y32 = nullptr;           // optional fp32 [d] pre-rounding output
     uint32_t* executions = nullptr;     // optional per-destination execution counts
     uint64_t* first_compute = nullptr;  // optional per-destination start stamps
-    uint32_t* claim_log = nullptr;      // optional claim log (queue positions)
+    uint32_t* claim_log = nullptr;      // optional claim log: 4 words per range a workgroup takes
+                                        // ({first, count, ready at claim or ~0u, worker}), in the order
+                                        // taken; holds queue_capacity ranges
     uint64_t* stamps = nullptr;         // optional per-worker phase stamps [max workers][32]
 };
 
@@ -83,12 +85,13 @@ public:
     KernelRuntimeState state{};
     // Optional lifecycle hooks (as in the Triton backend): completion proof and cache
     // installation belong to the application. Without `completed`, completion is the
-    // backend's own event recorded after the last kernel of the latest enqueue.
+    // host-coherent word the latest launch's last workgroup stores (no event); without
+    // `install_cache`, commit returns ENOTSUP (backends/triton/enqueue.cpp:45).
     void* lifecycle_context = nullptr;
     bool (*completed)(void*, uint32_t) = nullptr;
     int (*install_cache)(void*, uint32_t, Span<GroupId>) = nullptr;
 
-    uint32_t status() const;       // sticky device status bits (timeout, bad descriptor)
+    uint32_t status() const;       // sticky device status bits (lsamd::StatusBit / LS_STATUS_*)
     void clear_status();
     void set_spin_limit_ticks(uint64_t ticks) { spin_limit_ = ticks; }
     uint32_t slices() const { return slices_; }
@@ -98,6 +101,9 @@ public:
     uint32_t selected(KernelRuntimeState s) const { return selector_.select(s); }
     int last_candidate() const { return last_candidate_; }
     uint32_t max_workers() const { return max_workers_; }
+    // False for a backend bound for the dense path (batch 5..32), whose launches compute
+    // the resident groups only and do not consume the ready queue.
+    bool consumes_queue() const;
 
 private:
     struct Impl;

@@ -9,13 +9,17 @@
 //
 // HipCopyEngine issues hipMemcpyAsync on `streams` side streams (default priority,
 // non-blocking with respect to the null stream), one event per lane. Streams share the
-// process's hardware queues (GPU_MAX_HW_QUEUES): a copy stream that shares one with the
-// stream running the consumer can leave copies queued behind that kernel until its
-// bounded waits expire, so keep streams + other streams of the process within that count.
+// process's hardware queues (GPU_MAX_HW_QUEUES, 4 by default): a copy stream that shares
+// one with the stream running the consumer leaves copies queued behind that kernel until
+// its bounded waits expire. At most kMaxHipCopyStreams streams are accepted (with the null
+// stream and the consumer's stream that fills the default four queues); the SDMA engine
+// has no such hazard and is the one to use.
 #pragma once
 #include "host_staging_io.h"
 
 namespace leanstream::runtime {
+
+inline constexpr uint32_t kMaxHipCopyStreams = 2;
 
 class SdmaCopyEngine {
 public:
@@ -38,7 +42,8 @@ private:
 
 class HipCopyEngine {
 public:
-    // `lanes` >= the transport's qd; `streams` copy streams used round robin (1..8).
+    // `lanes` >= the transport's qd; `streams` copy streams used round robin
+    // (1..kMaxHipCopyStreams).
     // Throws std::runtime_error when a stream or event cannot be created.
     HipCopyEngine(int device, uint32_t lanes, uint32_t streams);
     ~HipCopyEngine();

@@ -60,14 +60,15 @@ typedef struct ls_hip_layer_buffers {
     void* y32;
     uint32_t* executions;
     uint64_t* first_compute;
-    uint32_t* claim_log;
+    uint32_t* claim_log;      /* optional: 4 words per range taken, queue_capacity ranges */
     uint64_t* stamps;
 } ls_hip_layer_buffers;
 
 /* Consumer modes (leanstream::runtime::ConsumerMode). */
 enum { LS_MODE_BATCH_COMPAT = 0, LS_MODE_PROGRESSIVE = 1, LS_MODE_AUTO = 2 };
 /* Device status bits returned by ls_hip_status. */
-enum { LS_STATUS_TIMEOUT = 1, LS_STATUS_QUEUE_ERROR = 2, LS_STATUS_BAD_DESCRIPTOR = 4, LS_STATUS_RANGE = 8 };
+enum { LS_STATUS_TIMEOUT = 1, LS_STATUS_QUEUE_ERROR = 2, LS_STATUS_BAD_DESCRIPTOR = 4, LS_STATUS_RANGE = 8,
+       LS_STATUS_QUEUE_UNCONSUMED = 16 /* dense (batch 5..32) launch whose layer published queue entries */ };
 
 /* ---- backend ---- */
 void* ls_hip_create(void);
@@ -83,7 +84,7 @@ int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t ou
 uint32_t ls_hip_status(void* backend);
 void ls_hip_clear_status(void* backend);
 void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
-/* Down-projection items (128-column tiles) per unit: d / 128. */
+/* Down-projection items (256-column tiles) per unit: d / 256. */
 uint32_t ls_hip_slices(void* backend);
 /* Overrides the selected candidate's persistent worker count (0 = the candidate's own
  * value). No reference counterpart: a tuning knob of the persistent launch. */
@@ -142,7 +143,7 @@ typedef struct ls_stream_setup {
     uint32_t layers;          /* Runtime layer contexts */
     uint32_t qd;              /* copies in flight, 1..32 */
     uint32_t copy_engine;     /* LS_COPY_SDMA or LS_COPY_HIP */
-    uint32_t copy_queues;     /* SDMA engines (1..16) or hipMemcpyAsync streams (1..8), round robin */
+    uint32_t copy_queues;     /* SDMA engines (1..16) or hipMemcpyAsync streams (1..2), round robin */
     uint32_t copy_chunk;      /* SDMA: bytes per copy piece (0 = one copy per group) */
     uint32_t mode;            /* LS_MODE_* */
     int32_t device;

@@ -12,7 +12,7 @@ from . import _native
 from ._native import DeviceQueue, ExecDesc, LayerBuffers
 
 MODE_BATCH_COMPAT, MODE_PROGRESSIVE, MODE_AUTO = 0, 1, 2
-STATUS_TIMEOUT, STATUS_QUEUE_ERROR, STATUS_BAD_DESCRIPTOR, STATUS_RANGE = 1, 2, 4, 8
+STATUS_TIMEOUT, STATUS_QUEUE_ERROR, STATUS_BAD_DESCRIPTOR, STATUS_RANGE, STATUS_QUEUE_UNCONSUMED = 1, 2, 4, 8, 16
 QUEUE_CONTROL_BYTES = 128
 
 

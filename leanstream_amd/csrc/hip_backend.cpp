@@ -21,7 +21,6 @@ struct HipBackend::Impl {
     uint32_t slot_words = 0;
     uint32_t* status = nullptr;  // host-coherent
     void* owned_hidden = nullptr;
-    void* owned_partial = nullptr;
     uint16_t* h16 = nullptr;     // dense path: fp16 h rows
     float* dpart = nullptr;      // dense path: down-projection partial rows
     uint16_t* x16 = nullptr;     // dense path: x converted to paired fp16
@@ -38,7 +37,6 @@ struct HipBackend::Impl {
         if (qmirror) (void)hipFree(qmirror);
         if (yacc) (void)hipFree(yacc);
         if (owned_hidden) (void)hipFree(owned_hidden);
-        if (owned_partial) (void)hipFree(owned_partial);
         if (h16) (void)hipFree(h16);
         if (dpart) (void)hipFree(dpart);
         if (x16) (void)hipFree(x16);
@@ -47,7 +45,7 @@ struct HipBackend::Impl {
         sync = nullptr;
         qmirror = nullptr;
         yacc = nullptr;
-        owned_hidden = owned_partial = nullptr;
+        owned_hidden = nullptr;
         h16 = nullptr;
         dpart = nullptr;
         x16 = nullptr;
@@ -91,7 +89,6 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess && dense) e = hipMalloc(&p.x16, sizeof(uint16_t) * 32 * b.width);
     // h rows >= batch stay zero: the dense down projection reads all 32 rows
     if (e == hipSuccess && dense) e = hipMemset(p.h16, 0, sizeof(uint16_t) * 32 * b.slot_capacity * b.group_size);
-    if (e == hipSuccess && !b.partial) e = hipMalloc(&p.owned_partial, sizeof(float) * b.slot_capacity * b.width);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
     int dev = 0;
@@ -120,12 +117,11 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     a.staging = static_cast<const uint8_t*>(b.staging);
     a.scales = static_cast<const uint16_t*>(b.scales);
     a.hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
-    a.partial = static_cast<float*>(b.partial ? b.partial : p.owned_partial);
     a.y32 = static_cast<float*>(b.y32);
     a.executions = b.executions;
     a.first_compute = b.first_compute;
     a.claim_log = b.claim_log;
-    a.claim_log_cap = b.claim_log ? b.queue_capacity : 0;
+    a.claim_log_cap = b.claim_log ? b.queue_capacity : 0;   // ranges (lsamd::kClaimLogWords words each)
     a.stamps = b.stamps;
     a.sync = p.sync;
     a.qmirror = p.qmirror;
@@ -207,6 +203,8 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     return 0;
 }
 
+bool HipBackend::consumes_queue() const { return !impl_->dense; }
+
 uint32_t HipBackend::status() const { return impl_->status ? __atomic_load_n(impl_->status, __ATOMIC_ACQUIRE) : 0; }
 void HipBackend::clear_status() {
     if (impl_->status) __atomic_store_n(impl_->status, 0u, __ATOMIC_RELEASE);
@@ -234,8 +232,10 @@ bool HipBackend::complete(void* ctx, uint32_t layer) {
 
 int HipBackend::commit(void* ctx, uint32_t layer, Span<GroupId> ids) {
     auto& b = *static_cast<HipBackend*>(ctx);
-    // Cache installation is application policy; without a hook there is nothing to install.
-    return b.install_cache ? b.install_cache(b.lifecycle_context, layer, ids) : 0;
+    // Cache installation is application policy: without the application's hook the
+    // backend cannot install anything and says so, as LeanStream's Triton backend does
+    // (backends/triton/enqueue.cpp:45).
+    return b.install_cache ? b.install_cache(b.lifecycle_context, layer, ids) : ENOTSUP;
 }
 
 ComputeBackend HipBackend::view() {

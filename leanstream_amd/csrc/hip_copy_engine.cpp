@@ -175,7 +175,7 @@ struct HipCopyEngine::Impl {
 HipCopyEngine::HipCopyEngine(int device, uint32_t lanes, uint32_t streams) : impl_(new Impl) {
     Impl& m = *impl_;
     m.device = device;
-    if (!lanes || lanes > 64 || !streams || streams > 8 || hipSetDevice(device) != hipSuccess) {
+    if (!lanes || lanes > 64 || !streams || streams > kMaxHipCopyStreams || hipSetDevice(device) != hipSuccess) {
         delete impl_;
         throw std::runtime_error("copy engine geometry");
     }

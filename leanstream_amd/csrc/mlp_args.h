@@ -53,6 +53,14 @@ constexpr uint32_t kDenseSplits = 16;     // unit splits of its down projection
 
 constexpr uint32_t pack_epoch(uint32_t state, uint32_t path, uint32_t total) { return state | (path << 2) | (total << 4); }
 
+// Claim log (candidates that consume the queue in groups of claim_batch positions, the
+// ready pairs of backends/triton/persistent.py:63-90): one entry per range a workgroup
+// takes, in the order the ranges were taken: {first position, count, ready count the
+// claim was made against, worker}. On the all-ready path the ranges are the static pairs
+// of descriptor indices (2w + 2kW, +1) and the third word is kClaimStatic.
+constexpr uint32_t kClaimLogWords = 4;
+constexpr uint32_t kClaimStatic = 0xFFFFFFFFu;
+
 // Phase stamps (100 MHz clock) written by lane 0 of every wave when MlpArgs::stamps is
 // set: stamps[(block * 4 + wave) * kStampSlots + phase]; 0 = the wave never got there.
 constexpr uint32_t kStampSlots = 32;
@@ -72,7 +80,10 @@ enum StampPhase : uint32_t {
 };
 
 // Status word bits (host-coherent, sticky until cleared by the host).
-enum StatusBit : uint32_t { kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u, kStatusRange = 8u };
+enum StatusBit : uint32_t {
+    kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u, kStatusRange = 8u,
+    kStatusQueueUnconsumed = 16u,   // a dense (batch > kMaxBatch) launch's layer published queue entries
+};
 
 // Arena extents used to validate descriptors on the device before any access.
 struct Bounds {
@@ -94,7 +105,6 @@ struct MlpArgs {
     const uint8_t* staging;
     const uint16_t* scales;       // fp16 [(physical*G + n)*3 + proj][d/128]
     uint64_t* hbuf;               // [slot][batch][G] h = fp16(silu(g)*u) as fp32 bits | launch seq << 32
-    float* partial;               // unused by the fixed-point reduction (kept in the buffer block)
     unsigned long long* yacc;     // [2][batch][d][kAccStride] packed accumulators (see kAccOne), buffer (seq & 1)
                                   // per launch
     uint16_t* y;                  // fp16 [batch][d]
@@ -104,8 +114,8 @@ struct MlpArgs {
     uint32_t* sync;               // base of the two ring slots
     uint32_t* status;             // host-coherent sticky status word
     uint32_t* done;               // host-coherent: the last workgroup of a launch stores seq
-    uint32_t* claim_log;          // optional: per-claim (head | (len << 24)), in claim order
-    uint32_t claim_log_cap;       // entries in claim_log
+    uint32_t* claim_log;          // optional: kClaimLogWords words per claimed range, in claim order
+    uint32_t claim_log_cap;       // entries (ranges) claim_log holds
     uint64_t* stamps;             // optional: per-worker phase stamps [workers][kStampSlots] (100 MHz clock)
     // geometry / control
     uint32_t width;               // d
@@ -113,7 +123,7 @@ struct MlpArgs {
     uint32_t slices;              // down-projection items per unit (d / kDnCols)
     uint32_t slot_words;          // words per ring slot
     uint32_t units_cap;           // max units (core + queue) the ring slot covers
-    uint32_t slot_capacity;       // rows in hbuf/partial
+    uint32_t slot_capacity;       // destination rows (rows of hbuf)
     uint32_t epoch;
     uint32_t seq;                 // launch sequence number (selects the ring slot)
     uint32_t batch_mode;          // 1: wait for batch_epoch before consuming the queue

@@ -92,6 +92,9 @@ struct StreamDecoder {
         sc.group_bytes = s.group_bytes;
         sc.staging_stride = s.staging_stride;
         io.reset(new HostStagingIO(sc));
+        // This loop installs nothing into a cache at commit (its groups stream every layer);
+        // a backend without the application's hook would refuse the commit (ENOTSUP).
+        if (!backend->install_cache) backend->install_cache = [](void*, uint32_t, Span<GroupId>) { return 0; };
         ManagerConfig mc{n, s.qd, s.group_bytes, s.staging_stride, 512, static_cast<ConsumerMode>(s.mode)};
         mc.io_backend = io->backend();
         runtime.reset(new Runtime(mc, backend->view(), s.layers));
@@ -144,12 +147,23 @@ struct StreamDecoder {
         }
         mark(5);
         if (!rc && !done) rc = ETIMEDOUT;
+        // A launch whose device status is set (a bounded wait expired, a descriptor or the
+        // queue was rejected, a value was out of range) produced no valid output and may
+        // have signalled completion with workgroups still resident: the layer fails.
+        const uint32_t status = backend->status();
+        if (status) {
+            backend->clear_status();
+            if (!rc) rc = status & LS_STATUS_TIMEOUT ? ETIMEDOUT : EIO;
+        }
         if (!rc) {
             rc = step.commit({});
             mark(6);
             if (!rc) return 0;
         }
-        // failure: cancel and retire once the kernel has exited (its waits are bounded)
+        // failure: wait until the launch stream has drained (every wait in the kernels is
+        // bounded), so no workgroup still reads the staging arena the next layer's copies
+        // will rewrite, then cancel and retire
+        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
         while (step.abort() == EBUSY && now_ns() < deadline + 5000000000ull) std::this_thread::yield();
         return rc;
     }
@@ -162,7 +176,8 @@ extern "C" {
 void* ls_stream_create(const ls_stream_setup* s) {
     if (!s || !s->backend || !s->host_store || !s->staging || !s->group_count || !s->layers || !s->qd ||
         s->qd > 32 || !s->copy_queues || s->copy_queues > 16 || s->copy_engine > LS_COPY_HIP ||
-        (s->copy_engine == LS_COPY_HIP && s->copy_queues > 8) || s->mode > 2)
+        (s->copy_engine == LS_COPY_HIP && s->copy_queues > kMaxHipCopyStreams) || s->mode > 2 ||
+        !static_cast<HipBackend*>(s->backend)->consumes_queue())
         return nullptr;
     auto* d = new (std::nothrow) StreamDecoder;
     if (!d) return nullptr;

@@ -1373,7 +1373,7 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
 // (total_count, epoch): adjacent words (byte offsets 8 and 12), read as one pair.
 __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
     const uint32_t lane = threadIdx.x & 63;
-    uint32_t state = 0, total = 0;
+    uint32_t state = 0, total = 0, path = 0;
     if (lane == 0) {
         Waiter wt(a.spin_limit);
         uint64_t te = pre;
@@ -1400,13 +1400,13 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
                 __builtin_amdgcn_s_sleep(8);
             }
         }
-        uint32_t path = 0;
         if (state == 1 && total) path = ld_sys(&a.control->ready_count) >= total ? 2u : 1u;
         st_agent(slot + kSyncEpoch, pack_epoch(state, path, state == 1 ? total : 0u));
         stamp(a, kStampMirrorEpoch);
     }
     state = wave_bcast(state);
     total = wave_bcast(total);
+    const bool by_index = a.claim_batch && wave_bcast(path) == 2u;
     if (state != 1) return;
     if (total == 0 && a.core_count == 0) {
         // no rows at all: the reduction of nothing is zero
@@ -1435,7 +1435,9 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
             for (uint32_t base = mirrored; base < ready; base += 64) {
                 const uint32_t pos = base + lane;
                 if (pos < ready) {
-                    const uint32_t idx = ld_sys(a.ready + pos);
+                    // All-ready launches of a pair-claiming candidate consume descriptors by
+                    // index (persistent.py:63-69); every other launch by publication position.
+                    const uint32_t idx = by_index ? pos : ld_sys(a.ready + pos);
                     const uint32_t* d = reinterpret_cast<const uint32_t*>(a.qdesc + (idx < a.capacity ? idx : 0));
                     uint32_t w[5];
 #pragma unroll
@@ -1459,8 +1461,21 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
     }
 }
 
+// One claim log entry (kClaimLogWords), written by one lane of the claiming workgroup.
+__device__ __forceinline__ void log_claim(const MlpArgs& a, uint32_t* slot, uint32_t first, uint32_t count,
+                                          uint32_t ready) {
+    if (!a.claim_log) return;
+    const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
+    if (seq >= a.claim_log_cap) return;
+    uint32_t* e = a.claim_log + (size_t)seq * kClaimLogWords;
+    e[0] = first;
+    e[1] = count;
+    e[2] = ready;
+    e[3] = blockIdx.x;
+}
+
 // Claim the next ready positions [head, min(head + claim_batch, ready)) against the
-// mirrored ready count (claim_batch = 2: the ready pair of backends/triton/persistent.py:77-86). Every wave of the workgroup takes part; `ok` is this
+// mirrored ready count (claim_batch = 2: the ready pair of backends/triton/persistent.py:73-87). Every wave of the workgroup takes part; `ok` is this
 // wave's success so far. Returns the number of claimed positions (0 = leave, also when
 // any wave of the workgroup failed).
 __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total, bool ok) {
@@ -1482,8 +1497,7 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
                 if (__hip_atomic_compare_exchange_strong(slot + kSyncClaimHead, &expected, end, __ATOMIC_RELAXED,
                                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
                     got = end - head;
-                    const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
-                    if (a.claim_log && seq < a.claim_log_cap) a.claim_log[seq] = head | (got << 24);
+                    log_claim(a, slot, head, got, ready);
                     break;
                 }
                 continue;
@@ -1523,8 +1537,9 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     pd.col = -1;
     const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
     bool ok = true;
-    enum : uint32_t { kCore, kDecide, kClaim, kDone };
+    enum : uint32_t { kCore, kDecide, kClaim, kPairs, kDone };
     uint32_t phase = CORE ? kCore : kDecide;
+    uint32_t pair = blockIdx.x;   // kPairs: this worker's next static range, in units of claim_batch
     for (;;) {
         uint32_t u0 = 0, u1 = 0, e = early;
         WaveRole r = role;
@@ -1546,7 +1561,13 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             // All positions published before the launch (path 2), or published while it
             // runs with striped consumption (path 1, claim_batch 0): every wave walks its
             // stripe of the queue's items, waiting for each item's position as needed.
-            if (path == 2 || (path == 1 && a.claim_batch == 0)) {
+            // With claim_batch > 0 the workgroups take ranges of claim_batch positions:
+            // static ranges of descriptor indices when all were ready (persistent.py:63-69),
+            // claimed ready ranges otherwise (persistent.py:71-90).
+            if (path == 2 && a.claim_batch) {
+                phase = kPairs;
+                continue;
+            } else if (path == 2 || (path == 1 && a.claim_batch == 0)) {
                 u0 = a.core_count;
                 u1 = u0 + ep.total;
                 phase = kDone;
@@ -1556,6 +1577,16 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             } else {
                 break;
             }
+        } else if (phase == kPairs) {
+            const uint32_t first = pair * a.claim_batch;
+            if (!ok || first >= ep.total) break;
+            const uint32_t got = min(a.claim_batch, ep.total - first);
+            if (threadIdx.x == 0) log_claim(a, slot, first, got, kClaimStatic);
+            u0 = a.core_count + first;
+            u1 = u0 + got;
+            pair += W;
+            r = WaveRole{wave, kWaves, 0};
+            e = 0;
         } else if (phase == kClaim) {
             const uint32_t got = claim_pair(a, sh, slot, ep.total, ok);
             if (!got) break;
@@ -1819,10 +1850,6 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
     constexpr uint32_t kq = D / kDenseGuWaves;
     const uint32_t G = a.group_size;
     const uint32_t unit = blockIdx.x >> 1, half = blockIdx.x & 1;
-    if (blockIdx.x == 0) {   // the next launch's ring slot (this one's was cleared before it)
-        uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-        for (uint32_t i = threadIdx.x; i < a.slot_words; i += blockDim.x) st_agent(other + i, 0u);
-    }
     const Unit u = resolve(a, b, a.core[unit], (int)D);
     const int lane = lane_id();
     const uint32_t w = wave_id();
@@ -2058,7 +2085,39 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs 
 }
 
 // Sum of the splits in a fixed order, fp16 rounding, completion word.
+// The queue of a dense launch (batch 5 .. 32) is not consumed: every group of a dense layer
+// is a resident core unit. Block 0 of the reduction waits for the layer epoch (bounded) and
+// raises kStatusQueueUnconsumed if the layer published queue entries, whose groups the
+// output then lacks.
+__device__ __forceinline__ void check_dense_queue(const MlpArgs& a, uint32_t* slot) {
+    Waiter wt(a.spin_limit);
+    for (;;) {
+        const uint64_t te = ld_sys64(&a.control->total_count);
+        if ((uint32_t)(te >> 32) == a.epoch) {
+            if ((uint32_t)te) raise_status(a, slot, kStatusQueueUnconsumed);
+            return;
+        }
+        if (ld_sys(&a.control->error)) {
+            raise_status(a, slot, kStatusQueueError);
+            return;
+        }
+        if (wt.expired()) {
+            raise_status(a, slot, kStatusTimeout);
+            return;
+        }
+        __builtin_amdgcn_s_sleep(8);
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    if (blockIdx.x == 0) {
+        // the next launch's ring slot: its last user, the previous launch, has finished
+        // (stream order); this kernel runs in every dense launch, with or without core units
+        uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
+        for (uint32_t i = threadIdx.x; i < a.slot_words; i += blockDim.x) st_agent(other + i, 0u);
+        if (threadIdx.x == 0) check_dense_queue(a, slot);
+    }
     const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * D + column
     const uint32_t tk = idx / a.width, col = idx - tk * a.width;
     float v = 0.f;
@@ -2073,7 +2132,7 @@ __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
     }
     if (a.y32) a.y32[idx] = v;
     a.y[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
-    finish_launch(a, a.sync + (a.seq & 1) * a.slot_words);
+    finish_launch(a, slot);
 }
 
 // ---------------------------------------------------------------------------------

@@ -18,7 +18,7 @@ def _check(rc, what):
 
 class DeviceLayer:
     def __init__(self, cfg, copies=1, logical=None, with_y32=True, diagnostics=True, queue_capacity=None,
-                 offline_table=None, stamps=False):
+                 offline_table=None, stamps=False, claim_log=False):
         import torch
 
         self.torch = torch
@@ -60,11 +60,16 @@ class DeviceLayer:
         self.executions = torch.zeros(self.slot_capacity, dtype=torch.int32, device=dev) if diagnostics else None
         self.queue = ReadyQueue(queue_capacity if queue_capacity else max(1, k))
         self.stamps = torch.zeros(4096 * 32, dtype=torch.int64, device=dev) if stamps else None
+        # claim log: 4 words per range a workgroup takes (candidates that consume the queue in
+        # ranges), at most one range per queue position
+        self.claim_log = (torch.zeros(self.queue.capacity * 4, dtype=torch.int32, device=dev) if claim_log
+                          else None)
         self.backend = NativeBackend(offline_table)
         self.backend.bind(d, G, self.slot_capacity, self.cache, self.scales, physical_groups=copies * n,
                           cache_groups=copies * n, staging=self.cache, staging_groups=copies * n,
                           queue_capacity=self.queue.capacity, hidden=self.hidden, partial=self.partial, y32=self.y32,
-                          executions=self.executions, batch=cfg.batch, stamps=self.stamps)
+                          executions=self.executions, batch=cfg.batch, stamps=self.stamps,
+                          claim_log=self.claim_log)
         torch.cuda.synchronize()
 
     def core_ptr(self, copy):

@@ -71,3 +71,60 @@ def test_dense_layer_matches_oracle(torch_gpu, key, rows):
         assert np.array_equal(layer.y32.cpu().numpy().reshape(cfg.batch, d).view(np.uint32), y32.view(np.uint32))
     finally:
         layer.close()
+
+
+def test_dense_launch_without_core_groups_then_with(torch_gpu):
+    """A dense launch with no core units (only the reduction kernel runs) followed by a launch
+    with core units: both complete (each launch leaves the next one's ring slot clear),
+    y is 0 for the empty launch and matches the normal layer afterwards."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1d32"]
+    log("case: dense launch with 0 core groups, then with core groups")
+    layer = DeviceLayer(cfg)
+    try:
+        layer.seal_empty_queue(1)
+        layer.run_core(epoch=1)
+        torch.cuda.synchronize()
+        want = layer.y32.cpu().numpy().copy()
+        stream = torch.cuda.current_stream().cuda_stream
+        for rep in range(2):
+            layer.backend.enqueue(0, 0, 1, layer.x, layer.y, stream, None, 0, layer.queue)
+            torch.cuda.synchronize()
+            assert layer.backend.complete() and layer.backend.status() == 0
+            assert not np.any(layer.y32.cpu().numpy())
+            layer.run_core(epoch=1)
+            torch.cuda.synchronize()
+            assert layer.backend.complete() and layer.backend.status() == 0
+            assert np.array_equal(layer.y32.cpu().numpy(), want)
+    finally:
+        layer.close()
+
+
+def test_dense_launch_flags_published_queue_entries(torch_gpu):
+    """The dense path computes resident groups only: a layer whose queue holds published
+    entries is reported (LS_STATUS_QUEUE_UNCONSUMED) instead of silently lacking them."""
+    from leanstream_amd.backend import STATUS_QUEUE_UNCONSUMED
+
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1d32"]
+    log("case: dense launch with a non-empty ready queue")
+    layer = DeviceLayer(cfg, queue_capacity=4)
+    try:
+        rows = synth.descriptors(cfg, layer.logical[:2], source_kind=0)
+        q = layer.queue
+        q.write_descriptors(rows)
+        q.reset(2)
+        q.seal(2)
+        q.publish(0)
+        q.publish(1)
+        layer.run_core(epoch=2)
+        torch.cuda.synchronize()
+        assert layer.backend.complete()
+        assert layer.backend.status() & STATUS_QUEUE_UNCONSUMED, layer.backend.status()
+        layer.backend.clear_status()
+        layer.seal_empty_queue(3)
+        layer.run_core(epoch=3)
+        torch.cuda.synchronize()
+        assert layer.backend.status() == 0
+    finally:
+        layer.close()

@@ -245,6 +245,40 @@ def test_modes_orders_and_entry_points_bit_exact(torch_gpu):
         assert np.array_equal(v, base), k
 
 
+@pytest.mark.parametrize("key", ["c1", "c2"])
+def test_ready_pair_consumption_order(torch_gpu, key):
+    """Candidate hip_fused_resident_pairs consumes the queue in LeanStream's ready pairs
+    (backends/triton/persistent.py:59-90): static descriptor-index pairs (2w + 2kW, +1) when
+    every position was published before the launch, claimed [head, min(head + 2, ready))
+    ranges of publication positions otherwise. Every logged range is checked (tests/claims.py),
+    every descriptor runs exactly once, and y is bit-identical to the default candidate's."""
+    from claims import check_claim_log
+
+    torch = torch_gpu
+    cfg = synth.CONFIGS[key]
+    log(f"case: ready-pair consumption order {cfg.name}")
+    base = DeviceLayer(cfg)
+    want = {}
+    for publish in ("before", "delayed"):
+        _queue_run(torch, base, 0, MODE_PROGRESSIVE, publish, epoch=3)
+        want[publish] = base.y32.cpu().numpy().copy()
+    base.close()
+    assert np.array_equal(want["before"], want["delayed"])
+    layer = DeviceLayer(cfg, offline_table=[[5]], claim_log=True)
+    workers = layer.backend.max_workers
+    for publish, kind in (("before", "static"), ("delayed", "claimed")):
+        log(f"  publish {publish}: expect {kind} ranges over {workers} workers")
+        layer.claim_log.zero_()
+        layer.executions.zero_()
+        rows, _ = _queue_run(torch, layer, 0, MODE_PROGRESSIVE, publish, epoch=4)
+        assert layer.backend.last_candidate() == 5
+        words = layer.claim_log.cpu().numpy().view(np.uint32)
+        assert check_claim_log(words, len(rows), 2, workers) == kind
+        assert np.all(layer.executions.cpu().numpy() == 1)
+        assert np.array_equal(layer.y32.cpu().numpy(), want[publish])
+    layer.close()
+
+
 def test_queue_error_stops_after_published_prefix(torch_gpu):
     torch = torch_gpu
     cfg = synth.CONFIGS["c1"]

@@ -148,3 +148,86 @@ def test_stream_create_rejects_invalid_setup():
     s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 2, 1, 0, 1, 0)    # unknown copy engine
     assert not lib.ls_stream_create(C.byref(s))
     assert lib.ls_stream_run(None, None, 0, 0, None, None, None, 1000) != 0
+
+
+# ---------------------------------------------------------------------------- argument errors
+EINVAL, ENOTSUP, EBUSY = 22, 95, 16
+
+
+def _buffers(**kw):
+    """A valid-looking buffer block (fake non-null device pointers); bind validates the
+    arguments before any HIP call, so the errors below are decided on the CPU."""
+    from leanstream_amd._native import LayerBuffers
+
+    f = dict(width=4096, group_size=64, batch=1, slot_capacity=58, cache_groups=192, staging_groups=0,
+             physical_groups=192, queue_capacity=58, cache=0x1000, staging=None, scales=0x2000)
+    f.update(kw)
+    return LayerBuffers(**f)
+
+
+@pytest.mark.parametrize("change,code", [
+    (dict(width=0), EINVAL), (dict(width=4000), EINVAL), (dict(group_size=0), EINVAL),
+    (dict(group_size=257), EINVAL), (dict(slot_capacity=0), EINVAL), (dict(physical_groups=0), EINVAL),
+    (dict(scales=None), EINVAL), (dict(cache=None), EINVAL), (dict(staging_groups=4, staging=None), EINVAL),
+    (dict(batch=0), ENOTSUP), (dict(batch=33), ENOTSUP), (dict(batch=8, group_size=32), ENOTSUP),
+    (dict(slot_capacity=4096), EINVAL), (dict(width=12288), ENOTSUP),
+])
+def test_bind_rejects_bad_arguments(change, code):
+    """HipBackend::bind validation (the Triton backend's bind and the CUDA enqueue validate
+    the same geometry: backends/triton/enqueue.cpp:19-25, kernels/streaming_mlp.cu:87)."""
+    lib = _native.library()
+    h = lib.ls_hip_create()
+    try:
+        assert lib.ls_hip_bind(h, C.byref(_buffers(**change))) == code
+    finally:
+        lib.ls_hip_destroy(h)
+
+
+def test_bind_and_enqueue_null_arguments():
+    lib = _native.library()
+    assert lib.ls_hip_bind(None, C.byref(_buffers())) == EINVAL
+    h = lib.ls_hip_create()
+    try:
+        assert lib.ls_hip_bind(h, None) == EINVAL
+        q = HostQueue(4)
+        x = np.zeros(4096, np.uint16)
+        y = np.zeros(4096, np.uint16)
+        args = (0, 0, 1, x.ctypes.data, y.ctypes.data, None, None, 0)
+        # no queue, bad mode, unbound backend: refused before any GPU work
+        assert lib.ls_hip_enqueue(h, *args, None, 1) == EINVAL
+        assert lib.ls_hip_enqueue(h, *args, C.byref(q.view), 3) == EINVAL
+        assert lib.ls_hip_enqueue(h, *args, C.byref(q.view), 1) == EINVAL
+        assert lib.ls_hip_enqueue(None, *args, C.byref(q.view), 1) == EINVAL
+        q.close()
+    finally:
+        lib.ls_hip_destroy(h)
+
+
+class _Span(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("size", C.c_size_t)]
+
+
+_COMMIT = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, _Span)
+_COMPLETE = C.CFUNCTYPE(C.c_bool, C.c_void_p, C.c_uint32)
+
+
+class _ComputeBackend(C.Structure):
+    """ComputeBackend (include/leanstream/runtime.h): context + five function pointers."""
+    _fields_ = [("context", C.c_void_p), ("enqueue", C.c_void_p), ("complete", _COMPLETE), ("commit", _COMMIT),
+                ("defer_commit", C.c_void_p), ("cancel", C.c_void_p)]
+
+
+def test_compute_backend_view_commit_without_hook_is_unsupported():
+    """Without the application's cache-installation hook, commit returns ENOTSUP (the
+    Triton backend's behaviour, backends/triton/enqueue.cpp:45); a backend that never
+    launched is complete."""
+    lib = _native.library()
+    h = lib.ls_hip_create()
+    try:
+        cb = _ComputeBackend()
+        assert lib.ls_hip_compute_backend(h, C.byref(cb), C.sizeof(cb)) == 0
+        assert cb.context and cb.enqueue and not cb.defer_commit and not cb.cancel
+        assert cb.commit(cb.context, 0, _Span(None, 0)) == ENOTSUP
+        assert cb.complete(cb.context, 0)
+    finally:
+        lib.ls_hip_destroy(h)
