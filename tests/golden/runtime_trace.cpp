@@ -390,11 +390,228 @@ void runtime_scenarios() {
 
 }  // namespace
 
+// Layout registration and plan reuse, prepare-time validation order, finalize's prefix
+// errors and completions that must not publish.
+void manager_more_scenarios() {
+    std::printf("== manager-more\n");
+    Fixture f;
+    WeightManager m(f.config());
+    GroupId core[] = {0};
+    auto show = [](const char* what, int rc) { std::printf("%s rc=%d\n", what, rc); };
+    LayerStorage s = f.storage({core, 1});
+    s.layout.size = N - 1;
+    show("p1 short layout", m.prepare_layer(s));
+    s = f.storage({core, 1});
+    s.staging_bytes = N * B - 1;
+    show("p2 small staging", m.prepare_layer(s));
+    s.staging_bytes = N * B;
+    show("p3 exact staging", m.prepare_layer(s));
+    f.layout[3].logical_group = 2;
+    show("p4 duplicate layout", m.prepare_layer(f.storage({core, 1})));
+    f.layout[3].logical_group = 3;
+    f.layout[4].bytes = B + 1;
+    show("p5 group bytes", m.prepare_layer(f.storage({core, 1})));
+    f.layout[4].bytes = B;
+    GroupId twice[] = {0, 0}, outside[] = {N}, pair[] = {0, 5};
+    show("p6 core twice", m.prepare_layer(f.storage({twice, 2})));
+    show("p7 core outside", m.prepare_layer(f.storage({outside, 1})));
+    const SlotId keep = f.dest[5];
+    f.dest[5] = f.dest[0];
+    show("p8 core dest clash", m.prepare_layer(f.storage({pair, 2}, N, true)));
+    f.dest[5] = keep;
+    s = f.storage({core, 1});
+    s.io_states = nullptr;
+    show("p9 no io states", m.prepare_layer(s));
+    show("p10 big queue", m.prepare_layer(f.storage({core, 1}, N + 1)));
+    show("p11 core pair", m.prepare_layer(f.storage({pair, 2}, N, true)));
+    dump_descs("p11 core", m.core_descriptors().data, m.core_descriptors().size);
+
+    // registered layout (generation 7): a later begin with the same generation and pointer
+    // keeps the registration, so edits of the immutable layout are not seen
+    s = f.storage({core, 1});
+    s.layout_generation = 7;
+    show("g1 begin", m.begin_layer(0, s));
+    dump_descs("g1 core", m.core_descriptors().data, m.core_descriptors().size);
+    show("g1 begin-while-active", m.begin_layer(0, s));
+    show("g1 prepare-while-active", m.prepare_layer(s));
+    show("g1 retire", m.retire());
+    f.layout[0].physical_group = 3;
+    show("g2 begin same generation", m.begin_layer(0, s));
+    dump_descs("g2 core", m.core_descriptors().data, m.core_descriptors().size);
+    show("g2 retire", m.retire());
+    s.layout_generation = 8;
+    show("g3 begin new generation", m.begin_layer(0, s));
+    dump_descs("g3 core", m.core_descriptors().data, m.core_descriptors().size);
+    show("g3 retire", m.retire());
+    f.layout[0].physical_group = N - 1;
+
+    // prepared plan (generation 3) reused only when every binding matches
+    s = f.storage({pair, 2}, N, true);
+    s.plan_generation = 3;
+    show("q1 prepare", m.prepare_layer(s));
+    f.cache[5] = 4;   // not seen when the prepared plan is reused
+    show("q1 begin reuse", m.begin_layer(1, s));
+    dump_descs("q1 core", m.core_descriptors().data, m.core_descriptors().size);
+    show("q1 retire", m.retire());
+    s.staging_bytes = N * B;   // a different binding: prepared again
+    show("q2 begin changed", m.begin_layer(1, s));
+    dump_descs("q2 core", m.core_descriptors().data, m.core_descriptors().size);
+    show("q2 retire", m.retire());
+    f.cache[5] = 2;
+
+    // argument and state errors of update / finalize
+    show("u1 update idle", m.update_prediction({core, 1}));
+    show("u1 finalize idle", m.finalize({core, 1}));
+    show("u2 begin", m.begin_layer(2, f.storage({pair, 2})));
+    show("u2 update null", m.update_prediction({nullptr, 2}));
+    show("u2 finalize short", m.finalize({core, 1}));
+    show("u2 finalize null", m.finalize({nullptr, 3}));
+    GroupId early[] = {0, 5, 6};
+    f.states[6] = 2;
+    f.io.deliver(6, 8, 0, f.io.epoch);   // before finalize: no plan, nothing published
+    dump_control("u2 early delivery", f.control);
+    f.io.slot[6] = -1;                   // READY at finalize but the transport has no slot
+    show("u2 finalize bad ready slot", m.finalize({early, 3}));
+    dump_control("u2 failed", f.control);
+    show("u2 retire", m.retire());
+    f.io.slot[6] = (6 * 5 + 3) % N;
+    f.states[6] = 0;
+    show("u3 begin", m.begin_layer(3, f.storage({core, 1}, N, true)));
+    GroupId clash[] = {0, 1, 9};
+    f.dest[9] = f.dest[1];
+    show("u3 finalize dest clash", m.finalize({clash, 3}));
+    f.dest[9] = (9 * 7 + 3) % N;
+    show("u3 finalize", m.finalize({clash, 3}));
+    dump_descs("u3 after-finalize", f.desc, f.control.total_count);
+    f.io.deliver(9, N, 0, f.io.epoch);   // slot outside the staging arena: the queue fails
+    dump_control("u3 bad slot", f.control);
+    show("u3 retire", m.retire());
+}
+
+struct DeferringGpu {
+    void (*retired)(void*, uint32_t) = nullptr;
+    void* context = nullptr;
+    uint32_t epoch = 0;
+    bool done = false;
+};
+int deferring_enqueue(void*, uint32_t layer, const void*, void*, void*, Span<ExecDesc> core, DeviceExecQueue,
+                      uint32_t epoch, ConsumerMode) {
+    std::printf("gpu enqueue layer=%u core=%zu epoch=%u\n", layer, core.size, epoch);
+    return 0;
+}
+bool deferring_complete(void* p, uint32_t) { return static_cast<DeferringGpu*>(p)->done; }
+int deferring_commit(void* p, uint32_t layer, Span<GroupId> ids, uint32_t epoch, void (*retired)(void*, uint32_t),
+                     void* context) {
+    auto& g = *static_cast<DeferringGpu*>(p);
+    g.retired = retired;
+    g.context = context;
+    g.epoch = epoch;
+    std::printf("gpu defer_commit layer=%u ids=%s epoch=%u\n", layer, ids_text(ids).c_str(), epoch);
+    return 0;
+}
+void deferring_cancel(void*, uint32_t layer, uint32_t epoch) { std::printf("gpu cancel layer=%u epoch=%u\n", layer, epoch); }
+
+// Deferred commit (retirement from the backend's callback), commit's check order, a
+// finalize failure after the launch, and lifecycle argument errors.
+void runtime_more_scenarios() {
+    std::printf("== runtime-more\n");
+    auto show = [](const char* what, int rc) { std::printf("%s rc=%d\n", what, rc); };
+    {
+        Fixture f;
+        DeferringGpu gpu;
+        ComputeBackend cb{};
+        cb.context = &gpu;
+        cb.enqueue = deferring_enqueue;
+        cb.complete = deferring_complete;
+        cb.defer_commit = deferring_commit;
+        cb.cancel = deferring_cancel;
+        Runtime r(f.config(), cb, 2);
+        LayerStep step, other;
+        GroupId core[] = {0}, final[] = {0, 1, 2}, next[] = {1};
+        show("d1 begin bad layer", r.begin_layer(2, f.storage({core, 1}), &step));
+        show("d1 begin null step", r.begin_layer(0, f.storage({core, 1}), nullptr));
+        show("d1 begin", r.begin_layer(0, f.storage({core, 1}), &step));
+        show("d1 begin again", r.begin_layer(0, f.storage({core, 1}), &other));
+        show("d1 commit-unfinalized", step.commit({next, 1}));
+        show("d1 enqueue", step.enqueue_compute(nullptr, nullptr, nullptr));
+        show("d1 enqueue again", step.enqueue_compute(nullptr, nullptr, nullptr));
+        show("d1 finalize", step.finalize({final, 3}));
+        show("d1 commit", step.commit({next, 1}));
+        show("d1 commit-pending", step.commit({next, 1}));
+        show("d1 abort-pending", step.abort());
+        show("d1 begin-pending", r.begin_layer(0, f.storage({core, 1}), &other));
+        gpu.retired(gpu.context, gpu.epoch + 1);   // another epoch: ignored
+        show("d1 begin-still-pending", r.begin_layer(0, f.storage({core, 1}), &other));
+        gpu.retired(gpu.context, gpu.epoch);
+        gpu.retired(gpu.context, gpu.epoch);       // twice: ignored
+        show("d1 drain", r.drain());
+        show("d1 begin-after-retire", r.begin_layer(0, f.storage({core, 1}), &step));
+        show("d1 abort-unlaunched", step.abort());
+        show("d1 drain", r.drain());
+    }
+    {
+        Fixture f;
+        FakeGpu gpu;
+        ComputeBackend cb{};
+        cb.context = &gpu;
+        cb.enqueue = fake_enqueue;
+        cb.complete = fake_complete;
+        cb.commit = fake_commit;
+        Runtime r(f.config(), cb);
+        LayerStep step;
+        GroupId core[] = {0}, final[] = {0, 1, 2}, big[N + 1] = {}, outside[] = {N}, twice[] = {1, 1},
+                unready[] = {1}, unready_then_outside[] = {1, N}, outside_then_unready[] = {N, 1};
+        show("c1 begin", r.begin_layer(0, f.storage({core, 1}), &step));
+        show("c1 enqueue", step.enqueue_compute(nullptr, nullptr, nullptr));
+        show("c1 finalize", step.finalize({final, 3}));
+        show("c1 commit too many", step.commit({big, N + 1}));
+        show("c1 commit null", step.commit({nullptr, 1}));
+        show("c1 commit while busy", step.commit({outside, 1}));
+        gpu.done = true;
+        show("c1 commit outside", step.commit({outside, 1}));
+        show("c1 commit twice", step.commit({twice, 2}));
+        show("c1 commit unready", step.commit({unready, 1}));
+        show("c1 commit unready-then-outside", step.commit({unready_then_outside, 2}));
+        show("c1 commit outside-then-unready", step.commit({outside_then_unready, 2}));
+        f.states[1] = 2;
+        f.io.deliver(1, 5, 0, f.io.epoch);
+        f.states[2] = 2;
+        f.io.deliver(2, 9, 0, f.io.epoch);
+        r.weights(0).cancel(EIO);             // a queue error: commit reports it first
+        show("c1 commit after queue error", step.commit({unready, 1}));
+        show("c1 abort", step.abort());
+        for (int g = 0; g <= N; ++g) f.states[g] = 0;
+        gpu.done = false;
+        // finalize fails after the launch: the manager and the backend are cancelled
+        show("c2 begin", r.begin_layer(0, f.storage({core, 1}), &step));
+        show("c2 enqueue", step.enqueue_compute(nullptr, nullptr, nullptr));
+        GroupId bad[] = {0, 1, 1};
+        show("c2 finalize dup", step.finalize({bad, 3}));
+        dump_control("c2 cancelled", f.control);
+        show("c2 finalize again", step.finalize({final, 3}));
+        show("c2 commit", step.commit({core, 1}));
+        show("c2 abort-while-busy", step.abort());
+        gpu.done = true;
+        show("c2 abort", step.abort());
+        // a backend without commit: ENOTSUP, the step stays open until abort
+        cb.commit = nullptr;
+        Runtime bare(f.config(), cb);
+        show("c3 begin", bare.begin_layer(0, f.storage({core, 1}), &step));
+        show("c3 enqueue", step.enqueue_compute(nullptr, nullptr, nullptr));
+        GroupId only[] = {0};
+        show("c3 finalize", step.finalize({only, 1}));
+        show("c3 commit", step.commit({}));
+        show("c3 abort", step.abort());
+    }
+}
+
 int main() {
     queue_scenarios();
     manager_scenarios();
     selector_scenarios();
     runtime_scenarios();
+    manager_more_scenarios();
+    runtime_more_scenarios();
     std::printf("== end\n");
     return 0;
 }
