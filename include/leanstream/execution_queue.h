@@ -4,6 +4,7 @@
 //   u32[5] error, u32[6] consumer_path, byte 64 claim_count, 128 bytes total.
 // The MI355X backend keeps this block in fine-grained coherent host memory; the
 // CPU publishes with release stores and the GPU polls with system-scope loads.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include "types.h"
 

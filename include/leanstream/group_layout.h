@@ -1,4 +1,5 @@
 // Registration record for one packed group on storage (LeanStream group_layout.h:4).
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include "types.h"
 

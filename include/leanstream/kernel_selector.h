@@ -1,6 +1,7 @@
 // O(1) offline-table kernel selection (LeanStream kernel_selector.h:4-41).
 // The selector is backend-neutral: the HIP backend supplies its own CDNA4
 // candidate catalog (hip_backend.h) and fallback.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include "types.h"
 

@@ -2,6 +2,7 @@
 // ComputeBackend::enqueue is the hot-path boundary: it pre-enqueues the sparse
 // INT4 MLP for one layer epoch; completion/commit callbacks never launch work.
 // A failed enqueue may leave partial GPU work live, so complete/cancel stay valid.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include "weight_manager.h"
 #include <condition_variable>

@@ -1,6 +1,7 @@
 // Core value types shared by the control runtime and the HIP compute backend.
 // Layout-compatible with LeanStream's include/leanstream/types.h:5-20 so that
 // callers compiled against that header bind to this implementation unchanged.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include <cstddef>
 #include <cstdint>

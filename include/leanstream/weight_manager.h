@@ -2,6 +2,7 @@
 // This implementation publishes READY groups through a borrowed IOBackend; the
 // reference's O_DIRECT stream engine is not part of this build, so an empty
 // io_backend is rejected at construction.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once
 #include "execution_queue.h"
 #include "group_layout.h"

@@ -9,6 +9,7 @@
 //   * fail(e) records the first error only.
 // Callers serialise producers; descriptor contents and weight bytes must already be
 // visible to the GPU before their index is published.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #include "leanstream/execution_queue.h"
 #include <cassert>
 

@@ -1,5 +1,6 @@
 // O(1) kernel selection (LeanStream src/runtime/kernel_selector.cpp:4-22).
 // No allocation, locking, string handling or device calls.
+// Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #include "leanstream/kernel_selector.h"
 #include <limits>
 

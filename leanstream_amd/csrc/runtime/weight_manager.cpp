@@ -1,18 +1,28 @@
-// Per-layer residency, prediction filtering and descriptor production.
+// WeightManager: one layer's residency plan, prediction admission and ready-queue
+// descriptors (the contract of include/leanstream/weight_manager.h; LeanStream
+// weight_manager.h:9-72, docs/execution_queue.md, docs/architecture.md).
 //
-// Observable behaviour follows LeanStream src/runtime/weight_manager.cpp:
-//   * prepare_layer (:81-108): layout registration keyed by (pointer, generation), core
-//     descriptors {g, physical(g), cache_slot(g), dest(g) or i, Cache};
-//   * begin_layer (:109-134): optional reuse of a prepared plan, ++epoch, queue reset;
-//   * update_prediction (:136-153): first-occurrence dedup, drop cached / non-EMPTY
-//     groups, truncate to io_budget, forward to the transport;
-//   * finalize (:154-204): validate everything before mutating, then build the queue
-//     descriptors in final order {g, physical, slot or 0, dest or core+idx,
-//     Cache|Staging}, publish cached and already-READY groups as the initial prefix;
-//   * completions (:46-72): publish READY groups with source_slot = ready slot,
-//     kind = Staging, exactly once, under the producer lock.
-// The transport is always a borrowed IOBackend; the reference's O_DIRECT engine is
-// not part of this build.
+// A manager moves through three phases per layer epoch:
+//
+//   Closed --begin_layer--> Open --finalize--> Frozen --retire--> Closed
+//
+//   * prepare_layer validates the bindings, registers the group layout (kept across
+//     layers while its (pointer, generation) key is unchanged) and builds the core plan:
+//     one Cache descriptor per resident group.
+//   * begin_layer reuses a prepared plan whose key equals the new bindings (else prepares
+//     again), opens epoch n, resets the queue and starts the transport.
+//   * update_prediction hands the transport the new priority list: first occurrences of
+//     groups that are neither cached nor already past EMPTY, cut to the I/O budget.
+//   * finalize checks the whole final membership before anything is written, then
+//     writes the queue descriptors in final order, publishes the prefix that is already
+//     readable (cached groups, groups whose bytes arrived) and passes the groups still to
+//     read to the transport.
+//   * completions (transport threads) publish each READY member exactly once.
+//
+// The observable behaviour -- descriptors, publication order, queue words, return codes
+// and transport calls -- is pinned line by line against LeanStream's own runtime
+// (tests/golden/runtime_trace.txt, tests/golden/staging_trace.txt). The transport is
+// always a borrowed IOBackend; LeanStream's O_DIRECT engine is not part of this build.
 #include "leanstream/weight_manager.h"
 #include <algorithm>
 #include <atomic>
@@ -22,171 +32,316 @@
 #include <stdexcept>
 #include <vector>
 
-#ifdef LEANSTREAM_RUNTIME_TESTING
-extern "C" void leanstream_test_finalize_hook(int);
-#define LS_FINALIZE_POINT(n) leanstream_test_finalize_hook(n)
-#else
-#define LS_FINALIZE_POINT(n) ((void)0)
-#endif
-
 namespace leanstream::runtime {
 
 namespace {
 
-uint32_t load_state(const uint32_t* states, GroupId g) { return __atomic_load_n(states + g, __ATOMIC_ACQUIRE); }
+// Per-group marks cleared in O(1): a group is marked when its stamp equals the round.
+class GroupMarks {
+public:
+    explicit GroupMarks(size_t n) : stamp_(n, 0) {}
+    void clear() {
+        if (++round_ == 0) {   // the round counter wrapped: forget every stamp once
+            std::fill(stamp_.begin(), stamp_.end(), 0u);
+            round_ = 1;
+        }
+    }
+    // true if i was already marked in this round
+    bool mark(size_t i) {
+        const bool was = stamp_[i] == round_;
+        stamp_[i] = round_;
+        return was;
+    }
+    bool marked(size_t i) const { return stamp_[i] == round_; }
 
-ManagerConfig validated(ManagerConfig c) {
-    const bool bad = c.group_count == 0 || c.group_count > static_cast<uint32_t>(std::numeric_limits<int32_t>::max()) ||
-                     c.group_bytes == 0 || c.staging_stride < c.group_bytes ||
-                     c.staging_stride > std::numeric_limits<size_t>::max() / c.group_count;
-    if (bad) throw std::invalid_argument("layout geometry/capacity overflow");
+private:
+    std::vector<uint32_t> stamp_;
+    uint32_t round_ = 1;
+};
+
+uint32_t io_word(const uint32_t* states, GroupId g) { return __atomic_load_n(states + g, __ATOMIC_ACQUIRE); }
+
+// The bindings a prepared plan depends on; a plan is reused only for an equal key.
+struct PlanKey {
+    uint64_t plan_generation = 0, layout_generation = 0, staging_bytes = 0;
+    const GroupLayout* layout = nullptr;
+    size_t layout_size = 0;
+    const SlotId* cache_slots = nullptr;
+    const SlotId* destination_slots = nullptr;
+    const GroupId* core = nullptr;
+    size_t core_size = 0;
+    const ExecDesc* mapped_core = nullptr;
+    const void* staging = nullptr;
+    const uint32_t* io_states = nullptr;
+    DeviceExecQueue queue{};
+
+    static PlanKey of(const LayerStorage& s) {
+        PlanKey k;
+        k.plan_generation = s.plan_generation;
+        k.layout_generation = s.layout_generation;
+        k.staging_bytes = s.staging_bytes;
+        k.layout = s.layout.data;
+        k.layout_size = s.layout.size;
+        k.cache_slots = s.cache_slots;
+        k.destination_slots = s.destination_slots;
+        k.core = s.core.data;
+        k.core_size = s.core.size;
+        k.mapped_core = s.mapped_core_descriptors;
+        k.staging = s.staging;
+        k.io_states = s.io_states;
+        k.queue = s.queue;
+        return k;
+    }
+    // A nonzero plan generation that matches, with every binding equal.
+    bool reusable_for(const PlanKey& n) const {
+        return n.plan_generation && n.plan_generation == plan_generation && n.layout_generation == layout_generation &&
+               n.staging_bytes == staging_bytes && n.layout == layout && n.layout_size == layout_size &&
+               n.cache_slots == cache_slots && n.destination_slots == destination_slots && n.core == core &&
+               n.core_size == core_size && n.mapped_core == mapped_core && n.staging == staging &&
+               n.io_states == io_states && n.queue.descriptors == queue.descriptors &&
+               n.queue.ready_indices == queue.ready_indices && n.queue.control == queue.control &&
+               n.queue.capacity == queue.capacity;
+    }
+};
+
+const ManagerConfig& checked(const ManagerConfig& c) {
+    const bool geometry_ok = c.group_count && c.group_count <= static_cast<uint32_t>(std::numeric_limits<GroupId>::max()) &&
+                             c.group_bytes && c.staging_stride >= c.group_bytes &&
+                             c.staging_stride <= std::numeric_limits<size_t>::max() / c.group_count;
+    if (!geometry_ok) throw std::invalid_argument("layout geometry/capacity overflow");
     const IOBackend& io = c.io_backend;
     if (!io.begin) throw std::invalid_argument("an IOBackend transport is required");
-    if (!io.update || !io.consume || !io.retire || !io.ready_slot)
-        throw std::invalid_argument("incomplete borrowed IO backend");
+    if (!(io.update && io.consume && io.retire && io.ready_slot)) throw std::invalid_argument("incomplete IO backend");
     return c;
 }
 
 }  // namespace
 
 struct WeightManager::Impl {
-    ManagerConfig config;
-    LayerStorage storage{}, prepared{};
-    const GroupLayout* registered = nullptr;
-    uint64_t registered_generation = 0;
+    enum class Phase : uint8_t { Closed, Open, Frozen };
+
+    const ManagerConfig config;
+    const uint32_t n;
+    // layout registry: GroupLayout by logical id, valid for (source, generation)
     std::vector<GroupLayout> layout;
-    std::vector<GroupId> priority, final_reads;
-    std::vector<int32_t> final_index;
-    std::vector<uint8_t> seen, published, in_core;
-    std::vector<ExecDesc> own_core;
+    const GroupLayout* registered_from = nullptr;
+    uint64_t registered_generation = 0;
+    // core plan
+    std::vector<ExecDesc> core_table;   // used when no GPU-visible table is bound
     ExecDesc* core = nullptr;
     uint32_t core_count = 0;
-    ExecutionQueue queue;
-    std::mutex producer;
+    std::vector<uint8_t> resident;      // member of the core plan
+    bool prepared = false;
+    PlanKey prepared_key;
+    // the open epoch
+    LayerStorage bound{};
+    std::atomic<Phase> phase{Phase::Closed};
     std::atomic<uint32_t> epoch{0};
-    std::atomic<bool> active{false}, finalized{false};
     uint64_t generation = 0;
+    std::vector<GroupId> admitted;      // the last priority list handed to the transport
+    std::vector<int32_t> position;      // queue descriptor index per member (-1: none)
+    std::vector<uint8_t> published;     // member already visible to the consumer
+    std::vector<GroupId> to_read;       // members the transport still has to deliver
+    GroupMarks marks;
+    ExecutionQueue queue;
+    std::mutex producer;                // serialises every write of the queue
 
     explicit Impl(const ManagerConfig& c)
-        : config(c), layout(c.group_count), final_index(c.group_count, -1), seen(c.group_count),
-          published(c.group_count), in_core(c.group_count), own_core(c.group_count) {
-        priority.reserve(c.group_count);
-        final_reads.reserve(c.group_count);
+        : config(checked(c)), n(c.group_count), layout(n), core_table(n), resident(n), position(n, -1), published(n),
+          marks(n) {
+        admitted.reserve(n);
+        to_read.reserve(n);
     }
 
-    bool in_range(GroupId g) const { return g >= 0 && static_cast<uint32_t>(g) < config.group_count; }
-    void clear_seen() { std::fill(seen.begin(), seen.end(), 0); }
+    bool valid_group(GroupId g) const { return g >= 0 && static_cast<uint32_t>(g) < n; }
+    bool valid_slot(SlotId s) const { return s >= 0 && static_cast<uint32_t>(s) < n; }
+    bool is_open() const { return phase.load(std::memory_order_acquire) != Phase::Closed; }
+    bool is_frozen() const { return phase.load(std::memory_order_acquire) == Phase::Frozen; }
+    const IOBackend& io() const { return config.io_backend; }
 
-    // producer lock held; the completed bytes are already visible to the GPU
-    void publish_ready(GroupId g, SlotId slot) {
-        const int32_t index = final_index[g];
-        if (index < 0 || published[g]) return;
-        if (slot < 0) slot = config.io_backend.ready_slot(config.io_backend.context, g);
-        if (slot < 0 || static_cast<uint32_t>(slot) >= config.group_count) {
+    // ---- prepare ----
+    int check_bindings(const LayerStorage& s) const {
+        const bool complete = s.layout.data && s.cache_slots && s.staging && s.io_states && s.queue.control &&
+                              s.queue.descriptors && s.queue.ready_indices;
+        if (!complete || s.layout.size != n || s.queue.capacity > n || s.core.size > n || (s.core.size && !s.core.data))
+            return EINVAL;
+        if (s.staging_bytes && s.staging_bytes < n * config.staging_stride) return ENOSPC;
+        return 0;
+    }
+
+    int register_layout(const LayerStorage& s) {
+        if (s.layout_generation && s.layout_generation == registered_generation && s.layout.data == registered_from)
+            return 0;
+        registered_from = nullptr;
+        registered_generation = 0;
+        marks.clear();
+        for (size_t i = 0; i < s.layout.size; ++i) {
+            const GroupLayout& e = s.layout[i];
+            if (e.logical_group >= n || marks.mark(e.logical_group) || e.bytes != config.group_bytes) return EINVAL;
+            layout[e.logical_group] = e;
+        }
+        registered_from = s.layout.data;
+        registered_generation = s.layout_generation;
+        return 0;
+    }
+
+    int plan_core(const LayerStorage& s) {
+        std::fill(resident.begin(), resident.end(), 0);
+        marks.clear();   // destination rows taken by core groups
+        core = s.mapped_core_descriptors ? s.mapped_core_descriptors : core_table.data();
+        core_count = static_cast<uint32_t>(s.core.size);
+        for (uint32_t i = 0; i < core_count; ++i) {
+            const GroupId g = s.core[i];
+            if (!valid_group(g) || resident[g] || s.cache_slots[g] < 0) return EINVAL;
+            resident[g] = 1;
+            uint32_t row = i;
+            if (s.destination_slots) {
+                const SlotId d = s.destination_slots[g];
+                if (!valid_slot(d) || marks.mark(static_cast<size_t>(d))) return EINVAL;
+                row = static_cast<uint32_t>(d);
+            }
+            ExecDesc& e = core[i];
+            e.logical_group = static_cast<uint32_t>(g);
+            e.physical_group = layout[g].physical_group;
+            e.source_slot = static_cast<uint32_t>(s.cache_slots[g]);
+            e.dest_slot = row;
+            e.source_kind = SourceKind::Cache;
+        }
+        return 0;
+    }
+
+    // ---- finalize ----
+    // Members in final order; every core group present, no group twice or outside, the
+    // queued ones fit the queue, destination rows (when bound) distinct. Nothing is
+    // written before the whole list passed.
+    int check_membership(Span<GroupId> ids, uint32_t& queued) {
+        marks.clear();
+        queued = 0;
+        for (size_t i = 0; i < ids.size; ++i) {
+            if (!valid_group(ids[i]) || marks.mark(static_cast<size_t>(ids[i]))) return EINVAL;
+            queued += resident[ids[i]] ? 0u : 1u;
+        }
+        for (uint32_t g = 0; g < n; ++g)
+            if (resident[g] && !marks.marked(g)) return EINVAL;
+        if (queued > bound.queue.capacity) return ENOSPC;
+        if (const SlotId* rows = bound.destination_slots) {
+            marks.clear();
+            for (size_t i = 0; i < ids.size; ++i)
+                if (!valid_slot(rows[ids[i]]) || marks.mark(static_cast<size_t>(rows[ids[i]]))) return EINVAL;
+        }
+        return 0;
+    }
+
+    // Queue descriptors of the non-core members, in final order. A cached group is read
+    // from its cache slot; the others come from staging (slot filled when READY).
+    void write_queue_plan(Span<GroupId> ids) {
+        to_read.clear();
+        uint32_t next = 0;
+        for (size_t i = 0; i < ids.size; ++i) {
+            const GroupId g = ids[i];
+            if (resident[g]) continue;
+            const SlotId cached = bound.cache_slots[g];
+            ExecDesc& e = bound.queue.descriptors[next];
+            e.logical_group = static_cast<uint32_t>(g);
+            e.physical_group = layout[g].physical_group;
+            e.source_slot = cached >= 0 ? static_cast<uint32_t>(cached) : 0u;
+            e.dest_slot = bound.destination_slots ? static_cast<uint32_t>(bound.destination_slots[g]) : core_count + next;
+            e.source_kind = cached >= 0 ? SourceKind::Cache : SourceKind::Staging;
+            position[g] = static_cast<int32_t>(next++);
+            if (cached < 0) to_read.push_back(g);
+        }
+    }
+
+    // The prefix visible at activation: cached members and members already READY, in
+    // final order. Producer lock held.
+    int stage_prefix(Span<GroupId> ids) {
+        for (size_t i = 0; i < ids.size; ++i) {
+            const GroupId g = ids[i];
+            if (resident[g]) continue;
+            if (bound.cache_slots[g] < 0) {
+                if (io_word(bound.io_states, g) != kIoReady) continue;
+                const SlotId slot = io().ready_slot(io().context, g);
+                if (!valid_slot(slot)) {
+                    queue.fail(EIO);
+                    return EIO;
+                }
+                bound.queue.descriptors[position[g]].source_slot = static_cast<uint32_t>(slot);
+            }
+            published[g] = 1;
+            queue.append_unpublished(static_cast<uint32_t>(position[g]));
+        }
+        return 0;
+    }
+
+    // ---- completions (transport threads) ----
+    // Producer lock held: a READY member becomes visible once, reading its staging slot.
+    void publish_member(GroupId g, SlotId slot) {
+        if (position[g] < 0 || published[g]) return;
+        if (slot < 0) slot = io().ready_slot(io().context, g);
+        if (!valid_slot(slot)) {
             queue.fail(EIO);
             return;
         }
-        ExecDesc& d = storage.queue.descriptors[index];
-        d.source_slot = static_cast<uint32_t>(slot);
-        d.source_kind = SourceKind::Staging;
+        ExecDesc& e = bound.queue.descriptors[position[g]];
+        e.source_slot = static_cast<uint32_t>(slot);
+        e.source_kind = SourceKind::Staging;
         published[g] = 1;
-        queue.publish(static_cast<uint32_t>(index));
+        queue.publish(static_cast<uint32_t>(position[g]));
     }
 
-    static void on_completion(void* arg, const IOCompletion& n) {
+    bool current(uint32_t at_epoch) const { return is_open() && at_epoch == epoch.load(std::memory_order_relaxed); }
+
+    static void on_delivery(void* arg, const IOCompletion& c) {
         Impl& m = *static_cast<Impl*>(arg);
-        if (!m.active.load(std::memory_order_acquire) || n.epoch != m.epoch.load(std::memory_order_relaxed)) return;
-        if (n.error) {
+        if (!m.current(c.epoch)) return;   // a late delivery of another epoch
+        if (c.error) {
             std::lock_guard<std::mutex> lock(m.producer);
-            if (m.active && n.epoch == m.epoch) m.queue.fail(static_cast<uint32_t>(n.error));
+            if (m.current(c.epoch)) m.queue.fail(static_cast<uint32_t>(c.error));
             return;
         }
-        if (!m.in_range(n.logical_group) || n.staging_slot < 0 ||
-            static_cast<uint32_t>(n.staging_slot) >= m.config.group_count) {
+        if (!m.valid_group(c.logical_group) || !m.valid_slot(c.staging_slot)) {
             m.queue.fail(EINVAL);
             return;
         }
-        // Before finalize the plan does not exist; finalize publishes READY groups itself.
-        if (!m.finalized.load(std::memory_order_acquire)) return;
+        // before finalize there is no plan: finalize publishes what is READY by then
+        if (!m.is_frozen()) return;
         std::lock_guard<std::mutex> lock(m.producer);
-        if (m.active && n.epoch == m.epoch) m.publish_ready(n.logical_group, n.staging_slot);
+        if (m.current(c.epoch)) m.publish_member(c.logical_group, c.staging_slot);
     }
 };
 
-WeightManager::WeightManager(ManagerConfig c) : impl_(new Impl(validated(c))) {}
+WeightManager::WeightManager(ManagerConfig c) : impl_(new Impl(c)) {}
 WeightManager::~WeightManager() = default;
 
 int WeightManager::prepare_layer(const LayerStorage& s) {
     Impl& m = *impl_;
-    if (m.active) return EBUSY;
-    const uint32_t n = m.config.group_count;
-    const bool missing = !s.layout.data || !s.cache_slots || !s.staging || !s.io_states || !s.queue.control ||
-                         !s.queue.descriptors || !s.queue.ready_indices;
-    if (s.layout.size != n || missing || s.queue.capacity > n || (s.core.size && !s.core.data) || s.core.size > n)
-        return EINVAL;
-    if (s.staging_bytes && s.staging_bytes < n * m.config.staging_stride) return ENOSPC;
-    m.prepared = {};
-    const bool registered = s.layout_generation && s.layout_generation == m.registered_generation &&
-                            s.layout.data == m.registered;
-    if (!registered) {
-        m.registered = nullptr;
-        m.registered_generation = 0;
-        m.clear_seen();
-        for (size_t i = 0; i < s.layout.size; ++i) {
-            const GroupLayout& g = s.layout[i];
-            if (g.logical_group >= n || m.seen[g.logical_group]++ || g.bytes != m.config.group_bytes) return EINVAL;
-            m.layout[g.logical_group] = g;
-        }
-        m.registered = s.layout.data;
-        m.registered_generation = s.layout_generation;
-    }
-    std::fill(m.in_core.begin(), m.in_core.end(), 0);
-    m.clear_seen();  // destination slots claimed by core groups
-    m.core_count = static_cast<uint32_t>(s.core.size);
-    m.core = s.mapped_core_descriptors ? s.mapped_core_descriptors : m.own_core.data();
-    for (size_t i = 0; i < s.core.size; ++i) {
-        const GroupId g = s.core[i];
-        if (!m.in_range(g) || m.in_core[g]++ || s.cache_slots[g] < 0) return EINVAL;
-        if (s.destination_slots) {
-            const SlotId d = s.destination_slots[g];
-            if (d < 0 || static_cast<uint32_t>(d) >= n || m.seen[d]++) return EINVAL;
-        }
-        m.core[i] = {static_cast<uint32_t>(g), m.layout[g].physical_group, static_cast<uint32_t>(s.cache_slots[g]),
-                     static_cast<uint32_t>(s.destination_slots ? s.destination_slots[g] : static_cast<SlotId>(i)),
-                     SourceKind::Cache};
-    }
-    m.prepared = s;
+    if (m.is_open()) return EBUSY;
+    if (const int rc = m.check_bindings(s)) return rc;
+    m.prepared = false;
+    if (const int rc = m.register_layout(s)) return rc;
+    if (const int rc = m.plan_core(s)) return rc;
+    m.prepared = true;
+    m.prepared_key = PlanKey::of(s);
     return 0;
 }
 
 int WeightManager::begin_layer(uint32_t, const LayerStorage& s) {
     Impl& m = *impl_;
-    if (m.active) return EBUSY;
-    if (m.epoch == std::numeric_limits<uint32_t>::max()) return EOVERFLOW;
-    const LayerStorage& p = m.prepared;
-    const bool reuse = s.plan_generation && s.plan_generation == p.plan_generation && s.layout.data == p.layout.data &&
-                       s.layout.size == p.layout.size && s.layout_generation == p.layout_generation &&
-                       s.cache_slots == p.cache_slots && s.destination_slots == p.destination_slots &&
-                       s.core.data == p.core.data && s.core.size == p.core.size &&
-                       s.mapped_core_descriptors == p.mapped_core_descriptors && s.queue.control == p.queue.control &&
-                       s.queue.descriptors == p.queue.descriptors && s.queue.ready_indices == p.queue.ready_indices &&
-                       s.queue.capacity == p.queue.capacity && s.staging == p.staging && s.io_states == p.io_states &&
-                       s.staging_bytes == p.staging_bytes;
-    if (!reuse) {
-        const int rc = prepare_layer(s);
-        if (rc) return rc;
-    }
-    m.storage = s;
+    if (m.is_open()) return EBUSY;
+    if (m.epoch.load() == std::numeric_limits<uint32_t>::max()) return EOVERFLOW;
+    if (!(m.prepared && m.prepared_key.reusable_for(PlanKey::of(s))))
+        if (const int rc = prepare_layer(s)) return rc;
+    m.bound = s;
     m.queue.bind(s.queue);
-    m.queue.reset(++m.epoch);
-    std::fill(m.final_index.begin(), m.final_index.end(), -1);
+    const uint32_t e = m.epoch.load() + 1;
+    m.epoch.store(e);
+    m.queue.reset(e);
+    std::fill(m.position.begin(), m.position.end(), -1);
     std::fill(m.published.begin(), m.published.end(), 0);
     m.generation = 0;
-    m.finalized = false;
-    m.active = true;
-    const IOBackend& io = m.config.io_backend;
-    const int rc = io.begin(io.context, Impl::on_completion, &m, m.epoch);
-    if (rc) m.active = false;
+    m.phase.store(Impl::Phase::Open, std::memory_order_release);
+    const int rc = m.io().begin(m.io().context, Impl::on_delivery, &m, e);
+    if (rc) m.phase.store(Impl::Phase::Closed, std::memory_order_release);
     return rc;
 }
 
@@ -194,133 +349,81 @@ int WeightManager::update_prediction(Span<GroupId> ids) { return update_predicti
 
 int WeightManager::update_prediction(Span<GroupId> ids, PredictionUpdateOptions options) {
     Impl& m = *impl_;
-    if (!m.active || m.finalized || (ids.size && !ids.data)) return EINVAL;
-    if (options.execution_epoch && options.execution_epoch != m.epoch) return ESTALE;
-    m.clear_seen();
-    m.priority.clear();
+    if (m.phase.load(std::memory_order_acquire) != Impl::Phase::Open || (ids.size && !ids.data)) return EINVAL;
+    if (options.execution_epoch && options.execution_epoch != m.epoch.load()) return ESTALE;
+    m.marks.clear();
+    m.admitted.clear();
     for (size_t i = 0; i < ids.size; ++i) {
         const GroupId g = ids[i];
-        if (!m.in_range(g)) return EINVAL;
-        if (m.seen[g]) continue;
-        m.seen[g] = 1;
-        // Cached, READY and INFLIGHT groups never spend the I/O budget.
-        if (m.storage.cache_slots[g] < 0 && load_state(m.storage.io_states, g) == kIoEmpty) m.priority.push_back(g);
+        if (!m.valid_group(g)) return EINVAL;
+        if (m.marks.mark(static_cast<size_t>(g))) continue;   // later duplicates keep the first rank
+        // cached, in-flight and ready groups never spend the I/O budget
+        const bool needs_read = m.bound.cache_slots[g] < 0 && io_word(m.bound.io_states, g) == kIoEmpty;
+        if (needs_read && m.admitted.size() < options.io_budget) m.admitted.push_back(g);
     }
-    if (m.priority.size() > options.io_budget) m.priority.resize(options.io_budget);
-    const IOBackend& io = m.config.io_backend;
-    const int rc = io.update(io.context, {m.priority.data(), m.priority.size()});
+    const int rc = m.io().update(m.io().context, {m.admitted.data(), m.admitted.size()});
     if (!rc) ++m.generation;
     return rc;
 }
 
 int WeightManager::finalize(Span<GroupId> ids) {
     Impl& m = *impl_;
-    if (!m.active || m.finalized || (ids.size && !ids.data) || ids.size < m.core_count) return EINVAL;
-    const uint32_t n = m.config.group_count;
-    // 1. validate the whole membership before anything becomes visible
-    m.clear_seen();
-    m.final_reads.clear();
+    if (m.phase.load(std::memory_order_acquire) != Impl::Phase::Open || (ids.size && !ids.data) ||
+        ids.size < m.core_count)
+        return EINVAL;
     uint32_t queued = 0;
-    for (size_t i = 0; i < ids.size; ++i) {
-        const GroupId g = ids[i];
-        if (!m.in_range(g) || m.seen[g]++) return EINVAL;
-        if (!m.in_core[g]) ++queued;
-    }
-    for (uint32_t g = 0; g < n; ++g)
-        if (m.in_core[g] && !m.seen[g]) return EINVAL;
-    if (queued > m.storage.queue.capacity) return ENOSPC;
-    if (m.storage.destination_slots) {
-        m.clear_seen();
-        for (size_t i = 0; i < ids.size; ++i) {
-            const SlotId d = m.storage.destination_slots[ids[i]];
-            if (d < 0 || static_cast<uint32_t>(d) >= n || m.seen[d]++) return EINVAL;
-        }
-    }
-    LS_FINALIZE_POINT(0);
+    if (const int rc = m.check_membership(ids, queued)) return rc;
     {
         std::lock_guard<std::mutex> lock(m.producer);
-        // 2. descriptors in final order, core groups excluded
-        uint32_t idx = 0;
-        for (size_t i = 0; i < ids.size; ++i) {
-            const GroupId g = ids[i];
-            if (m.in_core[g]) continue;
-            const SlotId slot = m.storage.cache_slots[g];
-            const uint32_t dest = m.storage.destination_slots ? static_cast<uint32_t>(m.storage.destination_slots[g])
-                                                               : m.core_count + idx;
-            m.storage.queue.descriptors[idx] = {static_cast<uint32_t>(g), m.layout[g].physical_group,
-                                                slot < 0 ? 0u : static_cast<uint32_t>(slot), dest,
-                                                slot < 0 ? SourceKind::Staging : SourceKind::Cache};
-            m.final_index[g] = static_cast<int32_t>(idx++);
-            if (slot < 0) m.final_reads.push_back(g);
-        }
-        LS_FINALIZE_POINT(1);
+        m.write_queue_plan(ids);
         m.queue.prepare(queued);
-        m.finalized.store(true, std::memory_order_release);
-        // 3. initial prefix: cached groups and groups whose bytes already arrived
-        const IOBackend& io = m.config.io_backend;
-        for (size_t i = 0; i < ids.size; ++i) {
-            const GroupId g = ids[i];
-            if (m.in_core[g]) continue;
-            const uint32_t index = static_cast<uint32_t>(m.final_index[g]);
-            if (m.storage.cache_slots[g] >= 0) {
-                m.published[g] = 1;
-                m.queue.append_unpublished(index);
-            } else if (load_state(m.storage.io_states, g) == kIoReady) {
-                const SlotId source = io.ready_slot(io.context, g);
-                if (source < 0 || static_cast<uint32_t>(source) >= n) {
-                    m.queue.fail(EIO);
-                    return EIO;
-                }
-                m.storage.queue.descriptors[index].source_slot = static_cast<uint32_t>(source);
-                m.published[g] = 1;
-                m.queue.append_unpublished(index);
-            }
-        }
+        m.phase.store(Impl::Phase::Frozen, std::memory_order_release);
+        if (const int rc = m.stage_prefix(ids)) return rc;
         m.queue.activate();
     }
-    LS_FINALIZE_POINT(2);
-    const IOBackend& io = m.config.io_backend;
-    const int rc = io.consume(io.context, {m.final_reads.data(), m.final_reads.size()});
+    const int rc = m.io().consume(m.io().context, {m.to_read.data(), m.to_read.size()});
     if (rc) m.queue.fail(static_cast<uint32_t>(rc));
     return rc;
 }
 
 int WeightManager::retire() {
     Impl& m = *impl_;
-    if (!m.active) return EINVAL;
-    const IOBackend& io = m.config.io_backend;
-    const int rc = io.retire(io.context);  // drains callbacks before the epoch can change
+    if (!m.is_open()) return EINVAL;
+    // the transport drains its callbacks before the epoch can change
+    const int rc = m.io().retire(m.io().context);
     std::lock_guard<std::mutex> lock(m.producer);
-    m.active = false;
+    m.phase.store(Impl::Phase::Closed, std::memory_order_release);
     return rc;
 }
 
 void WeightManager::cancel(int error) {
-    if (impl_->active) impl_->queue.fail(static_cast<uint32_t>(error ? error : ECANCELED));
+    Impl& m = *impl_;
+    if (m.is_open()) m.queue.fail(static_cast<uint32_t>(error ? error : ECANCELED));
 }
 
 GroupState WeightManager::group_state(GroupId g) const {
     const Impl& m = *impl_;
-    if (!m.active || !m.in_range(g)) return {};
-    const uint32_t s = load_state(m.storage.io_states, g);
-    SlotId slot = -1;
-    if (s == kIoReady || s == kIoInflight) slot = m.config.io_backend.ready_slot(m.config.io_backend.context, g);
-    const IOState state = s == kIoReady ? IOState::Ready : s == kIoInflight ? IOState::Inflight : IOState::Empty;
-    return {m.storage.cache_slots[g], slot, state};
+    GroupState st;
+    if (!m.is_open() || !m.valid_group(g)) return st;
+    const uint32_t w = io_word(m.bound.io_states, g);
+    st.cache_slot = m.bound.cache_slots[g];
+    st.io_state = w == kIoReady ? IOState::Ready : w == kIoInflight ? IOState::Inflight : IOState::Empty;
+    if (st.io_state != IOState::Empty) st.staging_slot = m.io().ready_slot(m.io().context, g);
+    return st;
 }
 
 uint64_t WeightManager::prediction_generation() const { return impl_->generation; }
-uint32_t WeightManager::epoch() const { return impl_->epoch; }
-DeviceExecQueue WeightManager::queue() const { return impl_->storage.queue; }
+uint32_t WeightManager::epoch() const { return impl_->epoch.load(); }
+DeviceExecQueue WeightManager::queue() const { return impl_->bound.queue; }
 Span<ExecDesc> WeightManager::core_descriptors() const { return {impl_->core, impl_->core_count}; }
 
 int WeightManager::wait_io(int timeout_ms) {
-    const IOBackend& io = impl_->config.io_backend;
+    const IOBackend& io = impl_->io();
     return io.wait ? io.wait(io.context, timeout_ms) : ENOTSUP;
 }
 
 uint64_t WeightManager::read_requests() const {
-    const IOBackend& io = impl_->config.io_backend;
+    const IOBackend& io = impl_->io();
     return io.requests ? io.requests(io.context) : 0;
 }
 

@@ -1220,13 +1220,34 @@ __device__ __forceinline__ void dn_accumulate_staged(const u32x4* sl, uint64_t h
     }
 }
 
+// The first descriptor batch of the resident range, fetched at the worker's start.
+struct Prefetched {
+    uint32_t word;
+    bool valid;
+};
+
+template <int D>
+__device__ __forceinline__ void prefetch_core_descs(const MlpArgs& a, uint32_t* slot, const WaveRole& role,
+                                                    Prefetched& p) {
+    constexpr uint32_t ipu = kStagedGroup / GuGeom<D>::NPI;
+    constexpr uint32_t T = D / kDnCols;
+    p.valid = false;
+    p.word = 0;
+    if (!a.core_count) return;
+    const ItemList il = make_items(role, a.core_count * ipu, a.core_count * T);
+    if (!il.K) return;
+    uint32_t seen = 0;
+    // resident units are never waited for: this cannot fail
+    p.valid = fetch_descs(a, slot, 0, seen, il, 0, min(il.K, (uint32_t)kDescItems), ipu, T, 1u, p.word);
+}
+
 // This wave's items of units [u0, u1) through its two LDS slots (stage: kWaves x 2 slots).
 // Same item lists, waits and reduction as process_items.
 template <int D, bool FUSED>
 __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& sh, u32x4* stage, uint32_t* slot,
                                                      const Bounds& b, unsigned long long* yacc, XPart<D>& xp,
                                                      u32x4* xl, Epoch& ep, uint32_t early, Pending& pd, uint32_t u0,
-                                                     uint32_t u1, const WaveRole& role) {
+                                                     uint32_t u1, const WaveRole& role, const Prefetched& first) {
     using Gm = GuGeom<D>;
     constexpr uint32_t T = D / kDnCols;
     constexpr uint32_t G = kStagedGroup;
@@ -1240,8 +1261,9 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
         return r;
     };
     if (!K) return leave(true);
-    uint32_t seen = 0, word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, 1u, word)) return leave(false);
+    uint32_t seen = 0, word = first.word, k0 = 0;
+    if (!first.valid && !fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, 1u, word))
+        return leave(false);
     if (a.stamps) {
         asm volatile("" : : "v"(word));   // the stamp waits for the descriptors
         stamp(a, kStampDescs);
@@ -1522,7 +1544,7 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
 template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, bool STAGED>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, u32x4* stage,
                                        uint32_t* slot) {
-    const uint32_t W = QUEUE ? gridDim.x - 1 : gridDim.x;
+    const uint32_t W = QUEUE ? a.grid - 1 : a.grid;
     const uint32_t wave = wave_id();
     // Roles by workgroup: the first gu_wgs workgroups take the gate/up items, the others
     // the down items (one workgroup alone takes both).
@@ -1532,10 +1554,17 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     XPart<D> xp;
     const uint32_t xrows = NB == 1 ? 1u : a.batch;   // the NB = 1 kernels hold one row of x
     load_x<D>(a.x, xrows, xp, xl);
+    // The staged walk's first descriptors of the resident range go out with x, before the
+    // workgroup's first barrier: that barrier also waits for the argument block's scalar
+    // loads, which the loads above (preloaded arguments only) do not need.
+    Prefetched first{};
+    if constexpr (STAGED && CORE) prefetch_core_descs<D>(a, slot, role, first);
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
     const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
+    if (threadIdx.x == 0) sh.xcount = 0;   // waves count themselves in once their part of x is staged
+    __syncthreads();
     bool ok = true;
     enum : uint32_t { kCore, kDecide, kClaim, kPairs, kDone };
     uint32_t phase = CORE ? kCore : kDecide;
@@ -1598,10 +1627,12 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
             break;
         }
         if (u1 > u0) {
-            if constexpr (STAGED)
-                ok = process_items_staged<D, FUSED>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
-            else
+            if constexpr (STAGED) {
+                ok = process_items_staged<D, FUSED>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r, first);
+                first.valid = false;   // only the resident range's first batch is prefetched
+            } else {
                 ok = process_items<D, FUSED, NB>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+            }
         }
     }
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
@@ -1688,21 +1719,43 @@ struct StageArea {
     static constexpr int VECS = STAGED ? 2 * kWaves * kSlotStride : kWaves * kDnCols / 4;
 };
 
+// The arguments a persistent worker needs before its first loads (x, its descriptors,
+// the weight arenas, its ring slot, the grid) lead the kernel's argument list as scalars,
+// so they can be preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count); the
+// block of the remaining arguments is read from the kernel-argument segment while the
+// first loads are in flight.
+#define LS_HOT_PARAMS                                                                                     \
+    const uint16_t *hot_x, const ExecDesc *hot_core, const uint8_t *hot_cache, const uint16_t *hot_scales, \
+        uint32_t *slot, uint32_t hot_core_count, uint32_t hot_seq, uint32_t hot_grid, MlpArgs args, Bounds b
+__device__ __forceinline__ MlpArgs with_hot(const MlpArgs& args, const uint16_t* x, const ExecDesc* core,
+                                            const uint8_t* cache, const uint16_t* scales, uint32_t core_count,
+                                            uint32_t seq, uint32_t grid) {
+    MlpArgs a = args;
+    a.x = x;
+    a.core = core;
+    a.cache = cache;
+    a.scales = scales;
+    a.core_count = core_count;
+    a.seq = seq;
+    a.grid = grid;
+    return a;
+}
+// `slot` (this launch's ring slot, sync + (seq & 1) slot_words) is a parameter of its own.
+#define LS_HOT_ARGS with_hot(args, hot_x, hot_core, hot_cache, hot_scales, hot_core_count, hot_seq, hot_grid)
+
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
 template <int D, int NB, bool STAGED>
-__global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_PARAMS) {
     static_assert(!STAGED || NB == 1, "the staged walk serves batch 1");
+    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<STAGED>::VECS];
-    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    if (threadIdx.x == 0) sh.xcount = 0;
-    __syncthreads();
-    if (blockIdx.x == gridDim.x - 1) {
+    if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
-        if (threadIdx.x < 64) await_workers(a, slot, gridDim.x - 1);
+        if (threadIdx.x < 64) await_workers(a, slot, a.grid - 1);
     } else {
         stamp(a, kStampEntry);
         worker<D, true, true, true, NB, STAGED>(a, b, sh, xl, stage, slot);
@@ -1713,26 +1766,22 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(MlpArgs
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
 template <int D, int NB, bool STAGED>
-__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(LS_HOT_PARAMS) {
+    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<STAGED>::VECS];
-    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    if (threadIdx.x == 0) sh.xcount = 0;
-    __syncthreads();
     worker<D, false, true, false, NB, STAGED>(a, b, sh, xl, stage, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
 template <int D, int NB, bool STAGED>
-__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(LS_HOT_PARAMS) {
+    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<STAGED>::VECS];
-    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    if (threadIdx.x == 0) sh.xcount = 0;
-    __syncthreads();
-    if (blockIdx.x == gridDim.x - 1) {
+    if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         return;
@@ -2225,15 +2274,24 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     Bounds b = bounds;
     if (a.batch < 1 || a.batch > kMaxBatch) return hipErrorInvalidValue;
     const int nb = family(p.width, (int)a.batch, (int)a.group_size);
-    void* kargs[] = {&a, &b};
-    if (p.entry_point == kEntryFused)
-        return hipLaunchKernel(v->fused[nb], dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
+    // the persistent kernels' leading scalars (LS_HOT_PARAMS), then the argument blocks
+    uint32_t grid = (uint32_t)p.workers + 1;
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    void* kargs[] = {&a.x, &a.core, &a.cache, &a.scales, &slot, &a.core_count, &a.seq, &grid, &a, &b};
+    if (p.entry_point == kEntryFused) {
+        a.grid = grid;
+        return hipLaunchKernel(v->fused[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
+    }
     hipError_t e = hipSuccess;
     if (a.core_count) {
-        e = hipLaunchKernel(v->stage_a[nb], dim3(p.workers), dim3(kThreads), kargs, 0, stream);
+        grid = (uint32_t)p.workers;   // stage A has no mirror workgroup
+        a.grid = grid;
+        e = hipLaunchKernel(v->stage_a[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
         if (e != hipSuccess) return e;
     }
-    e = hipLaunchKernel(v->stage_b[nb], dim3(p.workers + 1), dim3(kThreads), kargs, 0, stream);
+    grid = (uint32_t)p.workers + 1;
+    a.grid = grid;
+    e = hipLaunchKernel(v->stage_b[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
     return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
