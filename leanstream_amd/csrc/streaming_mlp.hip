@@ -711,23 +711,41 @@ __device__ __forceinline__ unsigned long long acc_term(const MlpArgs& a, uint32_
     return (unsigned long long)(__float2ll_rn(v) + kAccBias) + kAccOne;
 }
 
+// Columns of a lane's four sums of a down tile: dn_tile_column(l) + kTileColOff[i]. Each
+// atomic instruction then covers 64 consecutive columns (four 128-byte lines).
+__device__ __forceinline__ int dn_tile_column(int lane) { return lane; }
+__device__ constexpr int kTileColOff[4] = {0, 64, 128, 192};
+
 // The accumulator words returned by a wave's last column additions, checked once the
 // next additions are issued (or at the end), so the wave does not wait for the atomics'
 // round trip: the contribution that completes a column (count U) writes the output.
-// Lane l's four columns are col + l + 64 i (i < 4): each atomic instruction covers 64
-// consecutive columns (four 128-byte lines).
+// Each atomic instruction covers four runs of 16 consecutive columns (four 128-byte
+// lines): a lane's columns are col + kTileColOff[i] (i < n).
 struct Pending {
     unsigned long long v[4];
-    int col;   // first column of the lane's four; < 0: nothing pending
+    int col;   // first column of the lane's n; < 0: nothing pending
+    int n;     // columns col + kTileColOff[i], i < n (4: 256-column tiles, 1: 64-column quarters)
 };
 
 __device__ __forceinline__ void check_pending(const MlpArgs& a, Pending& pd, uint32_t U) {
     if (pd.col >= 0 && U) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            if ((uint32_t)(pd.v[i] >> 52) == U) write_output(a, pd.col + 64 * i, pd.v[i], U);
+            if (i < pd.n && (uint32_t)(pd.v[i] >> 52) == U) write_output(a, pd.col + kTileColOff[i], pd.v[i], U);
     }
     pd.col = -1;
+}
+
+// One column per lane (the quarters of the staged walk).
+__device__ __forceinline__ void add_column(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, int col,
+                                           float c, uint32_t U, Pending& pd) {
+    const unsigned long long t = acc_term(a, slot, c);
+    const unsigned long long v =
+        __hip_atomic_fetch_add(yacc + (size_t)col * kAccStride, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t;
+    check_pending(a, pd, U);
+    pd.v[0] = v;
+    pd.col = col;
+    pd.n = 1;
 }
 
 __device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, unsigned long long* yacc, int col,
@@ -736,13 +754,14 @@ __device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, un
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned long long t = acc_term(a, slot, c[i]);
-        n[i] = __hip_atomic_fetch_add(yacc + (size_t)(col + 64 * i) * kAccStride, t, __ATOMIC_RELAXED,
+        n[i] = __hip_atomic_fetch_add(yacc + (size_t)(col + kTileColOff[i]) * kAccStride, t, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT) + t;
     }
     check_pending(a, pd, U);
 #pragma unroll
     for (int i = 0; i < 4; ++i) pd.v[i] = n[i];
     pd.col = col;
+    pd.n = 4;
 }
 
 // Execution counters (diagnostics): a unit counts once all of its down items are done.
@@ -810,6 +829,24 @@ __device__ __forceinline__ ItemList make_items(const WaveRole& r, uint32_t NG, u
         l.ds = r.nw - r.gu_waves;
         l.K = stride_count(l.d0, ND, l.ds);
     }
+    return l;
+}
+
+// The staged walk's lists: one stripe over the gate/up items and then the down quarters,
+// as in make_items, with the quarters starting at the next multiple of 4 after the
+// gate/up items: with nw a multiple of 4 the four quarters 4t .. 4t + 3 of a tile go to
+// the four waves of one workgroup (q = w mod 4). Each wave takes at most one item more
+// than an even share, and its items keep the order of the list.
+__device__ __forceinline__ ItemList make_staged_items(const WaveRole& r, uint32_t NG, uint32_t NDQ) {
+    const uint32_t NGa = (NG + 3u) & ~3u;
+    ItemList l;
+    l.NG = NG;
+    l.g0 = r.w;
+    l.gs = r.nw;
+    l.KG = stride_count(r.w, NG, r.nw);
+    l.d0 = r.w + stride_count(r.w, NGa, r.nw) * r.nw - NGa;   // the stripe's first position >= NGa
+    l.ds = r.nw;
+    l.K = l.KG + stride_count(l.d0, NDQ, r.nw);
     return l;
 }
 
@@ -1006,15 +1043,16 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         float cs[4];
         dn_reduce(acc, cs);
         // re-deal through LDS: lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds
-        // columns l + 64 i
+        // columns dn_tile_column(l) + kTileColOff[i], as the staged walk does
         const int lane = lane_id();
         float* red = reinterpret_cast<float*>(stage) + wave * kDnCols;
         *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        const int col0 = dn_tile_column(lane);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cs[i] = red[lane + 64 * i];
+        for (int i = 0; i < 4; ++i) cs[i] = red[col0 + kTileColOff[i]];
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        add_columns(a, slot, yacc, (int)(m.row * D + m.tile * kDnCols) + lane, cs, U, pd);
+        add_columns(a, slot, yacc, (int)(m.row * D + m.tile * kDnCols) + col0, cs, U, pd);
         if (a.executions) count_execution(a, slot, m.unit, m.dest, T * nb);
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
@@ -1119,11 +1157,64 @@ __device__ __forceinline__ void gu_stage(const uint8_t* grp, const uint16_t* sc,
     }
 }
 
-// Down item: tile `tile` (256 columns) of the unit's 64 rows. Lane 8 g + dc's piece j is
-// row 8 g + j, columns 32 dc .. 32 dc + 31, at slot[j 64 + l]; the scale block holds the
-// tile's two scales of row l in word l.
+// Down quarter: columns 64 q .. 64 q + 63 of tile `tile` (256 columns) of the unit's 64
+// rows: 2 KB of weights and the tile's scales. LDS row r of the slot holds the quarter's
+// 32 bytes of unit row r (lane l of load j brings row 32 j + l / 2, half l & 1); word l of
+// the scale block holds row l's two scales of the tile (128-column blocks 2 tile, 2 tile +
+// 1). The 4 quarters of a tile are taken by the 4 waves of one workgroup, so each 128-byte
+// row line is requested by one CU.
 template <int D>
-__device__ __forceinline__ void dn_stage(const uint8_t* grp, const uint16_t* sc, int tile, u32x4* sl) {
+__device__ __forceinline__ void dn_stage_quarter(const uint8_t* grp, const uint16_t* sc, int tile, int q, u32x4* sl) {
+    constexpr int B = D / 128;
+    constexpr int RB = 3 * D / 2;
+    const int lane = lane_id();
+    const uint16_t* srow = uniform_ptr(sc + 2 * B + 2 * tile);
+    lds_load4(srow + (uint32_t)lane * 3 * B, sl + kSlotVecs);
+    const uint8_t* base = uniform_ptr(grp + D + tile * (kDnCols / 2) + q * 32);
+    const uint32_t wo = (uint32_t)(lane >> 1) * RB + (lane & 1) * 16;
+    lds_load16(base + wo, sl);
+    lds_load16(base + wo + 32 * RB, sl + 64);
+}
+
+// Dequantises lane (g, dc)'s part of staged quarter q -- rows 8 g .. 8 g + 7, columns
+// 8 dc .. 8 dc + 7 -- into fp16 (row 2p, row 2p + 1) pairs per column: w[p][c], c < 8. Runs
+// while the unit's h is still on its way.
+__device__ __forceinline__ void dn_dequant_quarter(const u32x4* sl, int q, h2 (&w)[4][8]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const uint32_t* rows = reinterpret_cast<const uint32_t*>(sl);
+    const u32x4* sv = sl + kSlotVecs + 2 * g;   // rows 8 g .. 8 g + 7: both scales each
+    const u32x4 s0 = sv[0], s1 = sv[1];
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    // the (row 2p, row 2p + 1) scales of the quarter's block: low or high halves
+    const uint32_t pick = (q >> 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t wa = rows[(8 * g + 2 * p) * 8 + dc], wb = rows[(8 * g + 2 * p + 1) * 8 + dc];
+        const h2 sab = as_h2(__builtin_amdgcn_perm(sw[2 * p + 1], sw[2 * p], pick));
+        dequant8(__builtin_amdgcn_perm(wb, wa, 0x05040100u), sab, &w[p][0]);   // columns 0..3
+        dequant8(__builtin_amdgcn_perm(wb, wa, 0x07060302u), sab, &w[p][4]);   // columns 4..7
+    }
+}
+
+// The quarter's dot products with h of rows 8 g .. 8 g + 7 (hs: the wave's 64 h as fp16):
+// acc[c] is column 8 dc + c over the lane's 8 rows.
+__device__ __forceinline__ void dn_dot_quarter(const h2 (&w)[4][8], const uint16_t* hs, float (&acc)[8]) {
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * (lane_id() >> 3));
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = dot2(w[p][c], as_h2(hw[p]), acc[c]);
+    }
+}
+
+// Down tile: columns 256 tile .. 256 tile + 255 of the unit's 64 rows (8 KB). Lane
+// 8 g + dc's piece j is row 8 g + j, columns 32 dc .. 32 dc + 31, at slot[j 64 + l]; word l
+// of the scale block holds row l's two scales of the tile.
+template <int D>
+__device__ __forceinline__ void dn_stage_tile(const uint8_t* grp, const uint16_t* sc, int tile, u32x4* sl) {
     constexpr int B = D / 128;
     constexpr int RB = 3 * D / 2;
     const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
@@ -1133,6 +1224,57 @@ __device__ __forceinline__ void dn_stage(const uint8_t* grp, const uint16_t* sc,
     const uint32_t wo = (uint32_t)(8 * g) * RB + dc * 16;
 #pragma unroll
     for (int j = 0; j < 8; ++j) lds_load16(base + wo + j * RB, sl + j * 64);
+}
+
+// Dequantisation and dot products of a staged tile in one pass, once h is in (lane (g, dc):
+// rows 8 g .. 8 g + 7, columns 32 dc + c; acc[c] over the lane's 8 rows).
+__device__ __forceinline__ void dn_accumulate_tile(const u32x4* sl, const uint16_t* hs, float (&acc)[32]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const u32x4* sv = sl + kSlotVecs + 2 * g;
+    const u32x4 s0 = sv[0], s1 = sv[1];
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t pick = (dc >> 2) ? 0x07060302u : 0x05040100u;
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+    for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const u32x4 va = sl[(2 * p) * 64 + lane], vb = sl[(2 * p + 1) * 64 + lane];
+        const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
+        const h2 sab = as_h2(__builtin_amdgcn_perm(sw[2 * p + 1], sw[2 * p], pick));
+        const h2 hab = as_h2(hw[p]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h2 w[4];
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
+        }
+    }
+}
+
+// Sum of a quarter's column partials over the wave's 8 row groups through LDS, in
+// dn_reduce's tree ((0 + 4) + (2 + 6)) + ((1 + 5) + (3 + 7)), so that quarters and tiles
+// give the same bits. Lane (g, dc) stores its columns 8 dc + c at red[g][12 dc + c] (a
+// 12-float stride keeps the 8 lanes of a 16-byte store on distinct banks); lane l returns
+// column l. red: 768 floats of the wave's slot.
+__device__ __forceinline__ float dn_sum_groups_quarter(const float (&acc)[8], float* red) {
+    constexpr int RS = 8 * 12;
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    float4* dst = reinterpret_cast<float4*>(red + g * RS + 12 * dc);
+    dst[0] = float4{acc[0], acc[1], acc[2], acc[3]};
+    dst[1] = float4{acc[4], acc[5], acc[6], acc[7]};
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its loads
+    const float* src = red + 12 * (lane >> 3) + (lane & 7);
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = src[j * RS];
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return ((r[0] + r[4]) + (r[2] + r[6])) + ((r[1] + r[5]) + (r[3] + r[7]));
 }
 
 // gu_dots of a staged item (batch 1): the same arithmetic, pieces and scales from LDS,
@@ -1189,56 +1331,42 @@ __device__ __forceinline__ void gu_dots_staged(const u32x4* sl, const u32x4* xl,
     }
 }
 
-// dn_accumulate of a staged item: row pieces and scales from LDS, h from `h` (row lane).
-__device__ __forceinline__ void dn_accumulate_staged(const u32x4* sl, uint64_t h, uint16_t* hs, uint16_t* ss,
-                                                     float acc[32]) {
-    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
-    const uint32_t s = reinterpret_cast<const uint32_t*>(sl + kSlotVecs)[lane];
-    hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)h));   // exact: h is fp16
-    ss[lane] = (uint16_t)s;
-    ss[kDnRows + lane] = (uint16_t)(s >> 16);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
-    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + kDnRows * (dc >> 2) + 8 * g);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, sw[4] = {sv.x, sv.y, sv.z, sv.w};
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const u32x4 wa = sl[(2 * p) * 64 + lane], wb = sl[(2 * p + 1) * 64 + lane];
-        const h2 hab = as_h2(hw[p]), sab = as_h2(sw[p]);
-        const uint32_t xa[4] = {wa.x, wa.y, wa.z, wa.w}, xb[4] = {wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            h2 w[4];
-            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);   // columns 8q + 0..3
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
-            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);   // columns 8q + 4..7
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
-        }
-    }
-}
-
 // The first descriptor batch of the resident range, fetched at the worker's start.
 struct Prefetched {
     uint32_t word;
     bool valid;
 };
 
+// Down items per unit of a staged range of nu units: 64-column quarters when every item
+// of the range gets a wave of its own (the 4 quarters of a tile on the 4 waves of a
+// workgroup, so the work after h is a quarter of a tile's), whole 256-column tiles
+// otherwise (a wave's items follow one another, and fewer of them finish sooner). The
+// widest staged kernels take tiles only: the quarter path's registers and code cost them
+// more than it saves.
+template <int D>
+constexpr bool kStagedQuarters = D <= 2048;
+
+template <int D>
+__device__ __forceinline__ uint32_t staged_down_items(const WaveRole& r, uint32_t nu) {
+    constexpr uint32_t T = D / kDnCols, ipu = kStagedGroup / GuGeom<D>::NPI;
+    if constexpr (!kStagedQuarters<D>) return T;
+    const uint32_t ng = (nu * ipu + 3u) & ~3u;
+    return ng + 4 * T * nu <= r.nw ? 4 * T : T;
+}
+
 template <int D>
 __device__ __forceinline__ void prefetch_core_descs(const MlpArgs& a, uint32_t* slot, const WaveRole& role,
                                                     Prefetched& p) {
     constexpr uint32_t ipu = kStagedGroup / GuGeom<D>::NPI;
-    constexpr uint32_t T = D / kDnCols;
     p.valid = false;
     p.word = 0;
     if (!a.core_count) return;
-    const ItemList il = make_items(role, a.core_count * ipu, a.core_count * T);
+    const uint32_t TQ = staged_down_items<D>(role, a.core_count);
+    const ItemList il = make_staged_items(role, a.core_count * ipu, a.core_count * TQ);
     if (!il.K) return;
     uint32_t seen = 0;
     // resident units are never waited for: this cannot fail
-    p.valid = fetch_descs(a, slot, 0, seen, il, 0, min(il.K, (uint32_t)kDescItems), ipu, T, 1u, p.word);
+    p.valid = fetch_descs(a, slot, 0, seen, il, 0, min(il.K, (uint32_t)kDescItems), ipu, TQ, 1u, p.word);
 }
 
 // This wave's items of units [u0, u1) through its two LDS slots (stage: kWaves x 2 slots).
@@ -1254,7 +1382,9 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     constexpr uint32_t ipu = G / Gm::NPI;   // gate/up items per unit
     const uint32_t nu = u1 - u0;
     const uint32_t NG = nu * ipu;
-    const ItemList il = make_items(role, NG, nu * T);
+    const uint32_t TQ = staged_down_items<D>(role, nu);   // down items per unit
+    const bool quarters = kStagedQuarters<D> && TQ != T;
+    const ItemList il = make_staged_items(role, NG, nu * TQ);
     const uint32_t K = il.K, KG = il.KG;
     auto leave = [&](bool r) -> bool {
         stage_x<D>(xp, 1u, xl, &sh.xcount);
@@ -1262,7 +1392,7 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     };
     if (!K) return leave(true);
     uint32_t seen = 0, word = first.word, k0 = 0;
-    if (!first.valid && !fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, 1u, word))
+    if (!first.valid && !fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, TQ, 1u, word))
         return leave(false);
     if (a.stamps) {
         asm volatile("" : : "v"(word));   // the stamp waits for the descriptors
@@ -1272,7 +1402,6 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     const int wave = wave_id();
     const int lane = lane_id();
     uint16_t* hs = sh.hs[wave];
-    uint16_t* ss = sh.ss[wave];
     u32x4* const sl0 = stage + (2 * wave) * kSlotStride;
     u32x4* const sl1 = sl0 + kSlotStride;
     ItemMeta m0, m1;
@@ -1282,7 +1411,7 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, 1u, word))
+            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, TQ, 1u, word))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -1299,11 +1428,18 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
             const uint32_t i = il.item(k), rel = i / ipu;
             m.n0 = (int)((i - rel * ipu) * Gm::NPI);
             gu_stage<D>(u.grp, u.sc, m.n0, sl);
-        } else {
-            const uint32_t d = il.item(k) - NG, rel = d / T;
+        } else if (quarters) {
+            // quarter j = 4 (tile of the unit) + q; q is the wave's index in its workgroup
+            const uint32_t j = il.item(k) - NG, rel = j / TQ, jt = j - rel * TQ;
             m.unit = u0 + rel;
-            m.tile = d - rel * T;
-            dn_stage<D>(u.grp, u.sc, (int)m.tile, sl);
+            m.tile = jt >> 2;
+            m.row = jt & 3;   // the quarter
+            dn_stage_quarter<D>(u.grp, u.sc, (int)m.tile, (int)m.row, sl);
+        } else {
+            const uint32_t j = il.item(k) - NG, rel = j / TQ;
+            m.unit = u0 + rel;
+            m.tile = j - rel * TQ;
+            dn_stage_tile<D>(u.grp, u.sc, (int)m.tile, sl);
         }
         return true;
     };
@@ -1330,26 +1466,40 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
             U = a.core_count + ep.total;
             have_u = true;
         }
+        // the first look at h goes out first (a quarter is dequantised while it travels)
         DnItem it;
         it.h = ld_agent_u64(uniform_ptr(m.hrow) + lane);
-        if (!dn_wait_h(a, slot, m.hrow, (int)G, 0, it)) return false;
-        if (k == KG) stamp(a, kStampHReady);
-        float acc[32];
+        if (quarters) {
+            h2 w[4][8];
+            dn_dequant_quarter(sl, (int)m.row, w);
+            if (!dn_wait_h(a, slot, m.hrow, (int)G, 0, it)) return false;
+            if (k == KG) stamp(a, kStampHReady);
+            hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS store lands before its loads
+            float acc[8];
+            dn_dot_quarter(w, hs, acc);
+            // through the slot: its pieces are in registers
+            const float col_sum = dn_sum_groups_quarter(acc, reinterpret_cast<float*>(sl));
+            add_column(a, slot, yacc, (int)(m.tile * kDnCols + m.row * 64) + lane, col_sum, U, pd);
+        } else {
+            if (!dn_wait_h(a, slot, m.hrow, (int)G, 0, it)) return false;
+            if (k == KG) stamp(a, kStampHReady);
+            hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            float acc[32], cs[4];
+            dn_accumulate_tile(sl, hs, acc);
+            dn_reduce(acc, cs);
+            // re-deal through the slot (its pieces are in registers by now): lane (g, dc)
+            // holds tile columns 32 dc + 4 g + i; lane l adds dn_tile_column(l) + kTileColOff[i]
+            float* red = reinterpret_cast<float*>(sl);
+            *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
-        for (int c = 0; c < 32; ++c) acc[c] = 0.f;
-        dn_accumulate_staged(sl, it.h, hs, ss, acc);
-        float cs[4];
-        dn_reduce(acc, cs);
-        // re-deal through the slot just consumed (its pieces are in registers by now):
-        // lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds columns l + 64 i
-        float* red = reinterpret_cast<float*>(sl);
-        *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cs[i] = red[lane + 64 * i];
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + lane, cs, U, pd);
-        if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
+            for (int i = 0; i < 4; ++i) cs[i] = red[dn_tile_column(lane) + kTileColOff[i]];
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            add_columns(a, slot, yacc, (int)(m.tile * kDnCols) + dn_tile_column(lane), cs, U, pd);
+        }
+        if (a.executions) count_execution(a, slot, m.unit, m.dest, TQ);
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
     };
@@ -1360,7 +1510,8 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
         auto next = [&]() -> bool { return k + 1 >= K || issue(k + 1, nsl, nm); };
         // a down item after the wave's last gate/up item waits until that item is computed:
         // its bytes are not needed before h, and issued earlier they compete with the
-        // gate/up bytes still streaming, which h waits for
+        // gate/up bytes still streaming, which h waits for (measured: all bytes requested
+        // at the start make the layer slower)
         if (k + 1 == KG) return compute_gu(k, sl, m, [] { return true; }) && next();
         if (k < KG) return compute_gu(k, sl, m, next);
         wait_loads_but<0>();
@@ -1562,6 +1713,7 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
+    pd.n = 0;
     const uint32_t early = (QUEUE || FUSED) && lane_id() == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
     if (threadIdx.x == 0) sh.xcount = 0;   // waves count themselves in once their part of x is staged
     __syncthreads();
