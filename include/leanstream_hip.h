@@ -94,6 +94,23 @@ int ls_hip_last_candidate(void* backend);
 uint32_t ls_hip_max_workers(void* backend);
 uint32_t ls_quantize_io_load(uint32_t remaining, uint32_t total, uint32_t buckets);
 
+/* ---- allocation-free resident layer ----
+ * No counterpart in LeanStream. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): one layer whose
+ * groups are all resident (the core descriptors; no ready queue), computed as ls_hip_enqueue
+ * computes it (fused persistent kernel, same bits) with its synchronisation words,
+ * accumulators and h rows in a per-GPU device array of the library (about 1.9 MB, held until
+ * the process ends) instead of the buffers ls_hip_bind allocates. Calls no hipMalloc/hipFree.
+ * Stream-ordered: output (fp16 [batch][width]), output32 (optional fp32) and status (optional
+ * device-visible word, cleared by the call, LS_STATUS_* bits) are valid once the stream
+ * reaches the end of the call. Calls that overlap on one GPU race on the shared array.
+ * Limits: width <= 8192 (a multiple of 256 with kernels built for it), batch 1..4 (ENOTSUP
+ * above), core_count <= 1024 and core_count * group_size <= 32768 (ENOSPC beyond). */
+int ls_hip_core_layer_noalloc(uint32_t width, uint32_t group_size, uint32_t batch, const void* cache,
+                              uint32_t cache_groups, const void* scales, uint32_t scale_groups, const ls_exec_desc* core,
+                              uint32_t core_count, const void* input, void* output, float* output32, uint32_t* status,
+                              void* stream);
+
 /* ---- coherent host memory (fine-grained, GPU-visible at system scope) ---- */
 void* ls_hip_host_alloc(uint64_t bytes);
 void ls_hip_host_free(void* ptr);

@@ -76,6 +76,7 @@ _SIGNATURES = [
     ("ls_hip_last_candidate", [p], C.c_int),
     ("ls_hip_max_workers", [p], u32),
     ("ls_quantize_io_load", [u32, u32, u32], u32),
+    ("ls_hip_core_layer_noalloc", [u32, u32, u32, p, u32, p, u32, p, u32, p, p, p, p, p], C.c_int),
     ("ls_hip_host_alloc", [u64], p),
     ("ls_hip_host_free", [p], None),
     ("ls_hip_release_u32", [p, C.c_int64, u32], None),
