@@ -184,12 +184,18 @@ void ls_stream_destroy(void* decoder);
 int ls_stream_queue(void* decoder, ls_device_queue* out);
 /* Runs `count` layers in order on `stream` (Runtime layer id = (first_layer + i) % layers).
  * times: optional [count][7] ns after the call's start: begin, after begin_layer, after
- * update_prediction, after enqueue_compute, after finalize, completion observed, after
- * commit. stamps: optional [count][group_count][3] ns after each layer's begin: admission,
+ * update_prediction, after enqueue_compute, after finalize, completion observed (left 0
+ * when the launch's completion was not observed), after commit. stamps: optional [count][group_count][3] ns after each layer's begin: admission,
  * copy submission, copy completion. Stops at the first failing layer and returns its code
  * (ETIMEDOUT when the kernel does not complete within timeout_ms). */
 int ls_stream_run(void* decoder, const ls_stream_layer* layers, uint32_t count, uint32_t first_layer, void* stream,
                   uint64_t* times, uint64_t* stamps, int32_t timeout_ms);
+/* Failure injection of the transport (the role of LeanStream's STREAM_TESTING read hook,
+ * src/io/stream_io.h): from now on every copy of logical group `group` into the staging
+ * arena is refused with `error` (a positive errno) at submission, as a failed read would
+ * be; error 0 clears it. The layer then fails with that code through the queue's error
+ * word, as a real transport error does. */
+int ls_stream_inject_copy_error(void* decoder, uint32_t group, int32_t error);
 
 /* ---- synthetic workload generation on the device (counter-based splitmix64) ---- */
 int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream);

@@ -98,6 +98,7 @@ _SIGNATURES = [
     ("ls_stream_destroy", [p], None),
     ("ls_stream_queue", [p, p], C.c_int),
     ("ls_stream_run", [p, p, u32, u32, p, p, p, i32], C.c_int),
+    ("ls_stream_inject_copy_error", [p, u32, i32], C.c_int),
     ("ls_synth_bytes", [p, u64, u64, p], C.c_int),
     ("ls_synth_uniform_f16", [p, u64, u64, C.c_double, C.c_double, p], C.c_int),
     ("ls_synth_normal_f16", [p, u64, u64, p], C.c_int),

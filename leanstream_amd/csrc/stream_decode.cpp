@@ -11,6 +11,7 @@
 // the previous layer retired, which is after its kernel finished, so the shared
 // staging arena never holds bytes a running kernel still reads.
 #include <hip/hip_runtime_api.h>
+#include <atomic>
 #include <cerrno>
 #include <chrono>
 #include <cstring>
@@ -57,6 +58,26 @@ struct StreamDecoder {
     std::unique_ptr<HipCopyEngine> copies;
     std::unique_ptr<HostStagingIO> io;
     std::unique_ptr<Runtime> runtime;
+    // the transport's engine, behind a filter that can refuse one group's copies
+    CopyEngine engine{};
+    std::atomic<uint32_t> fail_group{UINT32_MAX};
+    std::atomic<int> fail_error{0};
+
+    static int filtered_submit(void* ctx, uint32_t lane, void* dst, const void* src, uint64_t bytes) {
+        auto& d = *static_cast<StreamDecoder*>(ctx);
+        const int error = d.fail_error.load(std::memory_order_acquire);
+        if (error) {
+            const uint64_t g = d.fail_group.load(std::memory_order_relaxed);
+            const uint8_t* first = static_cast<const uint8_t*>(d.setup.staging) + g * d.setup.staging_stride;
+            if (static_cast<const uint8_t*>(dst) >= first && static_cast<const uint8_t*>(dst) < first + d.setup.staging_stride)
+                return error;
+        }
+        return d.engine.submit(d.engine.context, lane, dst, src, bytes);
+    }
+    static int filtered_poll(void* ctx, uint32_t lane) {
+        auto& d = *static_cast<StreamDecoder*>(ctx);
+        return d.engine.poll(d.engine.context, lane);
+    }
 
     ~StreamDecoder() {
         runtime.reset();  // drains every layer
@@ -82,11 +103,14 @@ struct StreamDecoder {
         StagingConfig sc;
         if (s.copy_engine == LS_COPY_SDMA) {
             sdma.reset(new SdmaCopyEngine(s.device, s.qd, s.copy_queues, s.copy_chunk));
-            sc.engine = sdma->view();
+            engine = sdma->view();
         } else {
             copies.reset(new HipCopyEngine(s.device, s.qd, s.copy_queues));
-            sc.engine = copies->view();
+            engine = copies->view();
         }
+        sc.engine.context = this;
+        sc.engine.submit = filtered_submit;
+        sc.engine.poll = filtered_poll;
         sc.group_count = n;
         sc.qd = s.qd;
         sc.group_bytes = s.group_bytes;
@@ -145,7 +169,7 @@ struct StreamDecoder {
         bool done = false;
         while (!(done = cb.complete(cb.context, id)) && now_ns() < deadline) {
         }
-        mark(5);
+        if (done) mark(5);
         if (!rc && !done) rc = ETIMEDOUT;
         // A launch whose device status is set (a bounded wait expired, a descriptor or the
         // queue was rejected, a value was out of range) produced no valid output and may
@@ -202,6 +226,16 @@ int ls_stream_queue(void* h, ls_device_queue* out) {
     out->ready_indices = q.ready_indices;
     out->control = q.control;
     out->capacity = q.capacity;
+    return 0;
+}
+
+int ls_stream_inject_copy_error(void* h, uint32_t group, int32_t error) {
+    if (!h || error < 0) return EINVAL;
+    auto& d = *static_cast<StreamDecoder*>(h);
+    if (error && group >= d.setup.group_count) return EINVAL;
+    d.fail_error.store(0, std::memory_order_release);
+    d.fail_group.store(group, std::memory_order_relaxed);
+    d.fail_error.store(error, std::memory_order_release);
     return 0;
 }
 

@@ -106,6 +106,12 @@ class StreamingDecode:
     def run(self, first=0, count=None, timeout_ms=10000):
         """Run layers [first, first + count); returns (times [count, 7] ns from the call's
         start, stamps [count, groups, 3] ns from each layer's begin)."""
+        rc, times, stamps = self.try_run(first, count, timeout_ms)
+        _check(rc, "ls_stream_run")
+        return times, stamps
+
+    def try_run(self, first=0, count=None, timeout_ms=10000):
+        """As run, returning (return code, times, stamps) instead of raising."""
         count = self.layers - first if count is None else count
         n = self.cfg.groups
         times = np.zeros((count, 7), dtype=np.uint64)
@@ -114,8 +120,19 @@ class StreamingDecode:
         entries = C.cast(C.byref(self.entries, first * C.sizeof(StreamLayer)), C.c_void_p)
         rc = self.lib.ls_stream_run(self.handle, entries, count, first, stream, times.ctypes.data, stamps.ctypes.data,
                                     timeout_ms)
-        _check(rc, "ls_stream_run")
-        return times, stamps
+        return rc, times, stamps
+
+    def inject_copy_error(self, group, error):
+        """Refuse every copy of logical group `group` with `error` (0 clears)."""
+        _check(self.lib.ls_stream_inject_copy_error(self.handle, group, error), "ls_stream_inject_copy_error")
+
+    def set_final(self, layer, ids):
+        """Replace layer `layer`'s final list (finalize argument) with `ids`."""
+        self._finals = getattr(self, "_finals", {})
+        arr = np.ascontiguousarray(ids, dtype=np.int32)
+        self._finals[layer] = arr
+        self.entries[layer].final_ids = arr.ctypes.data
+        self.entries[layer].final_count = len(arr)
 
     def queue(self):
         """(descriptors [capacity, 5], ready_indices [capacity], control words [32]) as numpy copies."""

@@ -148,6 +148,7 @@ def test_stream_create_rejects_invalid_setup():
     s = _native.StreamSetup(1, 1, 1, 1, 1, 1, 1, 8, 1, 8, 2, 1, 0, 1, 0)    # unknown copy engine
     assert not lib.ls_stream_create(C.byref(s))
     assert lib.ls_stream_run(None, None, 0, 0, None, None, None, 1000) != 0
+    assert lib.ls_stream_inject_copy_error(None, 0, 5) == 22
 
 
 # ---------------------------------------------------------------------------- argument errors
