@@ -159,6 +159,17 @@ struct StreamDecoder {
         if (rc) return rc;
         rc = step.update_prediction({L.rank, L.rank_count});
         mark(2);
+        // The selector's io bucket: this loop's own snapshot of the ranked groups not yet
+        // READY when the layer is submitted (docs/kernel_selection.md: an application-owned
+        // remaining/total snapshot), quantized as the offline table was measured.
+        uint32_t remaining = 0;
+        for (uint32_t i = 0; i < L.rank_count; ++i) {
+            const int32_t g = L.rank[i];
+            if (g >= 0 && static_cast<uint32_t>(g) < n &&
+                __atomic_load_n(io_states + g, __ATOMIC_ACQUIRE) != kIoReady)
+                ++remaining;
+        }
+        backend->state.io_bucket = quantize_io_load(remaining, L.rank_count);
         if (!rc) rc = step.enqueue_compute(L.input, L.output, stream);
         mark(3);
         if (!rc) rc = step.finalize({L.final_ids, L.final_count});
