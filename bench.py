@@ -42,7 +42,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 400 layers; 20 decode steps for c3)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 50 layers; 2 decode steps for c3)")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c4b4", "c5", "c1d32", "c3"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c4b4", "c5", "c1d32", "c3", "g2"],
                     help="c3: 36-layer streaming decode step staged from pinned host memory")
     ap.add_argument("--candidate", type=int, default=None, help="force a kernel candidate id (offline LUT of one entry)")
     ap.add_argument("--copies", type=int, default=0, help="layer copies to rotate over (0: enough to exceed 256 MB)")

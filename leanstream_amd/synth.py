@@ -158,6 +158,10 @@ CONFIGS = {
     # dense batched fallback: every group active, batch 32, bf16 x (matrix-core path)
     "c5": LayerConfig("dense_int4_mlp_d4096_f14336_g64_b32", 4096, 14336, 1.0, batch=32, selection="all",
                       x_dtype="bf16", seed=0xC5),
+    # Ministral-3 8B production geometry: Group2 bundles (2-neuron groups, 7168 groups), 1434
+    # active (20%), as LeanStream's Ministral packer lays them out
+    "g2": LayerConfig("ministral3_8b_group2_sparse_int4_mlp_d4096_f14336_a20_b1", 4096, 14336, 0.20, group_size=2,
+                      seed=0x62),
     # the same path at the d_model 1024 shape, 16 of 64 groups (quick parity case)
     "c1d32": LayerConfig("sparse_int4_mlp_d1024_f4096_g64_a25_b32", 1024, 4096, 0.25, batch=32,
                          selection="permutation", x_dtype="bf16", seed=0xC1),
