@@ -68,6 +68,23 @@ struct HipLayerBuffers {
     uint64_t* stamps = nullptr;         // optional per-worker phase stamps [max workers][32]
 };
 
+// Optional layer epilogue, run after every enqueue on the same stream (no LeanStream
+// C++ counterpart; the Triton reduction's PUBLISH path, backends/triton/reduction.py:17-28,
+// and the Ministral RMSNorm, examples/ministral/native/predictor_shared_input.cu:16-41):
+// hidden = fp16(fp32 residual + fp32 y) per row, then optionally RMSNorm(hidden) * weight,
+// then the flags (system-scope release stores of the enqueue's epoch) and the bell.
+// Device pointers, [batch][width] rows; the flags may be host-coherent words.
+struct HipEpilogue {
+    const void* residual = nullptr;     // fp16 [batch][width]
+    void* hidden = nullptr;             // fp16 [batch][width]
+    uint32_t* hidden_flag = nullptr;    // optional: epoch once every row of hidden is written
+    const void* norm_weight = nullptr;  // optional fp16 [width]
+    void* norm_output = nullptr;        // fp16 [batch][width], with norm_weight
+    uint32_t* norm_flag = nullptr;      // optional (with norm_weight): epoch once norm_output is written
+    uint32_t* bell = nullptr;           // optional: += 1 after the flags
+    float norm_eps = 0.f;               // 0 .. 1
+};
+
 class HipBackend {
 public:
     explicit HipBackend(KernelDecisionTable table = {});
@@ -80,6 +97,8 @@ public:
     int enqueue(KernelRuntimeState, const void* input, void* output, void* stream, Span<ExecDesc> core,
                 DeviceExecQueue, uint32_t epoch, ConsumerMode);
     ComputeBackend view();
+    // Installs (or, with nullptr, removes) the epilogue of every later enqueue; after bind.
+    int set_epilogue(const HipEpilogue*);
 
     // Latest caller-supplied selector state (layer is overwritten per enqueue).
     KernelRuntimeState state{};

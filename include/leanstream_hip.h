@@ -84,6 +84,25 @@ int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t ou
 uint32_t ls_hip_status(void* backend);
 void ls_hip_clear_status(void* backend);
 void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
+/* Identical to leanstream::runtime::HipEpilogue (include/leanstream/hip_backend.h): the layer
+ * epilogue run after every later enqueue on the same stream -- hidden = fp16(residual + y)
+ * (the Triton reduction's PUBLISH path, backends/triton/reduction.py:17-28), optionally
+ * RMSNorm(hidden) * norm_weight (examples/ministral/native/predictor_shared_input.cu:16-41),
+ * then hidden_flag / norm_flag receive the enqueue's epoch (system-scope release) and
+ * bell += 1. The completion word of the layer does not cover the epilogue: readers of
+ * hidden wait on the flags. NULL removes it. EINVAL for an unbound backend or an
+ * inconsistent block. */
+typedef struct ls_hip_epilogue {
+    const void* residual;
+    void* hidden;
+    uint32_t* hidden_flag;
+    const void* norm_weight;
+    void* norm_output;
+    uint32_t* norm_flag;
+    uint32_t* bell;
+    float norm_eps;
+} ls_hip_epilogue;
+int ls_hip_set_epilogue(void* backend, const ls_hip_epilogue* epilogue);
 /* Down-projection items (256-column tiles) per unit: d / 256. */
 uint32_t ls_hip_slices(void* backend);
 /* Overrides the selected candidate's persistent worker count (0 = the candidate's own

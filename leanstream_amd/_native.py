@@ -37,6 +37,13 @@ class LayerBuffers(C.Structure):
                 ("executions", p), ("first_compute", p), ("claim_log", p), ("stamps", p)]
 
 
+class Epilogue(C.Structure):
+    """ls_hip_epilogue / HipEpilogue (include/leanstream/hip_backend.h)."""
+
+    _fields_ = [("residual", p), ("hidden", p), ("hidden_flag", p), ("norm_weight", p), ("norm_output", p),
+                ("norm_flag", p), ("bell", p), ("norm_eps", C.c_float)]
+
+
 class GroupLayout(C.Structure):
     """GroupLayout (include/leanstream/group_layout.h); file_offset = offset in the host store."""
 
@@ -70,6 +77,7 @@ _SIGNATURES = [
     ("ls_hip_status", [p], u32),
     ("ls_hip_clear_status", [p], None),
     ("ls_hip_set_spin_limit", [p, u64], None),
+    ("ls_hip_set_epilogue", [p, p], C.c_int),
     ("ls_hip_slices", [p], u32),
     ("ls_hip_set_workers", [p, u32], None),
     ("ls_hip_select", [p, u32, u32], u32),

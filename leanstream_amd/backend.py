@@ -9,7 +9,7 @@ import ctypes as C
 import numpy as np
 
 from . import _native
-from ._native import DeviceQueue, ExecDesc, LayerBuffers
+from ._native import DeviceQueue, Epilogue, ExecDesc, LayerBuffers
 
 MODE_BATCH_COMPAT, MODE_PROGRESSIVE, MODE_AUTO = 0, 1, 2
 STATUS_TIMEOUT, STATUS_QUEUE_ERROR, STATUS_BAD_DESCRIPTOR, STATUS_RANGE, STATUS_QUEUE_UNCONSUMED = 1, 2, 4, 8, 16
@@ -165,6 +165,19 @@ class NativeBackend:
         if rc:
             raise RuntimeError(f"Native bind failed: {rc}")
         self._bound = (b, cache, scales, staging, hidden, partial, y32, executions, first_compute, claim_log, stamps)
+
+    def set_epilogue(self, residual, hidden, hidden_flag=None, norm_weight=None, norm_output=None, norm_flag=None,
+                     bell=None, eps=0.0):
+        """Install the layer epilogue (ls_hip_set_epilogue); every argument None removes it."""
+        if residual is None and hidden is None:
+            rc = self.lib.ls_hip_set_epilogue(self.context, None)
+        else:
+            e = Epilogue(_ptr(residual), _ptr(hidden), _ptr(hidden_flag), _ptr(norm_weight), _ptr(norm_output),
+                         _ptr(norm_flag), _ptr(bell), float(eps))
+            rc = self.lib.ls_hip_set_epilogue(self.context, C.byref(e))
+            self._epilogue = (e, residual, hidden, hidden_flag, norm_weight, norm_output, norm_flag, bell)
+        if rc:
+            raise RuntimeError(f"Native set_epilogue failed: {rc}")
 
     def enqueue(self, layer, io_bucket, epoch, x, y, stream, core, core_count, queue, mode=MODE_PROGRESSIVE):
         rc = self.lib.ls_hip_enqueue(self.context, layer, io_bucket, epoch, _ptr(x), _ptr(y), stream, _ptr(core),

@@ -101,6 +101,11 @@ void ls_hip_clear_status(void* p) {
 void ls_hip_set_spin_limit(void* p, uint64_t ticks) {
     if (p) backend(p)->set_spin_limit_ticks(ticks);
 }
+int ls_hip_set_epilogue(void* p, const ls_hip_epilogue* e) {
+    static_assert(sizeof(ls_hip_epilogue) == sizeof(HipEpilogue), "epilogue block");
+    if (!p) return EINVAL;
+    return backend(p)->set_epilogue(reinterpret_cast<const HipEpilogue*>(e));
+}
 uint32_t ls_hip_slices(void* p) { return p ? backend(p)->slices() : 0; }
 void ls_hip_set_workers(void* p, uint32_t workers) {
     if (p) backend(p)->set_workers(workers);

@@ -26,6 +26,9 @@ struct HipBackend::Impl {
     uint16_t* x16 = nullptr;     // dense path: x converted to paired fp16
     bool dense = false;          // batch > kMaxBatch: every launch takes the matrix-core path
     uint32_t* done = nullptr;    // host-coherent: sequence of the last finished launch
+    uint32_t* arrivals = nullptr;  // epilogue row workgroups that finished (zero between launches)
+    HipEpilogue epilogue{};
+    bool has_epilogue = false;
     uint32_t last_seq = 0;       // sequence of the last enqueued launch (0: none)
     bool needs_clear = true;
     uint32_t seq = 0;
@@ -42,6 +45,9 @@ struct HipBackend::Impl {
         if (x16) (void)hipFree(x16);
         if (status) (void)hipHostFree(status);
         if (done) (void)hipHostFree(done);
+        if (arrivals) (void)hipFree(arrivals);
+        arrivals = nullptr;
+        has_epilogue = false;
         sync = nullptr;
         qmirror = nullptr;
         yacc = nullptr;
@@ -91,6 +97,8 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess && dense) e = hipMemset(p.h16, 0, sizeof(uint16_t) * 32 * b.slot_capacity * b.group_size);
     if (e == hipSuccess)
         e = hipHostMalloc(reinterpret_cast<void**>(&p.done), 64, hipHostMallocCoherent | hipHostMallocMapped);
+    if (e == hipSuccess) e = hipMalloc(&p.arrivals, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(p.arrivals, 0, sizeof(uint32_t));
     int dev = 0;
     if (e == hipSuccess) e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&p.cus, hipDeviceAttributeMultiprocessorCount, dev);
@@ -200,6 +208,40 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
         return static_cast<int>(e);
     }
     p.last_seq = a.seq;
+    if (p.has_epilogue) {
+        const HipEpilogue& ep = p.epilogue;
+        lsamd::EpilogueArgs x{};
+        x.y = a.y;
+        x.residual = static_cast<const uint16_t*>(ep.residual);
+        x.hidden = static_cast<uint16_t*>(ep.hidden);
+        x.hidden_flag = ep.hidden_flag;
+        x.norm_weight = static_cast<const uint16_t*>(ep.norm_weight);
+        x.norm_out = static_cast<uint16_t*>(ep.norm_output);
+        x.norm_flag = ep.norm_flag;
+        x.bell = ep.bell;
+        x.arrivals = p.arrivals;
+        x.eps = ep.norm_eps;
+        x.width = p.buf.width;
+        x.rows = p.buf.batch;
+        x.epoch = epoch;
+        e = lsamd::launch_epilogue(x, hs);
+        if (e != hipSuccess) return static_cast<int>(e);
+    }
+    return 0;
+}
+
+int HipBackend::set_epilogue(const HipEpilogue* ep) {
+    Impl& p = *impl_;
+    if (!p.bound) return EINVAL;
+    if (!ep) {
+        p.has_epilogue = false;
+        return 0;
+    }
+    if (!ep->residual || !ep->hidden || (ep->norm_weight && !ep->norm_output) || (!ep->norm_weight && ep->norm_output) ||
+        (ep->norm_flag && !ep->norm_weight) || !(ep->norm_eps >= 0.f) || ep->norm_eps > 1.f)
+        return EINVAL;
+    p.epilogue = *ep;
+    p.has_epilogue = true;
     return 0;
 }
 

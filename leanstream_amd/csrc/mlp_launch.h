@@ -22,6 +22,22 @@ hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStr
 // Dense batched path (batch > kMaxBatch, core units only): gate/up -> down -> reduction.
 hipError_t launch_dense(const MlpArgs&, const Bounds&, hipStream_t);
 bool dense_available(int width);   // widths the dense (batch > kMaxBatch) path is compiled for
+// Layer epilogue (after the layer's launch, same stream): the next hidden state
+// fp16(residual + y) per row, optionally its RMSNorm, then the flags.
+struct EpilogueArgs {
+    const uint16_t* y;            // fp16 [rows][width]: the layer output
+    const uint16_t* residual;     // fp16 [rows][width]
+    uint16_t* hidden;             // fp16 [rows][width]
+    uint32_t* hidden_flag;        // optional: epoch, system release, once every row is written
+    const uint16_t* norm_weight;  // optional fp16 [width]
+    uint16_t* norm_out;           // fp16 [rows][width] (with norm_weight)
+    uint32_t* norm_flag;          // optional: epoch, after hidden_flag
+    uint32_t* bell;               // optional: +1 after the flags
+    uint32_t* arrivals;           // device word, zero between launches (the last row block resets it)
+    float eps;
+    uint32_t width, rows, epoch;
+};
+hipError_t launch_epilogue(const EpilogueArgs&, hipStream_t);
 // Zeroes both ring slots, both accumulator buffers and the tagged h rows.
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
                       uint32_t hwords, hipStream_t);

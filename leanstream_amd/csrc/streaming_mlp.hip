@@ -2490,6 +2490,79 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
                            dim3(kThreads), rargs, 0, stream);
 }
 
+// ---------------------------------------------------------------------------------
+// Epilogue: next-hidden publication (LeanStream backends/triton/reduction.py:17-28 with
+// PUBLISH) and RMSNorm (examples/ministral/native/predictor_shared_input.cu:16-41), one
+// workgroup per row after the layer's launch on the same stream, so every y word of the
+// launch is visible to it. hidden = fp16(fp32 residual + fp32 y); RMSNorm: thread t sums
+// hidden^2 over columns t, t + 256, ... in order, a halving tree over the 256 partial sums,
+// inverse = 1 / sqrt(sum / width + eps) (IEEE square root and division), out =
+// fp16(weight * fp16(hidden * inverse)). Products and sums are not contracted into fused
+// multiply-adds, so the result is the oracle's bit for bit. The last row's workgroup to
+// finish publishes the flags with system-scope release stores: hidden_flag, then
+// norm_flag, then bell += 1.
+// ---------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
+#pragma clang fp contract(off)
+    __shared__ float lanes[256];
+    __shared__ uint32_t last;
+    const uint32_t t = threadIdx.x, row = blockIdx.x;
+    const uint16_t* y = e.y + (size_t)row * e.width;
+    const uint16_t* res = e.residual + (size_t)row * e.width;
+    uint16_t* hid = e.hidden + (size_t)row * e.width;
+    float sum = 0.f;
+    for (uint32_t i = t; i < e.width; i += 256) {
+        const float a = (float)__builtin_bit_cast(_Float16, res[i]);
+        const float b = (float)__builtin_bit_cast(_Float16, y[i]);
+        float ab = a + b;
+        asm volatile("" : "+v"(ab));   // an fp32 sum rounded to fp16 (no mixed-precision fused form)
+        const _Float16 h = (_Float16)ab;
+        hid[i] = __builtin_bit_cast(uint16_t, h);
+        const float v = (float)h;
+        const float sq = v * v;
+        sum = sum + sq;
+    }
+    if (e.norm_weight) {
+        lanes[t] = sum;
+        __syncthreads();
+        for (uint32_t stride = 128; stride; stride >>= 1) {
+            if (t < stride) lanes[t] = lanes[t] + lanes[t + stride];
+            __syncthreads();
+        }
+        const float inverse = 1.0f / __builtin_sqrtf(lanes[0] / (float)e.width + e.eps);
+        uint16_t* out = e.norm_out + (size_t)row * e.width;
+        for (uint32_t i = t; i < e.width; i += 256) {
+            float p = (float)__builtin_bit_cast(_Float16, hid[i]) * inverse;
+            asm volatile("" : "+v"(p));   // the fp32 product, then fp16 (as the reference rounds)
+            const float n = (float)(_Float16)p;
+            const float w = (float)__builtin_bit_cast(_Float16, e.norm_weight[i]);
+            out[i] = __builtin_bit_cast(uint16_t, (_Float16)(w * n));   // the exact product, rounded once
+        }
+    }
+    if (!e.hidden_flag && !e.norm_flag && !e.bell) return;
+    // this workgroup's stores are visible at system scope before it counts itself in
+    __atomic_thread_fence(__ATOMIC_RELEASE);
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t before = __hip_atomic_fetch_add(e.arrivals, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_SYSTEM);
+        last = before == e.rows - 1;
+        if (last) {
+            __hip_atomic_store(e.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (e.hidden_flag) __hip_atomic_store(e.hidden_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (e.norm_flag) __hip_atomic_store(e.norm_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (e.bell) (void)__hip_atomic_fetch_add(e.bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+    }
+}
+
+hipError_t launch_epilogue(const EpilogueArgs& args, hipStream_t stream) {
+    EpilogueArgs e = args;
+    if (!e.y || !e.residual || !e.hidden || !e.rows || !e.width || (e.norm_weight && !e.norm_out) || !e.arrivals)
+        return hipErrorInvalidValue;
+    void* kargs[] = {&e};
+    return hipLaunchKernel(reinterpret_cast<const void*>(&epilogue_kernel), dim3(e.rows), dim3(256), kargs, 0, stream);
+}
+
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
                       uint32_t hwords, hipStream_t stream) {
     const uint32_t most = words > hwords ? words : hwords;

@@ -39,6 +39,8 @@ def lib():
             ("ora_layer", [p, C.c_uint32, C.c_uint32, p, p, p, p, C.c_uint32, C.c_uint32, C.c_int, p, p, p, p],
              C.c_int),
             ("ora_rank", [p, C.c_uint32, C.c_uint32, p], C.c_int),
+            ("ora_publish_hidden", [p, p, C.c_uint32, p], None),
+            ("ora_rmsnorm", [p, p, C.c_float, C.c_uint32, p], C.c_int),
         ]:
             f = getattr(l, name)
             f.argtypes = args
@@ -97,3 +99,23 @@ def rank(scores, k):
     if rc:
         raise ValueError(f"oracle rank failed: {rc}")
     return out[:k].astype(np.int64)
+
+
+def publish_hidden(residual, y16):
+    """fp16(fp32 residual + fp32 y) per element (the next layer's hidden state)."""
+    r = np.ascontiguousarray(residual, dtype=np.float16).view(np.uint16)
+    y = np.ascontiguousarray(y16, dtype=np.float16).view(np.uint16)
+    out = np.zeros(r.size, dtype=np.uint16)
+    lib().ora_publish_hidden(_addr(r), _addr(y), r.size, _addr(out))
+    return out.view(np.float16)
+
+
+def rmsnorm(x, weight, eps):
+    """RMSNorm of one fp16 row with an fp16 weight; fp16 out."""
+    xv = np.ascontiguousarray(x, dtype=np.float16).view(np.uint16)
+    w = np.ascontiguousarray(weight, dtype=np.float16).view(np.uint16)
+    out = np.zeros(xv.size, dtype=np.uint16)
+    rc = lib().ora_rmsnorm(_addr(xv), _addr(w), float(eps), xv.size, _addr(out))
+    if rc:
+        raise ValueError("oracle rmsnorm failed")
+    return out.view(np.float16)

@@ -10,6 +10,12 @@
  *                     sum256 tree order :16-20, down-projection accumulation :38-41)
  *   ora_reduce        kernels/streaming_mlp.cu:80-84   (fixed slot-order fp32 sum, fp16 out)
  *   ora_rank          predictor/predictor_cpu.cpp:192-201 (score desc, id asc)
+ *   ora_publish_hidden backends/triton/reduction.py:20-22 (fp16(fp32 residual + fp32 y16))
+ *   ora_rmsnorm       examples/ministral/native/predictor_shared_input.cu:16-34 (per-thread
+ *                     strided sum of x^2 over 256 threads, halving tree, inverse =
+ *                     1/sqrt(sum/width + eps), fp16(x*inverse) then the fp16 product with
+ *                     the weight); the reference's rsqrtf is an approximation, so the
+ *                     inverse is restated with IEEE sqrt and division
  *   ora_stream / ora_fill_*  the synthetic workload generator of this repository
  *                     (counter-based splitmix64, Irwin-Hall normal, double->fp16 RNE)
  * Rounding to fp16 is this file's own round-to-nearest-even integer implementation;
@@ -224,5 +230,31 @@ int ora_rank(const float* scores, uint32_t n, uint32_t k, int32_t* out) {
     qsort(ids, n, sizeof(int32_t), rank_cmp);
     memcpy(out, ids, sizeof(int32_t) * k);
     free(ids);
+    return 0;
+}
+
+/* ---------------- epilogue: next-hidden publication and RMSNorm ---------------- */
+void ora_publish_hidden(const uint16_t* residual, const uint16_t* y16, uint32_t n, uint16_t* hidden) {
+    for (uint32_t c = 0; c < n; ++c)
+        hidden[c] = ora_f32_to_f16(ora_f16_to_f32(residual[c]) + ora_f16_to_f32(y16[c]));
+}
+
+int ora_rmsnorm(const uint16_t* x, const uint16_t* weight, float eps, uint32_t width, uint16_t* out) {
+    float lanes[256];
+    if (!width) return -1;
+    for (int t = 0; t < 256; ++t) {
+        float sum = 0.f;
+        for (uint32_t i = (uint32_t)t; i < width; i += 256) {
+            const float v = ora_f16_to_f32(x[i]);
+            sum += v * v;
+        }
+        lanes[t] = sum;
+    }
+    const float total = tree256(lanes);
+    const float inverse = 1.0f / sqrtf(total / (float)width + eps);
+    for (uint32_t i = 0; i < width; ++i) {
+        const float normalized = round_half(ora_f16_to_f32(x[i]) * inverse);
+        out[i] = ora_f32_to_f16(ora_f16_to_f32(weight[i]) * normalized);   /* exact product, one rounding */
+    }
     return 0;
 }

@@ -24,4 +24,6 @@ int ora_layer(const ora_desc* descs, uint32_t count, uint32_t rows, const uint8_
               const uint16_t* scales, const uint16_t* x, uint32_t width, uint32_t G, int threads, float* y32,
               uint16_t* y16, float* h_rows, float* partial);
 int ora_rank(const float* scores, uint32_t n, uint32_t k, int32_t* out);
+void ora_publish_hidden(const uint16_t* residual, const uint16_t* y16, uint32_t n, uint16_t* hidden);
+int ora_rmsnorm(const uint16_t* x, const uint16_t* weight, float eps, uint32_t width, uint16_t* out);
 #endif

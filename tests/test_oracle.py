@@ -209,3 +209,44 @@ def test_f64_to_bf16_round_to_nearest_even():
     f16 = synth.bf16_to_f16(q).astype(np.float64)
     big = np.abs(val) >= 2.0 ** -17
     assert np.array_equal(f16[big], val[big])
+
+
+# ---------------------------------------------------------------------------- epilogue
+def test_publish_hidden_closed_forms():
+    rng = np.random.default_rng(21)
+    y = rng.standard_normal(4096).astype(np.float16)
+    r = rng.standard_normal(4096).astype(np.float16)
+    z = np.zeros(4096, dtype=np.float16)
+    assert np.array_equal(oracle.publish_hidden(z, y).view(np.uint16), y.view(np.uint16))
+    assert np.array_equal(oracle.publish_hidden(r, z).view(np.uint16), r.view(np.uint16))
+    assert np.array_equal(oracle.publish_hidden(r, y).view(np.uint16), oracle.publish_hidden(y, r).view(np.uint16))
+    # the sum of two fp16 values is exact in float64: one rounding of the exact sum (numpy)
+    want = (r.astype(np.float64) + y.astype(np.float64)).astype(np.float16)
+    assert np.array_equal(oracle.publish_hidden(r, y).view(np.uint16), want.view(np.uint16))
+
+
+def test_rmsnorm_closed_forms_and_planted_mistake():
+    w1 = np.ones(4096, dtype=np.float16)
+    # a constant row c: mean(x^2) = c^2, so x / rms = 1 (eps 0), within fp32 rounding of 1/sqrt
+    for c in (0.5, -3.0, 1e-2):
+        out = oracle.rmsnorm(np.full(4096, c, dtype=np.float16), w1, 0.0).astype(np.float64)
+        assert np.all(np.abs(out - np.sign(c)) <= 2.0 ** -10), c
+    # eps adds to the mean square, not the sum: c = 1, eps = 3 -> 1 / sqrt(4) = 0.5
+    out = oracle.rmsnorm(np.ones(1024, dtype=np.float16), np.ones(1024, dtype=np.float16), 3.0)
+    assert np.all(out == np.float16(0.5))
+    # brute force in float64 (the fp16 roundings of x / rms and of the weight product)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(4096).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 4096).astype(np.float16)
+    xf = x.astype(np.float64)
+    inv = 1.0 / np.sqrt(np.mean(xf * xf) + 1e-5)
+    want = (w.astype(np.float64) * (xf * inv).astype(np.float16).astype(np.float64)).astype(np.float16)
+    got = oracle.rmsnorm(x, w, 1e-5)
+    ulps = np.abs(got.view(np.int16).astype(np.int64) - want.view(np.int16).astype(np.int64))
+    assert ulps.max() <= 1 and np.count_nonzero(ulps) < 40
+    # scaling the weight by 2 scales the output exactly (outside fp16's subnormal range,
+    # where rounding is not scale-invariant)
+    twice = oracle.rmsnorm(x, (w.astype(np.float32) * 2).astype(np.float16), 1e-5).astype(np.float32)
+    normal = np.abs(got.astype(np.float32)) >= 2.0 ** -14
+    assert normal.sum() > 4000
+    assert np.array_equal(twice[normal], got.astype(np.float32)[normal] * 2)
