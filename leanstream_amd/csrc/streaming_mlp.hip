@@ -1992,6 +1992,7 @@ constexpr int kDenseDnWaves = kDenseCols / 32;   // 32 columns per wave
 constexpr int kDensePitch = 72;    // fp16 per LDS row: 64 neurons + 8 (rows stay 16-byte aligned)
 constexpr int kDenseGuWaves = 8;   // gate/up waves per workgroup, each reduces D / 8 columns
 constexpr int kDensePrefetch = 6;  // units whose down-tile loads are in flight per workgroup (9 loads each)
+constexpr int kDenseGuWindow = 3;  // gate/up steps (64 columns) whose weight loads a wave keeps in flight
 
 __device__ __forceinline__ _Float16 bf16_to_f16(uint32_t bits) {
     return (_Float16)__builtin_bit_cast(float, bits << 16);
@@ -2041,11 +2042,12 @@ __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
 // Gate/up of one 32-neuron half of one unit for all batch rows. Wave w reduces the
 // eighth [w D/8, (w+1) D/8) of the input in NI steps of 64 columns; the eight partial
 // tiles meet in LDS. Lane l (neuron 32 half + l % 32, row l % 32 of x) takes 32
-// consecutive columns per step: 16 bytes of each weight row and 64 bytes of x16. All NI
-// steps' weight loads are issued before the first MFMA (NI <= 16: at most 128 registers),
-// so a wave keeps its whole share of the weights in flight.
+// consecutive columns per step: 16 bytes of each weight row and 64 bytes of x16. Up to
+// d = 4096 the kernel stays within 128 registers (four waves per SIMD: two workgroups per
+// CU, so the whole layer's workgroups are resident at once) with the weights of
+// kDenseGuWindow steps in flight per wave.
 template <int NI>
-__global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(64 * kDenseGuWaves, NI <= 8 ? 4 : 2) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
     __shared__ float red[kDenseGuWaves / 2][2][16][64];   // 32 KB: two workgroups per CU fit
     constexpr uint32_t D = NI * 64 * kDenseGuWaves;
     constexpr uint32_t kq = D / kDenseGuWaves;
@@ -2073,13 +2075,17 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
         };
         issue_x(0, xq[0]);
         if (NI > 1) issue_x(1, xq[1]);
-        u32x4 qg[NI], qu[NI];
-#pragma unroll
-        for (int t = 0; t < NI; ++t) {
+        // The weights of WIN steps are in flight: step t's pieces go out into the slot
+        // step t - WIN has just been computed from.
+        constexpr int WIN = NI < kDenseGuWindow ? NI : kDenseGuWindow;
+        u32x4 qg[WIN], qu[WIN];
+        auto issue_w = [&](int t) {
             const uint32_t k0 = w * kq + 64 * t + 32 * hh;
-            qg[t] = ld_cached16(wg + k0 / 2);   // a row's 128-byte line serves four steps
-            qu[t] = ld_cached16(wu + k0 / 2);
-        }
+            qg[t % WIN] = ld_cached16(wg + k0 / 2);   // a row's 128-byte line serves four steps
+            qu[t % WIN] = ld_cached16(wu + k0 / 2);
+        };
+#pragma unroll
+        for (int t = 0; t < WIN; ++t) issue_w(t);
         // The wave's K range covers SB consecutive scale blocks of each row (step t uses
         // block t / 2): one 8-byte load per projection row where SB is a multiple of 4.
         constexpr int SB = NI >= 2 ? NI / 2 : 1;
@@ -2114,8 +2120,8 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
             for (int j = 0; j < 4; ++j) {
                 const h8 xa = __builtin_bit_cast(h8, xq[t % 3][j]);   // paired (dense_x_kernel)
                 h2 wgv[4], wuv[4];
-                dequant8(qg[t][j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
-                dequant8(qu[t][j], su2, wuv);
+                dequant8(qg[t % WIN][j], sg2, wgv);   // (column 8 j + i, column 8 j + i + 4)
+                dequant8(qu[t % WIN][j], su2, wuv);
                 h8 bg, bu;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -2127,6 +2133,7 @@ __global__ __launch_bounds__(64 * kDenseGuWaves) void dense_gate_up_kernel(MlpAr
                 cg = mfma32(xa, bg, cg);
                 cu = mfma32(xa, bu, cu);
             }
+            if (t + WIN < NI) issue_w(t + WIN);
         }
     }
     // Fixed-order sum of the eight partial tiles: wave w + 4 into wave w, then waves 0..3.
@@ -2227,7 +2234,12 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs 
     __shared__ alignas(16) _Float16 hl[32][kDensePitch];
     const uint32_t D = a.width;
     const uint32_t tiles = D / kDenseCols;
-    const uint32_t ct = blockIdx.x % tiles, split = blockIdx.x / tiles;
+    // XCD-aware order: workgroup blk runs on XCD blk % 8; the tiles of a split go to one
+    // XCD (kDenseSplits is a multiple of 8), so the split's h rows and down-scale lines
+    // are fetched into that XCD's L2 once instead of once per XCD
+    static_assert(kDenseSplits % 8 == 0, "two splits per XCD");
+    const uint32_t xcd = blockIdx.x % 8u, j = blockIdx.x / 8u;
+    const uint32_t split = xcd + 8u * (j / tiles), ct = j % tiles;
     const uint32_t c0 = ct * kDenseCols;
     const uint32_t per = (a.core_count + a.dsplits - 1) / a.dsplits;
     const uint32_t u0 = min(a.core_count, split * per), u1 = min(a.core_count, u0 + per);
