@@ -274,6 +274,12 @@ bool HipBackend::complete(void* ctx, uint32_t layer) {
 
 int HipBackend::commit(void* ctx, uint32_t layer, Span<GroupId> ids) {
     auto& b = *static_cast<HipBackend*>(ctx);
+    // A launch that raised a status bit (a bounded wait expired -- e.g. CUs held by another
+    // process kept the persistent grid from being co-resident --, a descriptor or the queue
+    // was rejected, a value was out of range) produced no valid output: the layer is not
+    // committed, so LayerStep::commit fails and the caller aborts the step. The bits stay
+    // set until clear_status().
+    if (const uint32_t st = b.status()) return st & lsamd::kStatusTimeout ? ETIMEDOUT : EIO;
     // Cache installation is application policy: without the application's hook the
     // backend cannot install anything and says so, as LeanStream's Triton backend does
     // (backends/triton/enqueue.cpp:45).

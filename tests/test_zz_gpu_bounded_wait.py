@@ -1,6 +1,7 @@
 """Every device wait is bounded: a layer whose epoch is never published ends with the
 timeout status bit instead of hanging (the condition is forced from the host with a
 short spin limit on the kernel's own bounded wait)."""
+import ctypes as C
 import time
 
 import numpy as np
@@ -11,6 +12,19 @@ from leanstream_amd.backend import MODE_PROGRESSIVE, STATUS_TIMEOUT
 from leanstream_amd.workload import DeviceLayer
 
 pytestmark = pytest.mark.gpu
+
+ETIMEDOUT, ENOTSUP = 110, 95
+
+
+class _Span(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("size", C.c_size_t)]
+
+
+class _ComputeBackend(C.Structure):
+    """ComputeBackend (include/leanstream/runtime.h): context + five function pointers."""
+    _fields_ = [("context", C.c_void_p), ("enqueue", C.c_void_p), ("complete", C.c_void_p),
+                ("commit", C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, _Span)), ("defer_commit", C.c_void_p),
+                ("cancel", C.c_void_p)]
 
 
 def test_unpublished_epoch_times_out(torch_gpu):
@@ -28,7 +42,12 @@ def test_unpublished_epoch_times_out(torch_gpu):
     torch.cuda.synchronize()
     assert time.time() - t0 < 5.0
     assert layer.backend.status() & STATUS_TIMEOUT
+    # the ComputeBackend view refuses to commit a layer whose launch timed out
+    view = _ComputeBackend()
+    assert layer.backend.lib.ls_hip_compute_backend(layer.backend.context, C.byref(view), C.sizeof(view)) == 0
+    assert view.commit(view.context, 0, _Span(None, 0)) == ETIMEDOUT
     layer.backend.clear_status()
+    assert view.commit(view.context, 0, _Span(None, 0)) == ENOTSUP   # no install hook: as before
     layer.backend.set_spin_limit(200_000_000)
     # the backend keeps working afterwards
     layer.seal_empty_queue(8)
