@@ -50,6 +50,10 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kWgPerCu = 2;          // resident workgroups per CU (register budget 256 per lane)
 constexpr int kDnRows = 64;          // rows of one down-item pass: 8 row groups x 8 rows
 constexpr int kDescItems = 12;       // item descriptors fetched per round trip (5 words each)
+// LDS per wave of the non-staged walks (16-byte vectors): a down item's 256 column sums for
+// the re-deal, then (batch rows) the rows' fp16 h for down items shared by the rows.
+template <int NB>
+constexpr int kNonStagedWaveVecs = (kDnCols * 4 + (NB > 1 ? NB * kDnRows * 2 : 0)) / 16;
 constexpr bool kSplitRoles = false;  // all-ready path: gate/up and down items on different workgroups
 #ifndef LS_GU_HALVES
 #define LS_GU_HALVES 1
@@ -535,18 +539,23 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
 
 // Waits until the h of every row of the pass carries the launch sequence. False when
 // the wait was abandoned (abort or timeout).
-__device__ __forceinline__ bool dn_wait_h(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int G, int r0,
-                                          DnItem& it) {
+__device__ __forceinline__ bool wait_h_word(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int r0,
+                                            uint64_t& h) {
     const uint64_t want = a.seq;
-    if (__all((it.h >> 32) == want)) return true;
+    if (__all((h >> 32) == want)) return true;
     const int n = r0 + lane_id();
     Waiter wt(a.spin_limit);
     for (;;) {
         if (wave_should_stop(a, slot, wt)) return false;
         __builtin_amdgcn_s_sleep(1);
-        if ((it.h >> 32) != want) it.h = ld_agent_u64(hrow + n);   // only rows < G can be stale
-        if (__all((it.h >> 32) == want)) return true;
+        if ((h >> 32) != want) h = ld_agent_u64(hrow + n);   // only rows < G can be stale
+        if (__all((h >> 32) == want)) return true;
     }
+}
+__device__ __forceinline__ bool dn_wait_h(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int G, int r0,
+                                          DnItem& it) {
+    (void)G;
+    return wait_h_word(a, slot, hrow, r0, it.h);
 }
 
 // Adds one pass into the lane's 32 column partials. The pass's h and scales go through
@@ -764,6 +773,65 @@ __device__ __forceinline__ void add_columns(const MlpArgs& a, uint32_t* slot, un
     pd.n = 4;
 }
 
+// Sum over the 8 row groups of 8 column partials, in dn_reduce's tree (row groups g, g ^ 4,
+// then g ^ 2, then g ^ 1), so a column gets the bits it gets there. Returns column g of the 8.
+__device__ __forceinline__ float dn_reduce8(const float acc[8]) {
+    float s1[4], s2[2];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) s1[c] = swap_sum32(acc[c], acc[c + 4]);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) s2[c] = swap_sum16(s1[c], s1[c + 2]);
+    const bool odd = (lane_id() >> 3) & 1;
+    const float x = odd ? s2[1] : s2[0], y = odd ? s2[0] : s2[1];
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x128, 0xF, 0xF, false));
+}
+
+// A down item for every batch row at once (batch 2..4, one 64-row pass): the item's pieces
+// are dequantised once and multiplied with the h of each row (hb[r]: row r's fp16 h in this
+// wave's LDS). The lane's 32 columns go in quarters of 8 (8 partials per row in flight),
+// each quarter summed over the row groups at once (dn_reduce8): part[r][q] is column
+// 32 dc + 8 q + g of the tile for row r. The dot2 order and the reduction tree are those of
+// dn_accumulate and dn_reduce: every row gets the bits a one-row item would give it.
+template <int NB>
+__device__ __forceinline__ void dn_accumulate_rows(const DnItem& it, const uint16_t (*hb)[kDnRows], uint16_t* ss,
+                                                   uint32_t nb, float (&part)[NB][4]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    ss[lane] = (uint16_t)it.s;
+    ss[kDnRows + lane] = (uint16_t)(it.s >> 16);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its loads
+    const u32x4 sv = *reinterpret_cast<const u32x4*>(ss + kDnRows * (dc >> 2) + 8 * g);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {   // columns 8 q + 0..7 of the lane's 32
+        float acc[NB][8];
+#pragma unroll
+        for (int r = 0; r < NB; ++r)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) acc[r][c] = 0.f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t xa = it.w[2 * p][q], xb = it.w[2 * p + 1][q];
+            const h2 sab = as_h2(sw[p]);
+            h2 w0[4], w1[4];
+            dequant8(__builtin_amdgcn_perm(xb, xa, 0x05040100u), sab, w0);   // columns 8q + 0..3
+            dequant8(__builtin_amdgcn_perm(xb, xa, 0x07060302u), sab, w1);   // columns 8q + 4..7
+#pragma unroll
+            for (int r = 0; r < NB; ++r) {
+                const h2 hab = as_h2(reinterpret_cast<const uint32_t*>(&hb[r][8 * g])[p]);   // rows 8g + 2p, + 1
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    acc[r][c] = dot2(w0[c], hab, acc[r][c]);
+                    acc[r][4 + c] = dot2(w1[c], hab, acc[r][4 + c]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < NB; ++r)
+            if ((uint32_t)r < nb) part[r][q] = dn_reduce8(acc[r]);
+    }
+}
+
 // Execution counters (diagnostics): a unit counts once all of its down items are done.
 __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot, uint32_t unit, uint32_t dest,
                                                 uint32_t items) {
@@ -931,7 +999,12 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     const uint32_t nu = u1 - u0;
     const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;   // gate/up items per unit (every batch row)
     const uint32_t NG = nu * ipu;
-    const ItemList il = make_items(role, NG, nu * nb * T);   // down items per batch unit
+    // With one 64-row pass (G <= 64) a down item serves every batch row: its pieces are
+    // loaded and dequantised once and multiplied with each row's h (dn_accumulate_rows).
+    // Larger groups take one down item per batch row and tile.
+    const bool dn_rows = NB > 1 && nb > 1 && G <= (uint32_t)kDnRows;
+    const uint32_t dnb = dn_rows ? 1u : nb;   // down items per unit and tile
+    const ItemList il = make_items(role, NG, nu * dnb * T);
     const uint32_t K = il.K, KG = il.KG;   // items of this wave; the first KG are gate/up
     // Every exit stages this wave's part of x first (siblings may be waiting for it).
     auto leave = [&](bool r) -> bool {
@@ -943,7 +1016,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
     uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, nb, word)) return leave(false);
+    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, dnb, word)) return leave(false);
     // x was loaded before the descriptors, so (in-order completion) it is in too
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     const int wave = wave_id();
@@ -970,7 +1043,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, nb, word))
+            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, dnb, word))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -996,12 +1069,12 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         Unit u;
         if (!fetch_unit(k, u)) return false;
         const uint32_t d = il.item(k) - NG, rel = d / T;
-        m.row = nb == 1 ? 0u : rel % nb;
+        m.row = dnb == 1 ? 0u : rel % dnb;
         m.grp = u.grp;
         m.sc = u.sc;
         m.dest = u.dest;
         m.hrow = a.hbuf + ((size_t)u.dest * nb + m.row) * G;
-        m.unit = u0 + (nb == 1 ? rel : rel / nb);
+        m.unit = u0 + (dnb == 1 ? rel : rel / dnb);
         m.tile = d - rel * T;
         dn_issue<D>(u.grp, u.sc, m.hrow, (int)G, (int)m.tile, 0, a.seq, di);
         // a fresh look at the epoch word, in flight with the item (U is needed to finish it)
@@ -1032,6 +1105,44 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
             U = a.core_count + ep.total;
             have_u = true;
         }
+        const int lane = lane_id();
+        float* red = reinterpret_cast<float*>(stage + wave * kNonStagedWaveVecs<NB>);
+        if constexpr (NB > 1) {
+            if (dn_rows) {
+                // every row's h: row 0 came with the item, the others go out now
+                uint16_t (*hb)[kDnRows] = reinterpret_cast<uint16_t (*)[kDnRows]>(red + kDnCols);
+                uint64_t hr[NB];
+                hr[0] = di.h;
+#pragma unroll
+                for (int r = 1; r < NB; ++r)
+                    hr[r] = (uint32_t)r < nb && lane < (int)G ? ld_agent_u64(m.hrow + (size_t)r * G + lane)
+                                                              : (uint64_t)a.seq << 32;
+#pragma unroll
+                for (int r = 0; r < NB; ++r) {
+                    if (!wait_h_word(a, slot, m.hrow + (size_t)r * G, 0, hr[r])) return false;
+                    hb[r][lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)hr[r]));   // exact
+                }
+                float part[NB][4];
+                dn_accumulate_rows<NB>(di, hb, ss, nb, part);
+                const int col0 = dn_tile_column(lane);
+#pragma unroll
+                for (int r = 0; r < NB; ++r) {
+                    if ((uint32_t)r >= nb) break;
+                    // re-deal row r's sums as the one-row items do
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) red[32 * (lane & 7) + 8 * q + (lane >> 3)] = part[r][q];
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    float cs[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) cs[i] = red[col0 + kTileColOff[i]];
+                    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+                    add_columns(a, slot, yacc, (int)(r * D + m.tile * kDnCols) + col0, cs, U, pd);
+                }
+                if (a.executions) count_execution(a, slot, m.unit, m.dest, T);
+                if (k == KG) stamp(a, kStampDnComputed);
+                return true;
+            }
+        }
         float acc[32];
 #pragma unroll
         for (int c = 0; c < 32; ++c) acc[c] = 0.f;
@@ -1044,8 +1155,6 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         dn_reduce(acc, cs);
         // re-deal through LDS: lane (g, dc) holds tile columns 32 dc + 4 g + i; lane l adds
         // columns dn_tile_column(l) + kTileColOff[i], as the staged walk does
-        const int lane = lane_id();
-        float* red = reinterpret_cast<float*>(stage) + wave * kDnCols;
         *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         const int col0 = dn_tile_column(lane);
@@ -1053,7 +1162,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         for (int i = 0; i < 4; ++i) cs[i] = red[col0 + kTileColOff[i]];
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         add_columns(a, slot, yacc, (int)(m.row * D + m.tile * kDnCols) + col0, cs, U, pd);
-        if (a.executions) count_execution(a, slot, m.unit, m.dest, T * nb);
+        if (a.executions) count_execution(a, slot, m.unit, m.dest, T * dnb);
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
     };
@@ -1866,9 +1975,9 @@ __device__ __forceinline__ void finish_launch(const MlpArgs& a, uint32_t* slot) 
 
 // LDS of a persistent workgroup beyond Shared and x: the staged kernels' item slots
 // (kWaves x 2), or the other kernels' per-wave re-deal rows of the down items.
-template <bool STAGED>
+template <bool STAGED, int NB>
 struct StageArea {
-    static constexpr int VECS = STAGED ? 2 * kWaves * kSlotStride : kWaves * kDnCols / 4;
+    static constexpr int VECS = STAGED ? 2 * kWaves * kSlotStride : kWaves * kNonStagedWaveVecs<NB>;
 };
 
 // The arguments a persistent worker needs before its first loads (x, its descriptors,
@@ -1903,7 +2012,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
+    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
     if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
@@ -1922,7 +2031,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(LS_HOT_PARA
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
+    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
     worker<D, false, true, false, NB, STAGED>(a, b, sh, xl, stage, slot);
 }
 
@@ -1932,7 +2041,7 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(LS_HOT_PARA
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED>::VECS];
+    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
     if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
