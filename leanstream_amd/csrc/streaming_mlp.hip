@@ -844,7 +844,8 @@ __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot
 // ---------------------------------------------------------------------------------
 
 // Unit (relative to u0) of item i: gate/up items [0, NG), ipu per unit (each serves every
-// batch row); then down items, T per batch unit (unit u, row b is batch unit u nb + b).
+// batch row); then down items, T per batch unit (unit u, row b is batch unit u nb + b;
+// nb = 1 when one down item serves every batch row).
 __device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T, uint32_t nb) {
     if (i < NG) return i / ipu;
     const uint32_t v = (i - NG) / T;
