@@ -1367,6 +1367,86 @@ __device__ __forceinline__ void dn_accumulate_tile(const u32x4* sl, const uint16
     }
 }
 
+#ifndef LS_DN_PRE
+#define LS_DN_PRE 1
+#endif
+// Row pairs of a staged down tile dequantised while the unit's h is on its way.
+constexpr int kDnPre = LS_DN_PRE;
+static_assert(kDnPre >= 0 && kDnPre <= 4, "a tile has four row pairs per lane");
+
+// Dequantises row pairs p < P of lane (g, dc)'s part of a staged tile (rows 8 g + 2 p,
+// + 1; columns 32 dc + 8 q + c): w[p][q][c], the operands dn_accumulate_tile forms.
+template <int P>
+__device__ __forceinline__ void dn_dequant_tile(const u32x4* sl, h2 (&w)[P > 0 ? P : 1][4][8]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const u32x4* sv = sl + kSlotVecs + 2 * g;
+    const u32x4 s0 = sv[0], s1 = sv[1];
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t pick = (dc >> 2) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const u32x4 va = sl[(2 * p) * 64 + lane], vb = sl[(2 * p + 1) * 64 + lane];
+        const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
+        const h2 sab = as_h2(__builtin_amdgcn_perm(sw[2 * p + 1], sw[2 * p], pick));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, &w[p][q][0]);
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, &w[p][q][4]);
+        }
+    }
+    // computed here, while h travels (the compiler would otherwise sink them to their uses)
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                uint32_t t = __builtin_bit_cast(uint32_t, w[p][q][c]);
+                asm volatile("" : "+v"(t));
+                w[p][q][c] = as_h2(t);
+            }
+}
+
+// dn_accumulate_tile with row pairs p < P already dequantised (dn_dequant_tile): the same
+// operands in the same order, so the same bits.
+template <int P>
+__device__ __forceinline__ void dn_accumulate_tile_pre(const u32x4* sl, const uint16_t* hs,
+                                                       const h2 (&pre)[P > 0 ? P : 1][4][8], float (&acc)[32]) {
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const u32x4* sv = sl + kSlotVecs + 2 * g;
+    const u32x4 s0 = sv[0], s1 = sv[1];
+    const uint32_t sw[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+    const uint32_t pick = (dc >> 2) ? 0x07060302u : 0x05040100u;
+    const u32x4 hv = *reinterpret_cast<const u32x4*>(hs + 8 * g);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+#pragma unroll
+    for (int c = 0; c < 32; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const h2 hab = as_h2(hw[p]);
+        if (p < P) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[8 * q + c] = dot2(pre[p < P ? p : 0][q][c], hab, acc[8 * q + c]);
+            continue;
+        }
+        const u32x4 va = sl[(2 * p) * 64 + lane], vb = sl[(2 * p + 1) * 64 + lane];
+        const uint32_t xa[4] = {va.x, va.y, va.z, va.w}, xb[4] = {vb.x, vb.y, vb.z, vb.w};
+        const h2 sab = as_h2(__builtin_amdgcn_perm(sw[2 * p + 1], sw[2 * p], pick));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h2 w[4];
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x05040100u), sab, w);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + c] = dot2(w[c], hab, acc[8 * q + c]);
+            dequant8(__builtin_amdgcn_perm(xb[q], xa[q], 0x07060302u), sab, w);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) acc[8 * q + 4 + c] = dot2(w[c], hab, acc[8 * q + 4 + c]);
+        }
+    }
+}
+
 // Sum of a quarter's column partials over the wave's 8 row groups through LDS, in
 // dn_reduce's tree ((0 + 4) + (2 + 6)) + ((1 + 5) + (3 + 7)), so that quarters and tiles
 // give the same bits. Lane (g, dc) stores its columns 8 dc + c at red[g][12 dc + c] (a
@@ -1592,12 +1672,14 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
             const float col_sum = dn_sum_groups_quarter(acc, reinterpret_cast<float*>(sl));
             add_column(a, slot, yacc, (int)(m.tile * kDnCols + m.row * 64) + lane, col_sum, U, pd);
         } else {
+            h2 pre[kDnPre > 0 ? kDnPre : 1][4][8];
+            dn_dequant_tile<kDnPre>(sl, pre);
             if (!dn_wait_h(a, slot, m.hrow, (int)G, 0, it)) return false;
             if (k == KG) stamp(a, kStampHReady);
             hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             float acc[32], cs[4];
-            dn_accumulate_tile(sl, hs, acc);
+            dn_accumulate_tile_pre<kDnPre>(sl, hs, pre, acc);
             dn_reduce(acc, cs);
             // re-deal through the slot (its pieces are in registers by now): lane (g, dc)
             // holds tile columns 32 dc + 4 g + i; lane l adds dn_tile_column(l) + kTileColOff[i]
