@@ -5,7 +5,10 @@
 // on (seed, i), so a host mirror (leanstream_amd/synth.py) produces the same bytes.
 //   bytes:    little-endian bytes of value(seed, i) for word i (uniform INT4 nibbles)
 //   uniform:  lo + (hi - lo) * u, u = (value >> 11) * 2^-53, rounded double -> fp16 (RNE)
-//   normal:   Irwin-Hall: sum of 12 uniforms (sequential double adds) - 6 -> fp16 or bf16 (RNE)
+//   normal:   Box-Muller of u1 = ((value(2i) >> 11) + 1) 2^-53 in (0, 1] and u2 = unit(2i + 1):
+//             sqrt(-2 ln u1) cos(2 pi u2) -> fp16 or bf16 (RNE). ln and cos are series in IEEE
+//             double +, -, *, / (no library calls, no fused multiply-add), so the host mirror
+//             computes the same doubles.
 // The double -> fp16 rounding is done in integer arithmetic (no double rounding).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -67,8 +70,8 @@ __global__ void synth_uniform_kernel(uint16_t* dst, uint64_t count, uint64_t see
         dst[i] = f64_to_f16_bits(lo + (hi - lo) * stream_unit(seed, i));
 }
 
-// Round-to-nearest-even conversion of a double to bfloat16 bits (finite, normal range:
-// the generator's values are in [-6, 6]; zero maps to +0).
+// Round-to-nearest-even conversion of a double to bfloat16 bits (finite values of the
+// normal generator, |v| < 9; below bf16's normal range maps to signed zero).
 __host__ __device__ inline uint16_t f64_to_bf16_bits(double d) {
     const uint64_t b = __builtin_bit_cast(uint64_t, d);
     const uint16_t sign = (uint16_t)((b >> 48) & 0x8000u);
@@ -88,20 +91,61 @@ __host__ __device__ inline uint16_t f64_to_bf16_bits(double d) {
     return sign | (uint16_t)(e << 7) | (uint16_t)m;
 }
 
-__global__ void synth_normal_bf16_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
-        double acc = 0.0;
-        for (int k = 0; k < 12; ++k) acc += stream_unit(seed, 12 * i + k);
-        dst[i] = f64_to_bf16_bits(acc - 6.0);
+// ln(u), u in (0, 1]: u = m 2^e with m in [sqrt(1/2), sqrt(2)), ln m = 2 atanh(t),
+// t = (m - 1) / (m + 1), series to t^25 in Horner form.
+__device__ inline double ln_unit(double u) {
+#pragma clang fp contract(off)
+    uint64_t b = __builtin_bit_cast(uint64_t, u);
+    int e = (int)((b >> 52) & 0x7ff) - 1022;
+    double m = __builtin_bit_cast(double, (b & 0x800FFFFFFFFFFFFFull) | (1022ull << 52));
+    if (m < 0.7071067811865476) {
+        m = m * 2.0;
+        e -= 1;
     }
+    const double t = (m - 1.0) / (m + 1.0), t2 = t * t;
+    double p = 1.0 / 25.0;
+    for (int k = 11; k >= 0; --k) p = p * t2 + 1.0 / (double)(2 * k + 1);
+    return (double)e * 0.6931471805599453 + 2.0 * t * p;
+}
+
+// cos(2 pi v), v in [0, 1): quadrant q = floor(4v), x = (4v - q) pi / 2, Taylor series of
+// cos x / sin x to x^22 / x^23, coefficients by the division sequence f = -f / ((k+1)(k+2)).
+__device__ inline double cos_turns(double v) {
+#pragma clang fp contract(off)
+    double cc[12], sc[12], f = 1.0, g = 1.0;
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        cc[k] = f;
+        sc[k] = g;
+        f = -f / (double)((2 * k + 1) * (2 * k + 2));
+        g = -g / (double)((2 * k + 2) * (2 * k + 3));
+    }
+    const double w = v * 4.0, q = __builtin_floor(w), x = (w - q) * 1.5707963267948966, x2 = x * x;
+    double c = cc[11], s = sc[11];
+#pragma unroll
+    for (int k = 10; k >= 0; --k) {
+        c = c * x2 + cc[k];
+        s = s * x2 + sc[k];
+    }
+    s = s * x;
+    return q == 0.0 ? c : q == 1.0 ? -s : q == 2.0 ? -c : s;
+}
+
+__device__ inline double box_muller(uint64_t seed, uint64_t i) {
+#pragma clang fp contract(off)
+    const double u1 = (double)((stream_value(seed, 2 * i) >> 11) + 1) * 0x1.0p-53;
+    const double u2 = stream_unit(seed, 2 * i + 1);
+    return __builtin_sqrt(-2.0 * ln_unit(u1)) * cos_turns(u2);
+}
+
+__global__ void synth_normal_bf16_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = f64_to_bf16_bits(box_muller(seed, i));
 }
 
 __global__ void synth_normal_kernel(uint16_t* dst, uint64_t count, uint64_t seed) {
-    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x) {
-        double acc = 0.0;
-        for (int k = 0; k < 12; ++k) acc += stream_unit(seed, 12 * i + k);
-        dst[i] = f64_to_f16_bits(acc - 6.0);
-    }
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = f64_to_f16_bits(box_muller(seed, i));
 }
 
 static unsigned grid_for(uint64_t n) {

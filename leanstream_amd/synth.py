@@ -4,7 +4,8 @@ Element i of every stream is mix64(seed + (i + 1) * 0x9E3779B97F4A7C15) (splitmi
 so host (numpy) and device generation produce identical bytes:
   * packed INT4 weights: the little-endian bytes of the stream (uniform nibbles in [-8, 7]);
   * fp16 scales: lo + (hi - lo) * u, u = (value >> 11) * 2^-53, rounded to fp16;
-  * fp16 activations: Irwin-Hall normal, sum of 12 uniforms - 6, rounded to fp16;
+  * fp16 / bf16 activations: standard normal by the Box-Muller transform of elements 2i and
+    2i + 1, rounded to fp16 / bf16 (normal_f64 states the arithmetic);
   * group scores: the same normal in fp32.
 
 Workloads named here are the layer shapes this library is measured on (d_model, d_ffn,
@@ -43,12 +44,59 @@ def uniform_f16(n, seed, lo, hi):
     return (lo + (hi - lo) * unit(seed, np.arange(n, dtype=np.uint64))).astype(np.float16)
 
 
+def _ln_unit(u):
+    """ln(u) for u in (0, 1] with IEEE +, -, *, / only (no library log): u = m 2^e with m in
+    [sqrt(1/2), sqrt(2)), ln m = 2 atanh(t), t = (m - 1) / (m + 1), series to t^25 in Horner form."""
+    m, e = np.frexp(u)
+    low = m < 0.7071067811865476
+    m = np.where(low, m * 2.0, m)
+    e = np.where(low, e - 1, e).astype(np.float64)
+    t = (m - 1.0) / (m + 1.0)
+    t2 = t * t
+    p = np.full_like(t, 1.0 / 25.0)
+    for k in range(11, -1, -1):
+        p = p * t2 + 1.0 / (2 * k + 1)
+    return e * 0.6931471805599453 + 2.0 * t * p
+
+
+def _cos_turns(v):
+    """cos(2 pi v) for v in [0, 1) with IEEE +, -, *, / only: quadrant q = floor(4 v) (exact),
+    x = (4 v - q) pi / 2, Taylor series of cos x and sin x to x^22 / x^23 in Horner form."""
+    w = v * 4.0
+    q = np.floor(w)
+    x = (w - q) * 1.5707963267948966
+    x2 = x * x
+    c = np.full_like(x, _COS_C[-1])
+    s = np.full_like(x, _SIN_C[-1])
+    for k in range(len(_COS_C) - 2, -1, -1):
+        c = c * x2 + _COS_C[k]
+        s = s * x2 + _SIN_C[k]
+    s = s * x
+    return np.where(q == 0, c, np.where(q == 1, -s, np.where(q == 2, -c, s)))
+
+
+def _taylor(first):
+    out, f, k = [], 1.0, first
+    for _ in range(12):
+        out.append(f)
+        f = -f / ((k + 1) * (k + 2))
+        k += 2
+    return out
+
+
+_COS_C = _taylor(0)   # (-1)^k / (2k)!     as the sequence of divisions above gives them
+_SIN_C = _taylor(1)   # (-1)^k / (2k + 1)!
+
+
 def normal_f64(n, seed):
-    base = np.arange(n, dtype=np.uint64) * np.uint64(12)
-    acc = np.zeros(n, dtype=np.float64)
-    for k in range(12):
-        acc += unit(seed, base + np.uint64(k))
-    return acc - 6.0
+    """Standard normal values: Box-Muller of u1 = ((v(2i) >> 11) + 1) 2^-53 in (0, 1] and
+    u2 = (v(2i+1) >> 11) 2^-53 in [0, 1): sqrt(-2 ln u1) cos(2 pi u2). Every step is an IEEE
+    double operation (frexp, +, -, *, /, sqrt) in a fixed order, so the C oracle and the device
+    generator compute the same doubles."""
+    i = np.arange(n, dtype=np.uint64) * np.uint64(2)
+    u1 = ((stream(seed, i) >> np.uint64(11)) + np.uint64(1)).astype(np.float64) * (2.0 ** -53)
+    u2 = unit(seed, i + np.uint64(1))
+    return np.sqrt(-2.0 * _ln_unit(u1)) * _cos_turns(u2)
 
 
 def normal_f16(n, seed):
@@ -76,7 +124,7 @@ def f64_to_bf16_bits(v):
 
 
 def normal_bf16(n, seed):
-    """bfloat16 bits of the Irwin-Hall normal stream."""
+    """bfloat16 bits of the normal stream."""
     return f64_to_bf16_bits(normal_f64(n, seed))
 
 

@@ -17,7 +17,8 @@
  *                     the weight); the reference's rsqrtf is an approximation, so the
  *                     inverse is restated with IEEE sqrt and division
  *   ora_stream / ora_fill_*  the synthetic workload generator of this repository
- *                     (counter-based splitmix64, Irwin-Hall normal, double->fp16 RNE)
+ *                     (counter-based splitmix64, Box-Muller normal with its own ln / cos
+ *                     series in IEEE double operations, double->fp16 RNE)
  * Rounding to fp16 is this file's own round-to-nearest-even integer implementation;
  * exp is the C library's expf (the reference's expf/tl.exp are only pinned to
  * tolerance by its own tests).
@@ -117,10 +118,50 @@ void ora_fill_uniform_f16(uint16_t* dst, uint64_t n, uint64_t seed, double lo, d
     for (uint64_t i = 0; i < n; ++i) dst[i] = ora_f64_to_f16(lo + (hi - lo) * unit(seed, i));
 }
 
+/* ln(u), u in (0, 1]: u = m 2^e with m in [sqrt(1/2), sqrt(2)) (exponent bits, exact),
+ * ln m = 2 atanh(t), t = (m - 1) / (m + 1), series to t^25 in Horner form. */
+static double ln_unit(double u) {
+    uint64_t b;
+    memcpy(&b, &u, 8);
+    int e = (int)((b >> 52) & 0x7ff) - 1022;
+    b = (b & 0x800FFFFFFFFFFFFFull) | (1022ull << 52);   /* m in [0.5, 1) */
+    double m;
+    memcpy(&m, &b, 8);
+    if (m < 0.7071067811865476) {
+        m = m * 2.0;
+        e -= 1;
+    }
+    const double t = (m - 1.0) / (m + 1.0), t2 = t * t;
+    double p = 1.0 / 25.0;
+    for (int k = 11; k >= 0; --k) p = p * t2 + 1.0 / (double)(2 * k + 1);
+    return (double)e * 0.6931471805599453 + 2.0 * t * p;
+}
+
+/* cos(2 pi v), v in [0, 1): quadrant q = floor(4v), x = (4v - q) pi/2, Taylor series of
+ * cos x / sin x to x^22 / x^23 (coefficients by the division sequence f = -f / ((k+1)(k+2))). */
+static double cos_turns(double v) {
+    double cc[12], sc[12], f = 1.0, g = 1.0;
+    for (int k = 0; k < 12; ++k) {
+        cc[k] = f;
+        sc[k] = g;
+        f = -f / (double)((2 * k + 1) * (2 * k + 2));
+        g = -g / (double)((2 * k + 2) * (2 * k + 3));
+    }
+    const double w = v * 4.0, q = floor(w), x = (w - q) * 1.5707963267948966, x2 = x * x;
+    double c = cc[11], s = sc[11];
+    for (int k = 10; k >= 0; --k) {
+        c = c * x2 + cc[k];
+        s = s * x2 + sc[k];
+    }
+    s = s * x;
+    return q == 0.0 ? c : q == 1.0 ? -s : q == 2.0 ? -c : s;
+}
+
+/* Standard normal by Box-Muller: u1 = ((v(2i) >> 11) + 1) 2^-53 in (0, 1], u2 = unit(2i + 1). */
 double ora_normal(uint64_t seed, uint64_t i) {
-    double acc = 0.0;
-    for (int k = 0; k < 12; ++k) acc += unit(seed, 12 * i + (uint64_t)k);
-    return acc - 6.0;
+    const double u1 = (double)((ora_stream(seed, 2 * i) >> 11) + 1) * (1.0 / 9007199254740992.0);
+    const double u2 = unit(seed, 2 * i + 1);
+    return sqrt(-2.0 * ln_unit(u1)) * cos_turns(u2);
 }
 
 void ora_fill_normal_f16(uint16_t* dst, uint64_t n, uint64_t seed) {
