@@ -132,6 +132,7 @@ struct MlpArgs {
                                   // claim up to n ready positions at a time
     uint32_t batch;               // rows of x / y (1 .. kMaxBatch; dense path: kMaxBatch + 1 .. kMaxDenseBatch)
     uint32_t grid;                // workgroups of a persistent launch (workers + the mirror)
+    uint32_t pack;                // units per down item: 64 / G for the packed kernels, else 1 (set per launch)
     // dense path (batch > kMaxBatch): x is bf16 [batch][d]
     uint16_t* h16;                // fp16 h rows [32][slot_capacity * G]
     float* dpart;                 // fp32 down-projection partial rows [dsplits][32][d]

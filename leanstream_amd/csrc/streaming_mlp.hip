@@ -846,10 +846,30 @@ __device__ __forceinline__ void count_execution(const MlpArgs& a, uint32_t* slot
 // Unit (relative to u0) of item i: gate/up items [0, NG), ipu per unit (each serves every
 // batch row); then down items, T per batch unit (unit u, row b is batch unit u nb + b;
 // nb = 1 when one down item serves every batch row).
-__device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T, uint32_t nb) {
+// With packs of P units (P > 1, pack_units) a down item stands for its pack's last unit
+// (nu units in the range), the one whose publication it waits for.
+__device__ __forceinline__ uint32_t item_unit(uint32_t i, uint32_t NG, uint32_t ipu, uint32_t T, uint32_t nb,
+                                              uint32_t P = 1, uint32_t nu = 0) {
     if (i < NG) return i / ipu;
-    const uint32_t v = (i - NG) / T;
-    return nb == 1 ? v : v / nb;
+    uint32_t v = (i - NG) / T;
+    v = nb == 1 ? v : v / nb;
+    return P == 1 ? v : min(v * P + P, nu) - 1;
+}
+
+// Small groups (G <= 32) at batch 1 (the packed kernels, MlpArgs::pack = 64 / G): a down
+// item of the resident (core) range packs the rows of P consecutive core units into one
+// 64-row pass (row G j + n is neuron n of the pack's unit j), so a tile column takes one
+// contribution per pack instead of one per unit. Core units are in descriptor order, so the
+// packs and their sums are the same in every launch. Queue units keep one unit per down item:
+// their positions follow the publication order, and one contribution per unit keeps y
+// independent of that order.
+__device__ __forceinline__ uint32_t pack_units(const MlpArgs& a) { return a.pack > 1 ? a.pack : 1u; }
+// Contributions per output column of a fused launch: one per down item of a column tile.
+template <bool PACKED>
+__device__ __forceinline__ uint32_t column_rows(const MlpArgs& a, uint32_t total) {
+    if constexpr (!PACKED) return a.core_count + total;
+    const uint32_t P = pack_units(a);
+    return (a.core_count + P - 1) / P + total;
 }
 
 // How the waves taking part share the items of a unit range: wave w of nw. With
@@ -925,13 +945,14 @@ __device__ __forceinline__ ItemList make_staged_items(const WaveRole& r, uint32_
 // the last position of the batch (`seen` is the count it last observed).
 __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, uint32_t u0, uint32_t& seen,
                                             const ItemList& il, uint32_t k0, uint32_t count, uint32_t ipu,
-                                            uint32_t T, uint32_t nb, uint32_t& word) {
+                                            uint32_t T, uint32_t nb, uint32_t& word, uint32_t P = 1,
+                                            uint32_t nu = 0) {
     // units rise along each of the wave's two lists (gate/up, then down items), so the
     // batch's last position is that of its last gate/up or its last down item
     const uint32_t kl = k0 + count - 1;
     uint32_t last = 0;
-    if (k0 < il.KG) last = item_unit(il.item(min(kl, il.KG - 1)), il.NG, ipu, T, nb);
-    if (kl >= il.KG) last = max(last, item_unit(il.item(kl), il.NG, ipu, T, nb));
+    if (k0 < il.KG) last = item_unit(il.item(min(kl, il.KG - 1)), il.NG, ipu, T, nb, P, nu);
+    if (kl >= il.KG) last = max(last, item_unit(il.item(kl), il.NG, ipu, T, nb, P, nu));
     const uint32_t g = u0 + last;
     const uint32_t need = g >= a.core_count ? g - a.core_count + 1 : 0u;
     if (need > seen) {
@@ -951,7 +972,7 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
     word = 0;
     if (lane < 5 * count) {
         const uint32_t j = lane / 5, w = lane - 5 * j;
-        const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T, nb);
+        const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T, nb, P, nu);
         word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
                                 : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
@@ -974,6 +995,78 @@ __device__ __forceinline__ bool unit_of(const MlpArgs& a, uint32_t* slot, const 
     return true;
 }
 
+// A packed down item's rows (pack_units): lane r holds row r's h pointer, unit and
+// destination; `lead` marks the lane of each unit's first row.
+struct PackLane {
+    const uint64_t* hp;
+    uint32_t unit, dest;
+    bool lead;
+};
+
+// Issues a down item over the rows of `units` consecutive units g0, g0 + 1, ... (G rows each,
+// G <= 32): lane r resolves the descriptor of row r's unit (agent-scope loads: queue
+// descriptors are mirrored during the launch) and holds that row's scales and h; lane 8 g + dc
+// loads columns 32 dc .. 32 dc + 31 of rows 8 g .. 8 g + 7 from their units' groups. Rows past
+// the pack have zero weights, scales and h. False (status raised) on an invalid descriptor.
+template <int D>
+__device__ __forceinline__ bool dn_issue_pack(const MlpArgs& a, uint32_t* slot, const Bounds& b, uint32_t g0,
+                                              uint32_t units, int tile, DnItem& it, PackLane& pl) {
+    constexpr int BLOCKS = D / 128;
+    constexpr int RB = 3 * D / 2;
+    const uint32_t G = a.group_size;
+    const int lane = lane_id(), g = lane >> 3, dc = lane & 7;
+    const uint32_t j = (uint32_t)lane / G, n = (uint32_t)lane - j * G;
+    const bool valid = j < units;
+    Unit u{nullptr, nullptr, 0, true};
+    if (valid) {
+        const uint32_t gu = g0 + j;
+        const uint32_t* w = gu < a.core_count ? reinterpret_cast<const uint32_t*>(a.core) + 5 * gu
+                                              : a.qmirror + 5 * (gu - a.core_count);
+        ExecDesc d;
+        d.logical_group = 0;
+        d.physical_group = ld_agent(w + 1);
+        d.source_slot = ld_agent(w + 2);
+        d.dest_slot = ld_agent(w + 3);
+        d.source_kind = (leanstream::runtime::SourceKind)ld_agent(w + 4);
+        u = resolve(a, b, d, D);
+    }
+    if (!__all(u.ok)) {
+        if (lane == 0) raise_status(a, slot, kStatusBadDescriptor);
+        return false;
+    }
+    const uint8_t* row = valid ? u.grp + (size_t)n * RB + D + tile * (kDnCols / 2) : nullptr;
+    const uint64_t rp = reinterpret_cast<uint64_t>(row);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int r = 8 * g + k;
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(r << 2, (int)(uint32_t)rp);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(r << 2, (int)(uint32_t)(rp >> 32));
+        const uint8_t* p = reinterpret_cast<const uint8_t*>((uint64_t)hi << 32 | lo);
+        it.w[k] = (uint32_t)r / G < units ? ld_stream16(p + dc * 16) : u32x4{0, 0, 0, 0};
+    }
+    it.s = valid ? *reinterpret_cast<const uint32_t*>(u.sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile) : 0u;
+    pl.hp = a.hbuf + (size_t)u.dest * G + n;
+    pl.unit = g0 + j;
+    pl.dest = u.dest;
+    pl.lead = valid && n == 0;
+    it.h = valid ? ld_agent_u64(pl.hp) : (uint64_t)a.seq << 32;
+    return true;
+}
+
+// Waits until every lane's h word carries the launch sequence, reloading from the lane's own
+// pointer (lanes already tagged never reload). False when the wait was abandoned.
+__device__ __forceinline__ bool wait_h_lanes(const MlpArgs& a, uint32_t* slot, const uint64_t* hp, uint64_t& h) {
+    const uint64_t want = a.seq;
+    if (__all((h >> 32) == want)) return true;
+    Waiter wt(a.spin_limit);
+    for (;;) {
+        if (wave_should_stop(a, slot, wt)) return false;
+        __builtin_amdgcn_s_sleep(1);
+        if ((h >> 32) != want) h = ld_agent_u64(hp);
+        if (__all((h >> 32) == want)) return true;
+    }
+}
+
 // Wave-uniform bookkeeping of an item in flight.
 struct ItemMeta {
     const uint8_t* grp;
@@ -988,7 +1081,7 @@ struct ItemMeta {
 // wait for another wave; down items wait for their unit's h (after every gate/up item
 // of this wave), so every h is eventually published. With FUSED, the U-th contribution
 // of a column writes the output (U = core + queue units, learnt from the epoch word).
-template <int D, bool FUSED, int NB>
+template <int D, bool FUSED, int NB, bool PACKED>
 __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x4* stage, uint32_t* slot, const Bounds& b,
                                               unsigned long long* yacc, XPart<D>& xp, u32x4* xl, Epoch& ep,
                                               uint32_t early, Pending& pd, uint32_t u0, uint32_t u1,
@@ -1005,7 +1098,9 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     // Larger groups take one down item per batch row and tile.
     const bool dn_rows = NB > 1 && nb > 1 && G <= (uint32_t)kDnRows;
     const uint32_t dnb = dn_rows ? 1u : nb;   // down items per unit and tile
-    const ItemList il = make_items(role, NG, nu * dnb * T);
+    const uint32_t P = PACKED && u1 <= a.core_count ? pack_units(a) : 1u;   // units per down item (core range)
+    const uint32_t NP = (nu + P - 1) / P;              // down items per tile (and batch row)
+    const ItemList il = make_items(role, NG, NP * dnb * T);
     const uint32_t K = il.K, KG = il.KG;   // items of this wave; the first KG are gate/up
     // Every exit stages this wave's part of x first (siblings may be waiting for it).
     auto leave = [&](bool r) -> bool {
@@ -1017,7 +1112,8 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
     uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, dnb, word)) return leave(false);
+    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, dnb, word, P, nu))
+        return leave(false);
     // x was loaded before the descriptors, so (in-order completion) it is in too
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     const int wave = wave_id();
@@ -1026,6 +1122,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     GuItem<D> gi;
     DnItem di;
     ItemMeta m;
+    PackLane pl{nullptr, 0, 0, false};
     uint32_t U = 0;
     bool have_u = !FUSED;
 
@@ -1044,7 +1141,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     auto fetch_unit = [&](uint32_t k, Unit& u) -> bool {
         if (k - k0 >= (uint32_t)kDescItems) {
             k0 = k;
-            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, dnb, word))
+            if (!fetch_descs(a, slot, u0, seen, il, k0, min(K - k0, (uint32_t)kDescItems), ipu, T, dnb, word, P, nu))
                 return false;
         }
         return unit_of(a, slot, b, word, k - k0, D, u);
@@ -1068,8 +1165,16 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     };
     auto issue_dn = [&](uint32_t k, DnItem& di, ItemMeta& m) -> bool {
         Unit u;
-        if (!fetch_unit(k, u)) return false;
+        if (!fetch_unit(k, u)) return false;   // a pack's last unit: every unit of it is published
         const uint32_t d = il.item(k) - NG, rel = d / T;
+        if constexpr (PACKED) {
+            m.row = 0;
+            m.unit = u0 + rel * P;
+            m.tile = d - rel * T;
+            if (!dn_issue_pack<D>(a, slot, b, u0 + rel * P, min(P, nu - rel * P), (int)m.tile, di, pl)) return false;
+            if (FUSED && !ep.known && lane_id() == 0) early = ld_agent(slot + kSyncEpoch);
+            return true;
+        }
         m.row = dnb == 1 ? 0u : rel % dnb;
         m.grp = u.grp;
         m.sc = u.sc;
@@ -1103,7 +1208,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     auto compute_dn = [&](uint32_t k, DnItem& di, const ItemMeta& m) -> bool {
         if (!have_u) {
             if (!await_epoch(a, slot, ep, early)) return false;
-            U = a.core_count + ep.total;
+            U = column_rows<PACKED>(a, ep.total);
             have_u = true;
         }
         const int lane = lane_id();
@@ -1147,10 +1252,15 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         float acc[32];
 #pragma unroll
         for (int c = 0; c < 32; ++c) acc[c] = 0.f;
-        for (int r0 = 0; r0 < (int)G; r0 += kDnRows) {
-            if (r0) dn_issue<D>(m.grp, m.sc, m.hrow, (int)G, (int)m.tile, r0, a.seq, di);
-            if (!dn_wait_h(a, slot, m.hrow, (int)G, r0, di)) return false;
+        if constexpr (PACKED) {
+            if (!wait_h_lanes(a, slot, pl.hp, di.h)) return false;
             dn_accumulate(di, hs, ss, acc);
+        } else {
+            for (int r0 = 0; r0 < (int)G; r0 += kDnRows) {
+                if (r0) dn_issue<D>(m.grp, m.sc, m.hrow, (int)G, (int)m.tile, r0, a.seq, di);
+                if (!dn_wait_h(a, slot, m.hrow, (int)G, r0, di)) return false;
+                dn_accumulate(di, hs, ss, acc);
+            }
         }
         float cs[4];
         dn_reduce(acc, cs);
@@ -1163,7 +1273,14 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         for (int i = 0; i < 4; ++i) cs[i] = red[col0 + kTileColOff[i]];
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         add_columns(a, slot, yacc, (int)(m.row * D + m.tile * kDnCols) + col0, cs, U, pd);
-        if (a.executions) count_execution(a, slot, m.unit, m.dest, T * dnb);
+        if (a.executions) {
+            if constexpr (PACKED) {   // every unit of the pack: its first row's lane counts it
+                if (pl.lead && add_agent(slot + kSyncUnits + pl.unit * kLine, 1u) == T - 1)
+                    __hip_atomic_fetch_add(a.executions + pl.dest, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            } else {
+                count_execution(a, slot, m.unit, m.dest, T * dnb);
+            }
+        }
         if (k == KG) stamp(a, kStampDnComputed);
         return true;
     };
@@ -1653,7 +1770,7 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     auto compute_dn = [&](uint32_t k, u32x4* sl, const ItemMeta& m) -> bool {
         if (!have_u) {
             if (!await_epoch(a, slot, ep, early)) return false;
-            U = a.core_count + ep.total;
+            U = column_rows<false>(a, ep.total);
             have_u = true;
         }
         // the first look at h goes out first (a quarter is dequantised while it travels)
@@ -1884,9 +2001,15 @@ __device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uin
 // which its four waves share. Every range goes through the one call of
 // process_items below, so the item loop exists once in the kernel's code (one copy per
 // range kind would triple the code and raise the register count).
-template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, bool STAGED>
+// Item walks of the persistent kernels: plain (one item in flight per wave, in registers),
+// staged (64-neuron groups at batch 1: items staged through LDS slots), packed (groups of at
+// most 32 neurons at batch 1: the plain walk with down items over packs of core units).
+enum Walk : int { kWalkPlain = 0, kWalkStaged = 1, kWalkPacked = 2 };
+
+template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, int WALK>
 __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, u32x4* stage,
                                        uint32_t* slot) {
+    constexpr bool STAGED = WALK == kWalkStaged;
     const uint32_t W = QUEUE ? a.grid - 1 : a.grid;
     const uint32_t wave = wave_id();
     // Roles by workgroup: the first gu_wgs workgroups take the gate/up items, the others
@@ -1975,13 +2098,14 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
                 ok = process_items_staged<D, FUSED>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r, first);
                 first.valid = false;   // only the resident range's first batch is prefetched
             } else {
-                ok = process_items<D, FUSED, NB>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd, u0, u1, r);
+                ok = process_items<D, FUSED, NB, WALK == kWalkPacked>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd,
+                                                                      u0, u1, r);
             }
         }
     }
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
     if (QUEUE) stamp(a, kStampQueueDone);
-    check_pending(a, pd, FUSED && ep.known && ep.ok ? a.core_count + ep.total : 0u);
+    check_pending(a, pd, FUSED && ep.known && ep.ok ? column_rows<WALK == kWalkPacked>(a, ep.total) : 0u);
     if (a.stamps) {
         drain_vmem();
         stamp(a, kStampDrained);
@@ -2089,48 +2213,48 @@ __device__ __forceinline__ MlpArgs with_hot(const MlpArgs& args, const uint16_t*
 
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_PARAMS) {
-    static_assert(!STAGED || NB == 1, "the staged walk serves batch 1");
+    static_assert(WALK == kWalkPlain || NB == 1, "the staged and packed walks serve batch 1");
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
+    __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
     if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         if (threadIdx.x < 64) await_workers(a, slot, a.grid - 1);
     } else {
         stamp(a, kStampEntry);
-        worker<D, true, true, true, NB, STAGED>(a, b, sh, xl, stage, slot);
+        worker<D, true, true, true, NB, WALK>(a, b, sh, xl, stage, slot);
         stamp(a, kStampExit);
         count_out(slot);
     }
 }
 
 // Split path, stage A: resident (core) units only; no queue, no conversion.
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(LS_HOT_PARAMS) {
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
-    worker<D, false, true, false, NB, STAGED>(a, b, sh, xl, stage, slot);
+    __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
+    worker<D, false, true, false, NB, WALK>(a, b, sh, xl, stage, slot);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(LS_HOT_PARAMS) {
     const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
-    __shared__ u32x4 stage[StageArea<STAGED, NB>::VECS];
+    __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
     if (blockIdx.x == a.grid - 1) {
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         return;
     }
-    worker<D, false, false, true, NB, STAGED>(a, b, sh, xl, stage, slot);
+    worker<D, false, false, true, NB, WALK>(a, b, sh, xl, stage, slot);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
@@ -2547,52 +2671,62 @@ namespace {
 
 struct Variant {
     int width;
-    // [0] batch 1, [1] batch 2 .. kMaxBatch, [2] batch 1 with 64-neuron groups (staged)
-    const void* fused[3];
-    const void* stage_a[3];
-    const void* stage_b[3];
+    // [0] batch 1, [1] batch 2 .. kMaxBatch, [2] batch 1 with 64-neuron groups (staged),
+    // [3] batch 1 with groups of at most 32 neurons (packed down items)
+    const void* fused[4];
+    const void* stage_a[4];
+    const void* stage_b[4];
     const void* reduce;
 };
 
 // Staged kernels exist only for the widths where they fit two workgroups per CU.
-template <int D, template <int, int, bool> class K>
+template <int D, template <int, int, int> class K>
 const void* staged_kernel() {
     if constexpr (staged_width(D))
-        return reinterpret_cast<const void*>(K<D, 1, true>::fn);
+        return reinterpret_cast<const void*>(K<D, 1, kWalkStaged>::fn);
     else
         return nullptr;
 }
 
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 struct FusedK {
-    static constexpr auto fn = &fused_layer_kernel<D, NB, STAGED>;
+    static constexpr auto fn = &fused_layer_kernel<D, NB, WALK>;
 };
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 struct StageAK {
-    static constexpr auto fn = &stage_a_kernel<D, NB, STAGED>;
+    static constexpr auto fn = &stage_a_kernel<D, NB, WALK>;
 };
-template <int D, int NB, bool STAGED>
+template <int D, int NB, int WALK>
 struct StageBK {
-    static constexpr auto fn = &stage_b_kernel<D, NB, STAGED>;
+    static constexpr auto fn = &stage_b_kernel<D, NB, WALK>;
 };
+
+template <int D, template <int, int, int> class K>
+void fill_family(const void* (&out)[4]) {
+    out[0] = reinterpret_cast<const void*>(K<D, 1, kWalkPlain>::fn);
+    out[1] = reinterpret_cast<const void*>(K<D, kMaxBatch, kWalkPlain>::fn);
+    out[2] = staged_kernel<D, K>();
+    out[3] = reinterpret_cast<const void*>(K<D, 1, kWalkPacked>::fn);
+}
 
 template <int D>
 Variant make_variant() {
-    return {D,
-            {reinterpret_cast<const void*>(&fused_layer_kernel<D, 1, false>),
-             reinterpret_cast<const void*>(&fused_layer_kernel<D, kMaxBatch, false>), staged_kernel<D, FusedK>()},
-            {reinterpret_cast<const void*>(&stage_a_kernel<D, 1, false>),
-             reinterpret_cast<const void*>(&stage_a_kernel<D, kMaxBatch, false>), staged_kernel<D, StageAK>()},
-            {reinterpret_cast<const void*>(&stage_b_kernel<D, 1, false>),
-             reinterpret_cast<const void*>(&stage_b_kernel<D, kMaxBatch, false>), staged_kernel<D, StageBK>()},
-            reinterpret_cast<const void*>(&reduce_kernel<D>)};
+    Variant v{};
+    v.width = D;
+    fill_family<D, FusedK>(v.fused);
+    fill_family<D, StageAK>(v.stage_a);
+    fill_family<D, StageBK>(v.stage_b);
+    v.reduce = reinterpret_cast<const void*>(&reduce_kernel<D>);
+    return v;
 }
 
 // Kernel family of a launch: 0 batch 1, 1 batch 2 .. kMaxBatch, 2 staged (batch 1,
-// 64-neuron groups, widths where two workgroups' slots fit a CU's LDS).
+// 64-neuron groups, widths where two workgroups' slots fit a CU's LDS), 3 packed (batch 1,
+// groups of at most 32 neurons).
 int family(int width, int batch, int group_size) {
     if (batch > 1) return 1;
-    return group_size == (int)kStagedGroup && staged_width(width) ? 2 : 0;
+    if (group_size == (int)kStagedGroup && staged_width(width)) return 2;
+    return group_size <= (int)kDnRows / 2 ? 3 : 0;
 }
 
 const Variant* find_variant(int width) {
@@ -2630,6 +2764,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     Bounds b = bounds;
     if (a.batch < 1 || a.batch > kMaxBatch) return hipErrorInvalidValue;
     const int nb = family(p.width, (int)a.batch, (int)a.group_size);
+    a.pack = nb == 3 ? kDnRows / a.group_size : 1u;   // units per down item (pack_units)
     // the persistent kernels' leading scalars (LS_HOT_PARAMS), then the argument blocks
     uint32_t grid = (uint32_t)p.workers + 1;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
