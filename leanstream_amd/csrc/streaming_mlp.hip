@@ -2510,9 +2510,10 @@ struct DenseDnLoad {
 };
 
 // Branch-free, so that the compiler can count the loads in flight and wait for exactly
-// one unit's: a position past the split re-reads the split's first unit, and an invalid
-// descriptor reads the partial-row buffer (at least 2048 d bytes, more than a group's
-// 96 d), both with ok = false. h rows >= batch are zero (cleared at bind).
+// one unit's: a position past the split, and an invalid descriptor, issue the same loads
+// at the first word of the h rows for every lane (one line per instruction instead of a
+// unit's 8 KB tile again; the h rows are not written by this kernel), with ok = false.
+// h rows >= batch are zero (cleared at bind).
 __device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b, uint32_t un, uint32_t u0,
                                                uint32_t u1, uint32_t c0, DenseDnLoad& L) {
     const uint32_t D = a.width, G = a.group_size, t = threadIdx.x;
@@ -2520,16 +2521,17 @@ __device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b
     const bool in = un < u1;
     const Unit u = resolve(a, b, a.core[in ? un : u0], (int)D);
     L.ok = in && u.ok;   // an invalid descriptor is reported by the gate/up kernel
-    const uint8_t* grp = u.ok ? u.grp : reinterpret_cast<const uint8_t*>(a.dpart);
-    const uint16_t* sc = u.ok ? u.sc : reinterpret_cast<const uint16_t*>(a.dpart);
+    const uint8_t* grp = L.ok ? u.grp : reinterpret_cast<const uint8_t*>(a.h16);
+    const uint16_t* sc = L.ok ? u.sc : a.h16;
     const uint32_t col = c0 + 8 * o;
+    const uint32_t on = L.ok ? 1u : 0u;   // 0: every lane reads the h rows' first word
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const uint32_t n = 4 * nq + r;
-        L.q[r] = *reinterpret_cast<const uint32_t*>(grp + (size_t)(n * 3 + 2) * (D / 2) + col / 2);
-        L.sb[r] = sc[(size_t)(n * 3 + 2) * (D / 128) + col / 128];
+        L.q[r] = *reinterpret_cast<const uint32_t*>(grp + on * ((size_t)(n * 3 + 2) * (D / 2) + col / 2));
+        L.sb[r] = sc[on * ((size_t)(n * 3 + 2) * (D / 128) + col / 128)];
     }
-    L.hv = *reinterpret_cast<const u32x2*>(a.h16 + (size_t)hr * a.slot_capacity * G + u.dest * G + 4 * hp);
+    L.hv = *reinterpret_cast<const u32x2*>(a.h16 + on * ((size_t)hr * a.slot_capacity * G + u.dest * G + 4 * hp));
 }
 
 // LDS position (in halves) of the 8-neuron granule gr of tile column col: rows of 64
