@@ -132,3 +132,34 @@ def test_streamed_layers_without_arrival_delay(torch_gpu):
         a.close()
         b.close()
         c.close()
+
+
+def test_full_decode_step_matches_oracle(torch_gpu):
+    """The whole streaming decode step of the C3 shape: 36 host-staged layers, every one
+    against the oracle, every destination executed once per layer."""
+    torch = torch_gpu
+    sc = synth.STREAMS["c3"]
+    layers = sc.layers
+    log(f"case: full streamed decode step {sc.name} layers={layers} arrivals on")
+    sd = StreamingDecode(sc, layers=layers)
+    try:
+        sd.run()
+        torch.cuda.synchronize()
+        assert sd.backend.status() == 0
+        ys = sd.y.cpu().numpy()
+        k = sd.cfg.active
+        worst = 0.0
+        for l in range(layers):
+            hl = sd.host_layer(l)
+            rows = synth.descriptors(hl.cfg, sd.ranks[l])
+            ref = oracle.layer(rows, k, hl.cache, hl.scales, hl.x, sd.cfg.width, sd.cfg.group_size, threads=8)
+            y = ys[l].astype(np.float64)
+            r = ref["y32"].astype(np.float64)
+            rel = np.linalg.norm(y - r) / max(np.linalg.norm(r), 1e-30)
+            mx = float(np.abs(y - r).max())
+            assert rel <= REL_L2 and mx <= MAX_ABS, (l, rel, mx)
+            worst = max(worst, rel)
+        log(f"  {layers} layers within tolerance, worst rel_l2 {worst:.3e}")
+        assert np.all(sd.executions.cpu().numpy() == layers)
+    finally:
+        sd.close()
