@@ -2642,27 +2642,51 @@ __device__ __forceinline__ void check_dense_queue(const MlpArgs& a, uint32_t* sl
 
 __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    if (blockIdx.x == 0) {
-        // the next launch's ring slot: its last user, the previous launch, has finished
-        // (stream order); this kernel runs in every dense launch, with or without core units
+    if (blockIdx.x == gridDim.x - 1) {
+        // The last block only clears the next launch's ring slot (its last user, the previous
+        // launch, has finished: stream order) and checks the layer's queue (a read of host
+        // memory), in parallel with the column blocks; this kernel runs in every dense
+        // launch, with or without core units.
         uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
         for (uint32_t i = threadIdx.x; i < a.slot_words; i += blockDim.x) st_agent(other + i, 0u);
         if (threadIdx.x == 0) check_dense_queue(a, slot);
+        finish_launch(a, slot);
+        return;
     }
-    const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * D + column
-    const uint32_t tk = idx / a.width, col = idx - tk * a.width;
-    float v = 0.f;
-    if (a.dsplits == kDenseSplits) {   // every split's load in flight at once
-        float p[kDenseSplits];
+    // four consecutive columns of one row per thread (width is a multiple of 256): every
+    // split's 16-byte load in flight
+    const uint32_t idx = 4 * (blockIdx.x * kThreads + threadIdx.x);   // row * D + column
+    if (idx < a.batch * a.width) {
+        const uint32_t tk = idx / a.width, col = idx - tk * a.width;
+        float4 v = {0.f, 0.f, 0.f, 0.f};
+        if (a.dsplits == kDenseSplits) {
+            float4 p[kDenseSplits];
 #pragma unroll
-        for (uint32_t s = 0; s < kDenseSplits; ++s) p[s] = a.dpart[((size_t)s * 32 + tk) * a.width + col];
+            for (uint32_t s = 0; s < kDenseSplits; ++s)
+                p[s] = *reinterpret_cast<const float4*>(a.dpart + ((size_t)s * 32 + tk) * a.width + col);
 #pragma unroll
-        for (uint32_t s = 0; s < kDenseSplits; ++s) v += p[s];
-    } else {
-        for (uint32_t s = 0; s < a.dsplits; ++s) v += a.dpart[((size_t)s * 32 + tk) * a.width + col];
+            for (uint32_t s = 0; s < kDenseSplits; ++s) {
+                v.x += p[s].x;
+                v.y += p[s].y;
+                v.z += p[s].z;
+                v.w += p[s].w;
+            }
+        } else {
+            for (uint32_t s = 0; s < a.dsplits; ++s) {
+                const float4 q = *reinterpret_cast<const float4*>(a.dpart + ((size_t)s * 32 + tk) * a.width + col);
+                v.x += q.x;
+                v.y += q.y;
+                v.z += q.z;
+                v.w += q.w;
+            }
+        }
+        if (a.y32) *reinterpret_cast<float4*>(a.y32 + idx) = v;
+        const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.x) |
+                            (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.y) << 16;
+        const uint32_t hi = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.z) |
+                            (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.w) << 16;
+        *reinterpret_cast<u32x2*>(a.y + idx) = u32x2{lo, hi};
     }
-    if (a.y32) a.y32[idx] = v;
-    a.y[idx] = __builtin_bit_cast(uint16_t, (_Float16)v);
     finish_launch(a, slot);
 }
 
@@ -2827,8 +2851,10 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
         a.dsplits = 0;   // nothing to sum: y = 0
     }
     if (e != hipSuccess) return e;
-    return hipLaunchKernel(reinterpret_cast<const void*>(&dense_reduce_kernel), dim3(a.batch * a.width / kThreads),
-                           dim3(kThreads), rargs, 0, stream);
+    // four columns per thread, plus one block for the ring slot and the queue check
+    return hipLaunchKernel(reinterpret_cast<const void*>(&dense_reduce_kernel),
+                           dim3((a.batch * a.width / 4 + kThreads - 1) / kThreads + 1), dim3(kThreads), rargs, 0,
+                           stream);
 }
 
 // ---------------------------------------------------------------------------------
