@@ -2112,6 +2112,13 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     }
 }
 
+// Words of a ring slot a launch uses: the per-unit execution counters (a line per unit from
+// kSyncUnits on) only with the optional execution counts. Clearing the rest cost a layer of
+// 1434 two-neuron groups 4 us: its slot is 367 KB.
+__device__ __forceinline__ uint32_t ring_words_used(const MlpArgs& a) {
+    return a.executions ? a.slot_words : (a.slot_words < kSyncUnits ? a.slot_words : kSyncUnits);
+}
+
 // The mirror workgroup: wave 0 mirrors the queue while waves 1..3 clear what the next
 // launch will use -- the other ring slot and the other accumulator buffer, both last
 // used by the previous launch (finished, by stream order).
@@ -2122,7 +2129,7 @@ __device__ __forceinline__ void run_mirror(const MlpArgs& a, uint32_t* slot, uin
     }
     const uint32_t t = threadIdx.x - 64, n = kThreads - 64;
     uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-    for (uint32_t i = t; i < a.slot_words; i += n) st_agent(other + i, 0u);
+    for (uint32_t i = t; i < ring_words_used(a); i += n) st_agent(other + i, 0u);
     unsigned long long* other_acc = a.yacc + (size_t)((a.seq + 1) & 1) * a.width * a.batch * kAccStride;
     for (uint32_t i = t; i < a.width * a.batch; i += n) st_agent_u64(other_acc + (size_t)i * kAccStride, 0ull);
 }
@@ -2648,7 +2655,7 @@ __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
         // memory), in parallel with the column blocks; this kernel runs in every dense
         // launch, with or without core units.
         uint32_t* other = a.sync + ((a.seq + 1) & 1) * a.slot_words;
-        for (uint32_t i = threadIdx.x; i < a.slot_words; i += blockDim.x) st_agent(other + i, 0u);
+        for (uint32_t i = threadIdx.x; i < ring_words_used(a); i += blockDim.x) st_agent(other + i, 0u);
         if (threadIdx.x == 0) check_dense_queue(a, slot);
         finish_launch(a, slot);
         return;
