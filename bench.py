@@ -14,6 +14,10 @@ Printed: one JSON line (rank 0). value = microseconds per layer in the back-to-b
 pipeline (HIP events on the launch stream around the timed steps, divided by steps).
 roofline.achieved = algorithmic bytes per layer / that per-layer time.
 
+The default run also times every other workload of the path with fewer steps (C1, C4 at
+batch 1 and 4, the Group2 Ministral-3 shape, C5 dense batch 32, and a few C3 decode steps),
+reported under "secondary" in the same JSON line.
+
 --workload c3 instead measures a streaming decode step: 36 layers of the d_model 1024
 shape whose 16 active groups per layer are staged from pinned host memory by SDMA
 copies as they arrive (exponential gaps of mean 5 us in rank order), each published
@@ -49,6 +53,8 @@ def parse():
     ap.add_argument("--isolated", type=int, default=100, help="isolated launches timed one by one")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="default c2 run only: skip the shorter back-to-back runs of the other workloads")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 5 plain 64 MiB device copies (counter calibration for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -150,38 +156,123 @@ def cpu_baseline(cfg, budget_s):
     }
 
 
+def decode_steps(sc, steps, warmup, **kw):
+    """`steps` timed decode steps of the streaming shape `sc` (after `warmup` untimed ones):
+    (arrival schedule, wall seconds per step, per-layer host times, per-group stamps)."""
+    import numpy as np
+    import torch
+
+    from leanstream_amd.streaming import StreamingDecode
+
+    sd = StreamingDecode(sc, **kw)
+    try:
+        for _ in range(warmup):
+            sd.run()
+        torch.cuda.synchronize()
+        walls, times, stamps = [], [], []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            t, st = sd.run()
+            walls.append(time.perf_counter() - t0)
+            times.append(t)
+            stamps.append(st)
+        assert sd.backend.status() == 0, sd.backend.status()
+        return sd.arrivals.copy(), np.array(walls), np.concatenate(times), np.concatenate(stamps)
+    finally:
+        sd.close()
+
+
+def timed_layer(cfg, steps, warmup, copies=0, table=None, isolated=0):
+    """One layer shape, every group resident and ready before launch: microseconds per layer
+    back to back (HIP events on the launch stream around `steps` launches that rotate over
+    `copies` copies of the layer, by default enough to exceed the Infinity Cache), then
+    `isolated` launches timed one by one on an otherwise idle GPU."""
+    import torch
+
+    from leanstream_amd.workload import DeviceLayer
+
+    active_bytes = cfg.active * cfg.group_bytes + cfg.active * cfg.scale_words * 2
+    copies = copies or max(2, math.ceil(1.5 * MALL_BYTES / active_bytes))
+    print(f"[bench] workload {cfg.name}: k={cfg.active} B_alg={cfg.algorithmic_bytes()} copies={copies}",
+          file=sys.stderr, flush=True)
+    layer = DeviceLayer(cfg, copies=copies, with_y32=False, diagnostics=False, offline_table=table)
+    try:
+        layer.seal_empty_queue(1)
+        stream = torch.cuda.current_stream()
+        for i in range(warmup):
+            layer.run_core(copy=i % copies, epoch=1)
+        torch.cuda.synchronize()
+        assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
+        print(f"[bench] warmup done, timing {steps} steps", file=sys.stderr, flush=True)
+        # back-to-back pipeline: events on the launch stream around the timed steps
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for i in range(steps):
+            layer.run_core(copy=i % copies, epoch=1)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        ms_total = start.elapsed_time(stop)
+        # isolated layers: one event pair per launch, idle GPU between launches
+        iso = []
+        for i in range(isolated):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            layer.run_core(copy=i % copies, epoch=1)
+            e1.record(stream)
+            e1.synchronize()
+            iso.append(e0.elapsed_time(e1) * 1000.0)
+        status = layer.backend.status()
+        candidate = layer.backend.last_candidate()
+        workers = layer.backend.max_workers
+    finally:
+        layer.close()
+    assert status == 0, f"device status {status}"
+    return {"us": ms_total * 1000.0 / steps, "ms_total": ms_total, "iso": iso, "copies": copies,
+            "active_bytes": active_bytes, "candidate": candidate, "workers": workers}
+
+
+# Shorter back-to-back runs of the other workloads, in the default run's JSON line:
+# (key, timed steps, warm-up steps); c3 in decode steps of 36 layers.
+SECONDARY = (("c1", 200, 20), ("c4", 200, 20), ("c4b4", 100, 10), ("g2", 200, 20), ("c5", 100, 10), ("c3", 5, 1))
+
+
+def secondary_workloads():
+    """Every other workload of the path, measured as its own bench line would (fewer steps)."""
+    from leanstream_amd import synth
+
+    out = {}
+    for key, steps, warmup in SECONDARY:
+        if key == "c3":
+            sc = synth.STREAMS["c3"]
+            print(f"[bench] streaming {sc.name}: {sc.layers} layers x {steps} steps", file=sys.stderr, flush=True)
+            _, walls, _, _ = decode_steps(sc, steps, warmup)
+            out[key] = {"workload": sc.name, "us_per_layer": round(float(walls.mean()) * 1e6 / sc.layers, 2),
+                        "steps": steps, "kind": "host-staged decode step, wall clock"}
+            continue
+        cfg = synth.CONFIGS[key]
+        r = timed_layer(cfg, steps, warmup)
+        gbs = cfg.algorithmic_bytes() / r["us"] / 1e3
+        out[key] = {"workload": cfg.name, "us_per_layer": round(r["us"], 3), "steps": steps,
+                    "algorithmic_bytes": cfg.algorithmic_bytes(), "achieved_GBps": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return out
+
+
 def streaming_bench(a):
     """C3: decode steps of 36 host-staged layers (HostStagingIO + SDMA copies + Runtime/LayerStep
     + the persistent consumer). A step's time is host wall clock around ls_stream_run (the
     call returns after the last layer's completion word and commit)."""
     import numpy as np
-    import torch
 
     from leanstream_amd import synth
-    from leanstream_amd.streaming import StreamingDecode
-    from leanstream_amd.workload import DeviceLayer
 
     sc = synth.STREAMS["c3"]
     steps, warmup = a.steps or 20, 2 if a.warmup is None else a.warmup
     print(f"[bench] streaming {sc.name}: {sc.layers} layers x {steps} steps", file=sys.stderr, flush=True)
 
     def run(**kw):
-        sd = StreamingDecode(sc, **kw)
-        try:
-            for _ in range(warmup):
-                sd.run()
-            torch.cuda.synchronize()
-            walls, times, stamps = [], [], []
-            for _ in range(steps):
-                t0 = time.perf_counter()
-                t, st = sd.run()
-                walls.append(time.perf_counter() - t0)
-                times.append(t)
-                stamps.append(st)
-            assert sd.backend.status() == 0, sd.backend.status()
-            return sd.arrivals.copy(), np.array(walls), np.concatenate(times), np.concatenate(stamps)
-        finally:
-            sd.close()
+        return decode_steps(sc, steps, warmup, **kw)
 
     arrivals, walls, times, stamps = run()
     us_layer = walls.mean() * 1e6 / sc.layers
@@ -198,20 +289,7 @@ def streaming_bench(a):
     staged = sc.layer.active * sc.layer.group_bytes
     print(f"[bench] no arrival delay: {us0:.1f} us/layer", file=sys.stderr, flush=True)
     # one layer of the shape with its groups resident in HBM (all ready before launch)
-    layer = DeviceLayer(sc.layer_config(0), copies=1, with_y32=False, diagnostics=False)
-    layer.seal_empty_queue(1)
-    for _ in range(20):
-        layer.run_core(epoch=1)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(200):
-        layer.run_core(epoch=1)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    resident_us = e0.elapsed_time(e1) * 1000.0 / 200
-    layer.close()
+    resident_us = timed_layer(sc.layer_config(0), 200, 20, copies=1)["us"]
     result = {
         "metric": "µs per host-staged sparse INT4 MLP layer (streaming decode step of 36 layers), batch 1",
         "value": round(us_layer, 2),
@@ -275,51 +353,13 @@ def main():
         return
     a.steps = 400 if a.steps is None else a.steps
     a.warmup = 50 if a.warmup is None else a.warmup
-    import torch
-
     from leanstream_amd import synth
-    from leanstream_amd.workload import DeviceLayer
 
     cfg = synth.CONFIGS[a.workload]
-    active_bytes = cfg.active * cfg.group_bytes + cfg.active * cfg.scale_words * 2
-    copies = a.copies or max(2, math.ceil(1.5 * MALL_BYTES / active_bytes))
     table = None if a.candidate is None else [[a.candidate]]
-    print(f"[bench] workload {cfg.name}: k={cfg.active} B_alg={cfg.algorithmic_bytes()} copies={copies}",
-          file=sys.stderr, flush=True)
-    layer = DeviceLayer(cfg, copies=copies, with_y32=False, diagnostics=False, offline_table=table)
-    layer.seal_empty_queue(1)
-    stream = torch.cuda.current_stream()
-    for i in range(a.warmup):
-        layer.run_core(copy=i % copies, epoch=1)
-    torch.cuda.synchronize()
-    assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
-    print(f"[bench] warmup done, timing {a.steps} steps", file=sys.stderr, flush=True)
-
-    # back-to-back pipeline: events on the launch stream around the timed steps
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for i in range(a.steps):
-        layer.run_core(copy=i % copies, epoch=1)
-    stop.record(stream)
-    torch.cuda.synchronize()
-    ms_total = start.elapsed_time(stop)
-    us_per_layer = ms_total * 1000.0 / a.steps
-
-    # isolated layers: one event pair per launch, idle GPU between launches
-    iso = []
-    for i in range(a.isolated):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        layer.run_core(copy=i % copies, epoch=1)
-        e1.record(stream)
-        e1.synchronize()
-        iso.append(e0.elapsed_time(e1) * 1000.0)
-    status = layer.backend.status()
-    candidate = layer.backend.last_candidate()
-    workers = layer.backend.max_workers
-    layer.close()
-    assert status == 0, f"device status {status}"
+    r = timed_layer(cfg, a.steps, a.warmup, copies=a.copies, table=table, isolated=a.isolated)
+    us_per_layer, ms_total, iso = r["us"], r["ms_total"], r["iso"]
+    copies, active_bytes, candidate, workers = r["copies"], r["active_bytes"], r["candidate"], r["workers"]
 
     balg = cfg.algorithmic_bytes()
     achieved = balg / us_per_layer / 1e3  # GB/s
@@ -360,6 +400,8 @@ def main():
             "traffic": traffic,
         },
     }
+    if a.workload == "c2" and a.candidate is None and not a.copies and not a.no_secondary:
+        result["secondary"] = secondary_workloads()
     if not a.no_cpu:
         try:
             result["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds)
