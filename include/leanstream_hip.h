@@ -56,7 +56,7 @@ typedef struct ls_hip_layer_buffers {
     const void* staging;
     const void* scales;
     void* hidden;
-    void* partial;
+    void* partial;            /* reserved, unused (the reduction accumulates in backend-owned fixed point) */
     void* y32;
     uint32_t* executions;
     uint64_t* first_compute;

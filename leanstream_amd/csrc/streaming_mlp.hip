@@ -1076,8 +1076,8 @@ struct ItemMeta {
     int n0, nvalid;
 };
 
-// This wave's items of units [u0, u1) (its share under `role`); the next item's loads
-// are issued before the current item is computed. Gate/up items never
+// This wave's items of units [u0, u1) (its share under `role`), one item in flight at a
+// time (a one-pass gate/up item in two halves at batch 1). Gate/up items never
 // wait for another wave; down items wait for their unit's h (after every gate/up item
 // of this wave), so every h is eventually published. With FUSED, the U-th contribution
 // of a column writes the output (U = core + queue units, learnt from the epoch word).

@@ -59,11 +59,10 @@ class StreamingDecode:
         k = cfg.active
         self.y32 = torch.empty(cfg.batch * d, dtype=torch.float32, device=dev)
         self.hidden = torch.zeros(k * cfg.batch * G, dtype=torch.int64, device=dev)
-        self.partial = torch.zeros(k * d, dtype=torch.float32, device=dev)
         self.executions = torch.zeros(k, dtype=torch.int32, device=dev)
         self.backend = NativeBackend()
         self.backend.bind(d, G, k, None, self.scales, physical_groups=L * n, cache_groups=0, staging=self.staging,
-                          staging_groups=n, queue_capacity=n, hidden=self.hidden, partial=self.partial, y32=self.y32,
+                          staging_groups=n, queue_capacity=n, hidden=self.hidden, y32=self.y32,
                           executions=self.executions, batch=cfg.batch)
         # per-layer rank, layout and arrival tables
         self.ranks = [synth.stream_rank(sc, l) for l in range(L)]

@@ -56,7 +56,6 @@ class DeviceLayer:
         # h of each destination row and batch row: fp32 bits in the low word, launch
         # sequence tag in the high word ([slot][batch][G])
         self.hidden = torch.zeros(self.slot_capacity * cfg.batch * G, dtype=torch.int64, device=dev)
-        self.partial = torch.zeros(self.slot_capacity * d, dtype=torch.float32, device=dev)
         self.executions = torch.zeros(self.slot_capacity, dtype=torch.int32, device=dev) if diagnostics else None
         self.queue = ReadyQueue(queue_capacity if queue_capacity else max(1, k))
         self.stamps = torch.zeros(4096 * 32, dtype=torch.int64, device=dev) if stamps else None
@@ -67,7 +66,7 @@ class DeviceLayer:
         self.backend = NativeBackend(offline_table)
         self.backend.bind(d, G, self.slot_capacity, self.cache, self.scales, physical_groups=copies * n,
                           cache_groups=copies * n, staging=self.cache, staging_groups=copies * n,
-                          queue_capacity=self.queue.capacity, hidden=self.hidden, partial=self.partial, y32=self.y32,
+                          queue_capacity=self.queue.capacity, hidden=self.hidden, y32=self.y32,
                           executions=self.executions, batch=cfg.batch, stamps=self.stamps,
                           claim_log=self.claim_log)
         torch.cuda.synchronize()

@@ -423,8 +423,8 @@ def test_rebinding_a_used_hidden_buffer(torch_gpu):
     n = cfg.groups
     layer.backend.bind(cfg.width, cfg.group_size, layer.slot_capacity, layer.cache, layer.scales,
                        physical_groups=2 * n, cache_groups=2 * n, staging=layer.cache, staging_groups=2 * n,
-                       queue_capacity=layer.queue.capacity, hidden=layer.hidden, partial=layer.partial,
-                       y32=layer.y32, executions=layer.executions)
+                       queue_capacity=layer.queue.capacity, hidden=layer.hidden, y32=layer.y32,
+                       executions=layer.executions)
     layer.run_core(copy=0, epoch=1)            # sequence 1 again, copy-0 data
     sync_and_check_status(torch, layer)
     ref = oracle_for(layer, layer.core_rows[0])
