@@ -2542,10 +2542,13 @@ __device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b
 }
 
 // LDS position (in halves) of the 8-neuron granule gr of tile column col: rows of 64
-// neurons, granules XOR-swizzled by bits 3..5 of the column so that the 8-byte writes of
-// one instruction (32 columns 8 apart) and the MFMA's 16-byte reads spread over the banks.
+// neurons (128 bytes, so every column starts on the same bank), granules XOR-swizzled by
+// (col ^ col >> 3) & 7: eight consecutive columns (the MFMA's 16-byte reads) take eight
+// different granule slots, and so do eight columns 8 apart (the 8-byte writes of one
+// instruction). Swizzling by bits 3..5 alone left the reads of eight consecutive columns on
+// one slot: a third more bank-conflict cycles in the down kernel (SQ_LDS_BANK_CONFLICT).
 __device__ __forceinline__ uint32_t dn_tile_pos(uint32_t col, uint32_t gr) {
-    return col * 64 + 8 * (gr ^ ((col >> 3) & 7));
+    return col * 64 + 8 * (gr ^ ((col ^ (col >> 3)) & 7));
 }
 
 // Down projection of 256 columns over one split of the units. Per unit the workgroup
