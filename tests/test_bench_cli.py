@@ -27,3 +27,23 @@ def test_secondary_workloads_name_known_configs():
     for key, steps, warmup in bench.SECONDARY:
         assert key in synth.CONFIGS or key in synth.STREAMS, key
         assert steps > 0 and warmup >= 0
+
+
+def test_a_failing_secondary_workload_does_not_lose_the_others(monkeypatch):
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    def fake_layer(cfg, steps, warmup, **kw):
+        if "llama70b" in cfg.name:
+            raise AssertionError("device status 1")
+        return {"us": 10.0}
+
+    def fake_decode(sc, steps, warmup, **kw):
+        raise RuntimeError("ETIMEDOUT")
+
+    monkeypatch.setattr(bench, "timed_layer", fake_layer)
+    monkeypatch.setattr(bench, "decode_steps", fake_decode)
+    out = bench.secondary_workloads()
+    assert set(out) == {k for k, _, _ in bench.SECONDARY}
+    assert "error" in out["c4"] and "error" in out["c4b4"] and "error" in out["c3"]
+    assert out["c1"]["us_per_layer"] == 10.0 and out["c5"]["us_per_layer"] == 10.0
