@@ -7,7 +7,8 @@ oracle: d = 256, 512 and 2048 beside the 1024, 4096 and 8192 of the named worklo
 - plain walk with 128-neuron groups (two 64-row passes per down tile);
 - packed walk (8-neuron groups: a down item spans the rows of 8 core units);
 - dense batched path (batch 32, bf16 x, matrix cores);
-- the ready queue (a third of the units resident, the rest published while the launch runs).
+- the ready queue (a third of the units resident, the rest published while the launch runs);
+- the split entry point (stage A, stage B, reduction) at batch 4, bit for bit the fused launch.
 
 Bars as in the other parity tests: relative L2 <= 1e-3 and max-abs <= 2e-2 on the fp32 output,
 the fp16 output the round-to-nearest of it, h per neuron, every descriptor executed once.
@@ -102,3 +103,37 @@ def test_queue_units_at_other_widths(torch_gpu, d, G):
         assert np.all(layer.executions.cpu().numpy()[:k] == 1)
     finally:
         layer.close()
+
+
+@pytest.mark.parametrize("d", [1024, 2048])
+def test_split_entry_point_at_batch_4_matches_fused(torch_gpu, d):
+    """The reference's three-launch split (stage A, stage B, reduction; candidate 4) at batch 4:
+    the same bits as the fused launch, resident-only and with a third of the units resident and
+    the rest published while stage B runs (integer column sums: entry-point independent)."""
+    torch = torch_gpu
+    cfg = config(d, 64, 4)
+    log(f"case: split entry point {cfg.name} k={cfg.active}")
+    out = {}
+    for name, table in (("fused", None), ("split", [[4]])):
+        layer = DeviceLayer(cfg, offline_table=table)
+        try:
+            layer.seal_empty_queue(1)
+            layer.run_core(epoch=1)
+            sync_and_check_status(torch, layer)
+            if table:
+                assert layer.backend.last_candidate() == 4
+            out[name, "core"] = (layer.y32.cpu().numpy().copy(), layer.y.cpu().numpy().copy())
+            assert np.all(layer.executions.cpu().numpy() == 1)
+            k = len(layer.logical)
+            layer.executions.zero_()
+            rows, _ = _queue_run(torch, layer, k // 3, MODE_PROGRESSIVE, "delayed", epoch=3)
+            out[name, "queue"] = (layer.y32.cpu().numpy().copy(), layer.y.cpu().numpy().copy())
+            assert np.all(layer.executions.cpu().numpy()[:k] == 1)
+            if name == "split":
+                check_rows(layer, rows, f"{cfg.name} split queue")
+        finally:
+            layer.close()
+    for run in ("core", "queue"):
+        for a, b in zip(out["fused", run], out["split", run]):
+            assert np.array_equal(a.view(np.uint32 if a.dtype == np.float32 else np.uint16),
+                                  b.view(np.uint32 if b.dtype == np.float32 else np.uint16)), run

@@ -2,7 +2,7 @@
 the same inputs: y (fp16) and the fp32 y bit for bit, and a clean status word, over calls
 in a row whose inputs shrink (a smaller width, then fewer groups), so that what one call
 leaves in the library's shared array cannot reach the next call's output; one of the layers
-has 8-neuron groups (the packed kernels)."""
+has 8-neuron groups (the packed kernels), one has four batch rows."""
 import numpy as np
 import pytest
 
@@ -53,9 +53,9 @@ def test_noalloc_layer_matches_enqueue(torch_gpu):
     torch = torch_gpu
     lib = _native.library()
     # (config, core groups): each call smaller than the one before; "g8" (8-neuron groups,
-    # d_model 1024) takes the packed kernels, whose down items span 8 units
+    # d_model 1024) takes the packed kernels, whose down items span 8 units; "c1b4" is batch 4
     g8 = synth.LayerConfig("sparse_int4_mlp_d1024_f4096_g8_a20", 1024, 4096, 0.20, group_size=8, seed=0x6808)
-    cases = [("c2", None), ("g8", None), ("c1", None), ("c1", 5)]
+    cases = [("c2", None), ("c1b4", None), ("g8", None), ("c1", None), ("c1", 5)]
     layers = {}
     for key, count in cases:
         cfg = g8 if key == "g8" else synth.CONFIGS[key]
