@@ -245,7 +245,7 @@ def test_modes_orders_and_entry_points_bit_exact(torch_gpu):
         assert np.array_equal(v, base), k
 
 
-@pytest.mark.parametrize("key", ["c1", "c2"])
+@pytest.mark.parametrize("key", ["c1", "c2", "c1b4"])
 def test_ready_pair_consumption_order(torch_gpu, key):
     """Candidate hip_fused_resident_pairs consumes the queue in LeanStream's ready pairs
     (backends/triton/persistent.py:59-90): static descriptor-index pairs (2w + 2kW, +1) when
