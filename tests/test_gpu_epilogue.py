@@ -2,7 +2,8 @@
 (LeanStream backends/triton/reduction.py:17-28) and its RMSNorm
 (examples/ministral/native/predictor_shared_input.cu:16-41) bit for bit against the oracle on
 the layer's own y, the flags carrying the enqueue's epoch and the bell counting launches;
-batch rows each normalized on their own, the flags released once per launch."""
+batch rows each normalized on their own, the flags released once per launch; also after a
+dense (batch 32, matrix-core) launch."""
 import numpy as np
 import pytest
 
@@ -18,7 +19,7 @@ def log(msg):
     print(msg, flush=True)
 
 
-@pytest.mark.parametrize("key", ["c2", "c1b4"])
+@pytest.mark.parametrize("key", ["c2", "c1b4", "c1d32"])
 def test_epilogue_publishes_hidden_and_rmsnorm(torch_gpu, key):
     torch = torch_gpu
     cfg = synth.CONFIGS[key]
