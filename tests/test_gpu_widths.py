@@ -6,7 +6,8 @@ oracle: d = 256, 512 and 2048 beside the 1024, 4096 and 8192 of the named worklo
 - plain walk at batch 4 (down tiles shared by the rows);
 - plain walk with 128-neuron groups (two 64-row passes per down tile);
 - packed walk (8-neuron groups: a down item spans the rows of 8 core units);
-- dense batched path (batch 32, bf16 x, matrix cores);
+- batch 2 and 3 on the batch-4 kernels;
+- dense batched path (batch 5 .. 32, bf16 x, matrix cores);
 - the ready queue (a third of the units resident, the rest published while the launch runs);
 - the split entry point (stage A, stage B, reduction) at batch 4, bit for bit the fused launch.
 
@@ -54,7 +55,8 @@ def check_rows(layer, rows, what):
 CASES = [(256, 64, 1), (512, 64, 1), (2048, 64, 1),       # staged walk
          (256, 64, 4), (512, 64, 4), (2048, 64, 4),       # plain walk, batch 4
          (1024, 128, 1), (2048, 128, 1),                  # plain walk, two-pass down tiles
-         (512, 8, 1), (2048, 8, 1)]                       # packed walk
+         (512, 8, 1), (2048, 8, 1),                       # packed walk
+         (1024, 64, 2), (1024, 64, 3), (8192, 64, 3)]     # batch 2 and 3 on the batch-4 kernels
 
 
 @pytest.mark.parametrize("d,G,batch", CASES)
@@ -73,10 +75,11 @@ def test_core_layer_at_every_width(torch_gpu, d, G, batch):
         layer.close()
 
 
-@pytest.mark.parametrize("d", [512, 2048])
-def test_dense_layer_at_other_widths(torch_gpu, d):
+@pytest.mark.parametrize("d,batch", [(512, 32), (2048, 32), (1024, 5), (1024, 19)])
+def test_dense_layer_at_other_widths(torch_gpu, d, batch):
+    """Other widths, and batches below 32 (rows >= batch of x16 and h16 are zero)."""
     torch = torch_gpu
-    cfg = config(d, batch=32, dense=True)
+    cfg = config(d, batch=batch, dense=True)
     log(f"case: dense layer {cfg.name} k={cfg.active}")
     layer = DeviceLayer(cfg)
     try:
