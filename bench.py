@@ -46,8 +46,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 400 layers; 20 decode steps for c3)")
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 50 layers; 2 decode steps for c3)")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c4b4", "c5", "c1d32", "c3", "g2"],
-                    help="c3: 36-layer streaming decode step staged from pinned host memory")
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c4", "c4b4", "c5", "c1d32", "c3", "g2",
+                                                          "chain", "c1chain"],
+                    help="c3: 36-layer streaming decode step staged from pinned host memory; chain / c1chain: "
+                         "36 distinct C2 / C1 layers chained through the epilogue in one launch")
+    ap.add_argument("--layers", type=int, default=36, help="layers per chain launch (chain workloads)")
+    ap.add_argument("--stamps", default=None, help="chain workloads: write per-layer phase stamps (.npy) here")
     ap.add_argument("--candidate", type=int, default=None, help="force a kernel candidate id (offline LUT of one entry)")
     ap.add_argument("--copies", type=int, default=0, help="layer copies to rotate over (0: enough to exceed 256 MB)")
     ap.add_argument("--isolated", type=int, default=100, help="isolated launches timed one by one")
@@ -232,6 +236,64 @@ def timed_layer(cfg, steps, warmup, copies=0, table=None, isolated=0):
             "active_bytes": active_bytes, "candidate": candidate, "workers": workers}
 
 
+def timed_chain(cfg, steps, warmup, layers=36, isolated=0, stamps=False):
+    """A decode step's MLP stack: `layers` distinct layers of one shape chained through the
+    epilogue (layer i's hidden state fp16(residual_i + y_i) is layer i + 1's residual, and its
+    RMSNorm times the layer's weight is layer i + 1's input), computed by one persistent
+    launch (ls_hip_enqueue_chain). `steps` launches back to back, HIP events on the launch
+    stream around them; microseconds per layer = elapsed / (steps * layers)."""
+    import torch
+
+    from leanstream_amd.workload import DeviceLayer
+
+    print(f"[bench] chain {cfg.name}: {layers} distinct layers per launch, B_alg/layer={cfg.algorithmic_bytes()}",
+          file=sys.stderr, flush=True)
+    layer = DeviceLayer(cfg, copies=layers, with_y32=False, diagnostics=False)
+    out = {}
+    try:
+        outputs = layer.chain_outputs(layers)
+        norm = layer.chain_norm_weights(layers)
+        blocks = layer.chain_layers(list(range(layers)), outputs, output32=False, norm=norm)
+        stream = torch.cuda.current_stream()
+        sid = stream.cuda_stream
+        for _ in range(warmup):
+            layer.backend.enqueue_chain(blocks, sid)
+        torch.cuda.synchronize()
+        assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
+        print(f"[bench] chain warmup done, timing {steps} launches", file=sys.stderr, flush=True)
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            layer.backend.enqueue_chain(blocks, sid)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        ms_total = start.elapsed_time(stop)
+        iso = []
+        for _ in range(isolated):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            layer.backend.enqueue_chain(blocks, sid)
+            e1.record(stream)
+            e1.synchronize()
+            iso.append(e0.elapsed_time(e1) * 1000.0)
+        if stamps:
+            w = layer.backend.chain_workers + 1
+            st = torch.zeros(layers * w * 4 * 32, dtype=torch.int64, device="cuda")
+            layer.backend.set_chain_stamps(st, layers)
+            layer.backend.enqueue_chain(blocks, sid)
+            torch.cuda.synchronize()
+            out["stamps"] = st.cpu().numpy().reshape(layers, w * 4, 32)
+            layer.backend.set_chain_stamps(None, 0)
+        status = layer.backend.status()
+        out["workers"] = layer.backend.chain_workers
+    finally:
+        layer.close()
+    assert status == 0, f"device status {status}"
+    out.update({"us": ms_total * 1000.0 / (steps * layers), "ms_total": ms_total, "iso": iso, "layers": layers})
+    return out
+
+
 # Shorter back-to-back runs of the other workloads, in the default run's JSON line:
 # (key, timed steps, warm-up steps); c3 in decode steps of 36 layers.
 SECONDARY = (("c1", 200, 20), ("c4", 200, 20), ("c4b4", 100, 10), ("g2", 200, 20), ("c5", 100, 10), ("c3", 5, 1))
@@ -346,6 +408,50 @@ def streaming_bench(a):
     print(json.dumps(result), flush=True)
 
 
+def chain_bench(a):
+    from leanstream_amd import synth
+
+    cfg = synth.CONFIGS["c2" if a.workload == "chain" else "c1"]
+    steps = 20 if a.steps is None else a.steps
+    warmup = 3 if a.warmup is None else a.warmup
+    r = timed_chain(cfg, steps, warmup, layers=a.layers, isolated=min(a.isolated, 20), stamps=bool(a.stamps))
+    if a.stamps:
+        import numpy as np
+
+        np.save(a.stamps, r["stamps"])
+    balg = cfg.algorithmic_bytes()
+    achieved = balg / r["us"] / 1e3
+    result = {
+        "metric": METRIC,
+        "value": round(r["us"], 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(r["ms_total"] / steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16-f32acc",
+        "data": "synthetic (seeded splitmix64 INT4 weights per layer, U(lo,hi) fp16 scales, N(0,1) fp16 x)",
+        "config": {
+            "workload": f"chain{a.layers}_{cfg.name}",
+            "layers_per_launch": a.layers,
+            "d_model": cfg.width,
+            "d_ffn": cfg.ffn,
+            "group_size": cfg.group_size,
+            "active_groups": cfg.active,
+            "batch": cfg.batch,
+            "algorithmic_bytes_per_layer": balg,
+            "chain_workers": r["workers"],
+            "isolated_launch_us_p50": round(percentile(r["iso"], 0.5), 2) if r["iso"] else None,
+        },
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -356,6 +462,9 @@ def main():
         return
     if a.workload == "c3":
         streaming_bench(a)
+        return
+    if a.workload in ("chain", "c1chain"):
+        chain_bench(a)
         return
     a.steps = 400 if a.steps is None else a.steps
     a.warmup = 50 if a.warmup is None else a.warmup

@@ -85,6 +85,35 @@ struct HipEpilogue {
     float norm_eps = 0.f;               // 0 .. 1
 };
 
+// One layer of a chain (HipBackend::enqueue_chain): a sequence of layers computed by one
+// persistent launch. Layer i's hidden state fp16(residual_i + fp16(y_i)) -- the epilogue's
+// publication (backends/triton/reduction.py:17-22) -- is handed over inside the grid: it is
+// layer i + 1's residual, and its input either as it is or as RMSNorm(hidden) * norm_weight
+// (the Ministral epilogue, examples/ministral/native/predictor_shared_input.cu:16-41). The
+// weights of later layers stream while earlier layers finish (no LeanStream C++
+// counterpart: the reference submits future layers ahead and gates each on an input-ready
+// epoch, docs/architecture.md:9, backends/triton/core.py:20-28). Device pointers; batch 1.
+struct HipChainLayer {
+    const ExecDesc* core = nullptr;     // device-visible core descriptors (resident groups)
+    const void* cache = nullptr;        // packed groups [cache_groups][64][3][d/2]
+    const void* staging = nullptr;      // optional packed groups [staging_groups][64][3][d/2]
+    const void* scales = nullptr;       // fp16 [physical_groups*64][3][d/128]
+    const void* input = nullptr;        // first layer: fp16 [d]; every later layer: nullptr
+    const void* residual = nullptr;     // first layer: optional fp16 [d] (nullptr: the input); later: nullptr
+    const void* norm_weight = nullptr;  // later layers: optional fp16 [d]: input = RMSNorm(previous hidden) * it
+    void* output = nullptr;             // fp16 y [d]
+    float* output32 = nullptr;          // optional fp32 y [d] (pre-rounding)
+    void* hidden = nullptr;             // optional fp16 [d]: fp16(residual + y)
+    uint32_t* hidden_flag = nullptr;    // optional: epoch (system release) once the layer is done
+    uint32_t* bell = nullptr;           // optional: += 1 after the flag
+    uint32_t core_count = 0;
+    uint32_t cache_groups = 0;
+    uint32_t staging_groups = 0;
+    uint32_t physical_groups = 0;
+    uint32_t epoch = 0;
+    float norm_eps = 0.f;               // 0 .. 1
+};
+
 class HipBackend {
 public:
     explicit HipBackend(KernelDecisionTable table = {});
@@ -99,6 +128,18 @@ public:
     ComputeBackend view();
     // Installs (or, with nullptr, removes) the epilogue of every later enqueue; after bind.
     int set_epilogue(const HipEpilogue*);
+    // `count` layers in one persistent launch on `stream` (a hipStream_t); layer i gets
+    // sequence last_seq() - count + 1 + i, and the completion word takes each layer's
+    // sequence as it finishes (complete() covers the last). ENOTSUP for a geometry without
+    // chain kernels (batch 1, 64-neuron groups, d 1024 or 4096), EBUSY while more than the
+    // record ring's worth of layers is in flight. No allocation, no synchronisation.
+    int enqueue_chain(const HipChainLayer* layers, uint32_t count, void* stream);
+    // Diagnostics: per-layer phase stamps of chains of at most `layers` layers
+    // ([layers][(chain_workers() + 1) * 4][32] u64, 100 MHz clock); nullptr removes them.
+    int set_chain_stamps(uint64_t* stamps, uint32_t layers);
+    uint32_t chain_workers() const;   // persistent worker workgroups of a chain launch (0: no chains)
+    uint32_t last_seq() const;        // sequence of the last enqueued layer
+    uint32_t done_seq() const;        // the completion word: sequence of the last finished layer
 
     // Latest caller-supplied selector state (layer is overwritten per enqueue).
     KernelRuntimeState state{};

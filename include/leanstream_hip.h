@@ -103,6 +103,44 @@ typedef struct ls_hip_epilogue {
     float norm_eps;
 } ls_hip_epilogue;
 int ls_hip_set_epilogue(void* backend, const ls_hip_epilogue* epilogue);
+/* ---- layer chains ----
+ * Identical to leanstream::runtime::HipChainLayer. A sequence of layers computed by one persistent
+ * launch (batch 1, 64-neuron groups, width 1024 or 4096). Layer i's hidden state
+ * fp16(residual_i + y_i) -- the epilogue's publication (backends/triton/reduction.py:17-22) -- is
+ * handed over inside the grid: it is layer i + 1's residual, and its input as it is or, with
+ * norm_weight, as RMSNorm(hidden) * norm_weight (examples/ministral/native/predictor_shared_input.cu:
+ * 16-41), so later layers' weights stream while earlier layers finish. No LeanStream C++
+ * counterpart: LeanStream submits future layers ahead and gates each on an input-ready epoch
+ * (docs/architecture.md:9, backends/triton/core.py:20-28). The first layer's input (and optional
+ * residual) is read as the stream finds it; every later layer's input and residual must be NULL,
+ * and the first layer's norm_weight NULL. Layer i gets sequence ls_hip_last_seq() - count + 1 + i;
+ * the completion word (ls_hip_done_seq) takes each layer's sequence once every wave is out of it,
+ * and then hidden_flag receives the epoch (system release) and bell += 1, unless a status bit is
+ * set. ls_hip_complete covers the whole chain. Returns EINVAL for an invalid block, ENOTSUP for a
+ * geometry without chain kernels, EBUSY while more than 1024 layers are in flight. */
+typedef struct ls_hip_chain_layer {
+    const ls_exec_desc* core;
+    const void* cache;
+    const void* staging;
+    const void* scales;
+    const void* input;
+    const void* residual;
+    const void* norm_weight;
+    void* output;
+    float* output32;
+    void* hidden;
+    uint32_t* hidden_flag;
+    uint32_t* bell;
+    uint32_t core_count, cache_groups, staging_groups, physical_groups, epoch;
+    float norm_eps;
+} ls_hip_chain_layer;
+int ls_hip_enqueue_chain(void* backend, const ls_hip_chain_layer* layers, uint32_t count, void* stream);
+/* Diagnostics: per-layer phase stamps of chains of at most `layers` layers,
+ * [layers][(ls_hip_chain_workers() + 1) * 4][32] u64 (100 MHz clock); NULL removes them. */
+int ls_hip_set_chain_stamps(void* backend, uint64_t* stamps, uint32_t layers);
+uint32_t ls_hip_chain_workers(void* backend);
+uint32_t ls_hip_last_seq(void* backend);
+uint32_t ls_hip_done_seq(void* backend);
 /* Down-projection items (256-column tiles) per unit: d / 256. */
 uint32_t ls_hip_slices(void* backend);
 /* Overrides the selected candidate's persistent worker count (0 = the candidate's own

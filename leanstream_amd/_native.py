@@ -44,6 +44,15 @@ class Epilogue(C.Structure):
                 ("norm_flag", p), ("bell", p), ("norm_eps", C.c_float)]
 
 
+class ChainLayer(C.Structure):
+    """ls_hip_chain_layer / HipChainLayer (include/leanstream/hip_backend.h)."""
+
+    _fields_ = [("core", p), ("cache", p), ("staging", p), ("scales", p), ("input", p), ("residual", p),
+                ("norm_weight", p), ("output", p), ("output32", p), ("hidden", p), ("hidden_flag", p), ("bell", p),
+                ("core_count", u32), ("cache_groups", u32), ("staging_groups", u32), ("physical_groups", u32),
+                ("epoch", u32), ("norm_eps", C.c_float)]
+
+
 class GroupLayout(C.Structure):
     """GroupLayout (include/leanstream/group_layout.h); file_offset = offset in the host store."""
 
@@ -78,6 +87,11 @@ _SIGNATURES = [
     ("ls_hip_clear_status", [p], None),
     ("ls_hip_set_spin_limit", [p, u64], None),
     ("ls_hip_set_epilogue", [p, p], C.c_int),
+    ("ls_hip_enqueue_chain", [p, p, u32, p], C.c_int),
+    ("ls_hip_set_chain_stamps", [p, p, u32], C.c_int),
+    ("ls_hip_chain_workers", [p], u32),
+    ("ls_hip_last_seq", [p], u32),
+    ("ls_hip_done_seq", [p], u32),
     ("ls_hip_slices", [p], u32),
     ("ls_hip_set_workers", [p, u32], None),
     ("ls_hip_select", [p, u32, u32], u32),

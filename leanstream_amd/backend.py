@@ -189,6 +189,40 @@ class NativeBackend:
         return self.lib.ls_hip_enqueue(self.context, layer, io_bucket, epoch, _ptr(x), _ptr(y), stream, _ptr(core),
                                        core_count, C.byref(queue.view), mode)
 
+    def try_enqueue_chain(self, layers, stream):
+        """ls_hip_enqueue_chain over a list of dicts with ls_hip_chain_layer's field names
+        (device tensors or integer addresses); returns the library's code."""
+        arr = (_native.ChainLayer * len(layers))()
+        for dst, src in zip(arr, layers):
+            for name, kind in _native.ChainLayer._fields_:
+                if name in src:
+                    v = src[name]
+                    setattr(dst, name, _ptr(v) if kind is _native.p else float(v) if kind is C.c_float else int(v))
+        return self.lib.ls_hip_enqueue_chain(self.context, arr, len(layers), stream)
+
+    def enqueue_chain(self, layers, stream):
+        rc = self.try_enqueue_chain(layers, stream)
+        if rc:
+            raise RuntimeError(f"Native enqueue_chain failed: {rc}")
+
+    def set_chain_stamps(self, stamps, layers):
+        rc = self.lib.ls_hip_set_chain_stamps(self.context, _ptr(stamps), layers)
+        if rc:
+            raise RuntimeError(f"Native set_chain_stamps failed: {rc}")
+        self._chain_stamps = stamps
+
+    @property
+    def chain_workers(self):
+        return int(self.lib.ls_hip_chain_workers(self.context))
+
+    @property
+    def last_seq(self):
+        return int(self.lib.ls_hip_last_seq(self.context))
+
+    @property
+    def done_seq(self):
+        return int(self.lib.ls_hip_done_seq(self.context))
+
     def complete(self, layer=0):
         return bool(self.lib.ls_hip_complete(self.context, layer))
 

@@ -106,6 +106,17 @@ int ls_hip_set_epilogue(void* p, const ls_hip_epilogue* e) {
     if (!p) return EINVAL;
     return backend(p)->set_epilogue(reinterpret_cast<const HipEpilogue*>(e));
 }
+int ls_hip_enqueue_chain(void* p, const ls_hip_chain_layer* layers, uint32_t count, void* stream) {
+    static_assert(sizeof(ls_hip_chain_layer) == sizeof(HipChainLayer), "chain layer block");
+    if (!p) return EINVAL;
+    return backend(p)->enqueue_chain(reinterpret_cast<const HipChainLayer*>(layers), count, stream);
+}
+int ls_hip_set_chain_stamps(void* p, uint64_t* stamps, uint32_t layers) {
+    return p ? backend(p)->set_chain_stamps(stamps, layers) : EINVAL;
+}
+uint32_t ls_hip_chain_workers(void* p) { return p ? backend(p)->chain_workers() : 0; }
+uint32_t ls_hip_last_seq(void* p) { return p ? backend(p)->last_seq() : 0; }
+uint32_t ls_hip_done_seq(void* p) { return p ? backend(p)->done_seq() : 0; }
 uint32_t ls_hip_slices(void* p) { return p ? backend(p)->slices() : 0; }
 void ls_hip_set_workers(void* p, uint32_t workers) {
     if (p) backend(p)->set_workers(workers);

@@ -5,6 +5,7 @@
 #include "leanstream/hip_backend.h"
 #include <hip/hip_runtime_api.h>
 #include <algorithm>
+#include <atomic>
 #include <cerrno>
 #include <cstring>
 #include "mlp_launch.h"
@@ -30,6 +31,19 @@ struct HipBackend::Impl {
     HipEpilogue epilogue{};
     bool has_epilogue = false;
     uint32_t last_seq = 0;       // sequence of the last enqueued launch (0: none)
+    // Layer chains (batch 1, 64-neuron groups, widths lsamd::chain_available): records in a
+    // pinned host ring and its device mirror (index seq % ring), the synchronisation block,
+    // the self-resetting accumulators [2][d] and the tagged hidden words [2][d].
+    lsamd::ChainRec* chain_host = nullptr;
+    lsamd::ChainRec* chain_dev = nullptr;
+    uint32_t* chain_sync = nullptr;
+    unsigned long long* chain_acc = nullptr;
+    uint32_t* chain_words = nullptr;
+    uint64_t* chain_stamps = nullptr;   // optional diagnostics [layers][grid * 4][32]
+    uint32_t chain_stamp_layers = 0;
+    int per_cu_chain = 0;
+    bool chain_needs_clear = false;
+    uint32_t chain_clear_seq = 0;       // sequence at the last clear of the tagged hidden words
     bool needs_clear = true;
     uint32_t seq = 0;
     int cus = 0, per_cu_fused = 0, per_cu_split = 0;
@@ -46,6 +60,19 @@ struct HipBackend::Impl {
         if (status) (void)hipHostFree(status);
         if (done) (void)hipHostFree(done);
         if (arrivals) (void)hipFree(arrivals);
+        if (chain_host) (void)hipHostFree(chain_host);
+        if (chain_dev) (void)hipFree(chain_dev);
+        if (chain_sync) (void)hipFree(chain_sync);
+        if (chain_acc) (void)hipFree(chain_acc);
+        if (chain_words) (void)hipFree(chain_words);
+        chain_host = nullptr;
+        chain_dev = nullptr;
+        chain_sync = nullptr;
+        chain_acc = nullptr;
+        chain_words = nullptr;
+        chain_stamps = nullptr;
+        chain_stamp_layers = 0;
+        per_cu_chain = 0;
         arrivals = nullptr;
         has_epilogue = false;
         sync = nullptr;
@@ -109,6 +136,21 @@ int HipBackend::bind(const HipLayerBuffers& b) {
         e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(rows), gs, &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
         e = hipErrorInvalidConfiguration;
+    // layer chains: the geometry of the staged batch-1 kernels
+    const bool chains = !dense && b.batch == 1 && b.group_size == 64 && lsamd::chain_available(static_cast<int>(b.width));
+    const uint32_t ring = lsamd::chain_ring();
+    if (e == hipSuccess && chains)
+        e = hipHostMalloc(reinterpret_cast<void**>(&p.chain_host), sizeof(lsamd::ChainRec) * ring,
+                          hipHostMallocCoherent | hipHostMallocMapped);
+    if (e == hipSuccess && chains) e = hipMalloc(&p.chain_dev, sizeof(lsamd::ChainRec) * ring);
+    if (e == hipSuccess && chains) e = hipMalloc(&p.chain_sync, sizeof(uint32_t) * lsamd::kChainSyncWords);
+    if (e == hipSuccess && chains) e = hipMalloc(&p.chain_acc, sizeof(long long) * 2 * b.width);
+    if (e == hipSuccess && chains) e = hipMalloc(&p.chain_words, sizeof(uint32_t) * 2 * b.width);
+    if (e == hipSuccess && chains) e = lsamd::chain_resident(static_cast<int>(b.width), &p.per_cu_chain);
+    if (e == hipSuccess && chains && p.cus * p.per_cu_chain < 2) e = hipErrorInvalidConfiguration;
+    if (e == hipSuccess && chains)
+        e = lsamd::clear_sync(p.chain_sync, lsamd::kChainSyncWords, p.chain_acc, 2 * b.width,
+                              reinterpret_cast<uint64_t*>(p.chain_words), b.width, nullptr);
     uint64_t* hbuf = static_cast<uint64_t*>(b.hidden ? b.hidden : p.owned_hidden);
     if (e == hipSuccess)
         e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * b.width * rows * lsamd::kAccStride, hbuf,
@@ -150,11 +192,117 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     slices_ = b.width / lsamd::kDnCols;
     max_workers_ = static_cast<uint32_t>(p.cus * p.per_cu_fused) - 1;
     p.needs_clear = false;
+    p.chain_needs_clear = false;
+    p.chain_clear_seq = 0;
     p.last_seq = 0;
     *p.done = 0;
     p.bound = true;
     return 0;
 }
+
+int HipBackend::enqueue_chain(const HipChainLayer* layers, uint32_t count, void* stream) {
+    Impl& p = *impl_;
+    if (!p.bound || !layers || !count) return EINVAL;
+    if (!p.chain_dev) return ENOTSUP;   // geometry without chain kernels
+    const uint32_t ring = lsamd::chain_ring();
+    if (count > ring / 2) return EINVAL;
+    for (uint32_t i = 0; i < count; ++i) {
+        const HipChainLayer& l = layers[i];
+        // the first layer reads its input; every later one takes the previous hidden state
+        if ((i == 0) != (l.input != nullptr) || (i && l.residual) || (!i && l.norm_weight)) return EINVAL;
+        if (!(l.norm_eps >= 0.f) || l.norm_eps > 1.f) return EINVAL;
+        if (!l.output || !l.cache || !l.scales || (l.core_count && !l.core) || (l.staging_groups && !l.staging))
+            return EINVAL;
+        if (l.core_count > p.buf.slot_capacity || !l.cache_groups || !l.physical_groups) return EINVAL;
+    }
+    auto hs = static_cast<hipStream_t>(stream);
+    hipError_t e = hipSuccess;
+    // Sequences of a chain are consecutive (tags of the hidden words). Before the launch
+    // sequence wraps, or once the tagged words could hold a tag from 32768 sequences back,
+    // everything tagged is cleared; after a failed launch the synchronisation block too.
+    const bool wrap = p.seq > UINT32_MAX - count - 1;
+    if (wrap || p.needs_clear) {
+        const uint32_t rows = 1;
+        e = lsamd::clear_sync(p.sync, 2 * p.slot_words, p.yacc, 2 * p.buf.width * rows * lsamd::kAccStride, p.base.hbuf,
+                              p.buf.slot_capacity * rows * p.buf.group_size, hs);
+        if (e != hipSuccess) return static_cast<int>(e);
+        p.needs_clear = false;
+        if (wrap) p.seq = 0;
+    }
+    if (status() || p.chain_needs_clear || wrap || p.seq + count - p.chain_clear_seq > lsamd::kChainClearPeriod) {
+        e = lsamd::clear_sync(p.chain_sync, lsamd::kChainSyncWords, p.chain_acc, 2 * p.buf.width,
+                              reinterpret_cast<uint64_t*>(p.chain_words), p.buf.width, hs);
+        if (e != hipSuccess) return static_cast<int>(e);
+        p.chain_needs_clear = false;
+        p.chain_clear_seq = p.seq;
+    }
+    const uint32_t seq0 = p.seq + 1;
+    // host ring: the records of sequences after the last completed layer are live
+    const uint32_t done = __atomic_load_n(p.done, __ATOMIC_ACQUIRE);
+    if (p.last_seq && static_cast<int32_t>(seq0 + count - 1 - done) > static_cast<int32_t>(ring)) return EBUSY;
+    for (uint32_t i = 0; i < count; ++i) {
+        const HipChainLayer& l = layers[i];
+        lsamd::ChainRec r{};
+        r.core = l.core;
+        r.cache = static_cast<const uint8_t*>(l.cache);
+        r.staging = static_cast<const uint8_t*>(l.staging);
+        r.scales = static_cast<const uint16_t*>(l.scales);
+        r.x = static_cast<const uint16_t*>(l.input);
+        r.residual = static_cast<const uint16_t*>(l.residual);
+        r.norm_weight = static_cast<const uint16_t*>(l.norm_weight);
+        r.norm_eps = l.norm_eps;
+        r.y = static_cast<uint16_t*>(l.output);
+        r.y32 = l.output32;
+        r.hidden = static_cast<uint16_t*>(l.hidden);
+        r.hidden_flag = l.hidden_flag;
+        r.bell = l.bell;
+        r.core_count = l.core_count;
+        r.cache_groups = l.cache_groups;
+        r.staging_groups = l.staging_groups;
+        r.physical_groups = l.physical_groups;
+        r.epoch = l.epoch;
+        r.seq = seq0 + i;
+        r.chained = i ? 1u : 0u;
+        p.chain_host[(seq0 + i) % ring] = r;
+    }
+    std::atomic_thread_fence(std::memory_order_release);
+    lsamd::ChainArgs c{};
+    c.host_recs = p.chain_host;
+    c.recs = p.chain_dev;
+    c.count = count;
+    c.csync = p.chain_sync;
+    c.hbuf = p.base.hbuf;
+    c.yacc = p.chain_acc;
+    c.xtag = p.chain_words;
+    c.status = p.status;
+    c.done = p.done;
+    c.stamps = count <= p.chain_stamp_layers ? p.chain_stamps : nullptr;
+    c.width = p.buf.width;
+    c.slot_capacity = p.buf.slot_capacity;
+    c.grid = static_cast<uint32_t>(p.cus * p.per_cu_chain);
+    c.spin_limit = spin_limit_;
+    e = lsamd::launch_chain(c, seq0 % ring, hs);
+    if (e != hipSuccess) {
+        p.chain_needs_clear = true;
+        return static_cast<int>(e);
+    }
+    p.seq = seq0 + count - 1;
+    p.last_seq = p.seq;
+    last_candidate_ = -1;
+    return 0;
+}
+
+int HipBackend::set_chain_stamps(uint64_t* stamps, uint32_t layers) {
+    Impl& p = *impl_;
+    if (!p.bound || !p.chain_dev) return EINVAL;
+    p.chain_stamps = layers ? stamps : nullptr;
+    p.chain_stamp_layers = stamps ? layers : 0;
+    return 0;
+}
+
+uint32_t HipBackend::chain_workers() const { return impl_->chain_dev ? static_cast<uint32_t>(impl_->cus * impl_->per_cu_chain) - 1 : 0; }
+uint32_t HipBackend::last_seq() const { return impl_->last_seq; }
+uint32_t HipBackend::done_seq() const { return impl_->done ? __atomic_load_n(impl_->done, __ATOMIC_ACQUIRE) : 0; }
 
 int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, void* stream, Span<ExecDesc> core,
                         DeviceExecQueue q, uint32_t epoch, ConsumerMode mode) {
@@ -249,7 +397,9 @@ bool HipBackend::consumes_queue() const { return !impl_->dense; }
 
 uint32_t HipBackend::status() const { return impl_->status ? __atomic_load_n(impl_->status, __ATOMIC_ACQUIRE) : 0; }
 void HipBackend::clear_status() {
-    if (impl_->status) __atomic_store_n(impl_->status, 0u, __ATOMIC_RELEASE);
+    // a failed chain launch may have left its synchronisation block dirty: the next chain
+    // launch clears it first
+    if (impl_->status && __atomic_exchange_n(impl_->status, 0u, __ATOMIC_ACQ_REL)) impl_->chain_needs_clear = true;
 }
 
 int HipBackend::submit(void* ctx, uint32_t layer, const void* input, void* output, void* stream, Span<ExecDesc> core,

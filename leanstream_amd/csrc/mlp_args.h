@@ -79,6 +79,82 @@ enum StampPhase : uint32_t {
     kStampExit = 31,
 };
 
+// ---------------------------------------------------------------------------------
+// Layer chains (chain_mlp.hip): one persistent launch computes a sequence of layers whose
+// records the host writes into pinned memory. Layer i publishes its hidden state
+// fp16(residual_i + fp16(y_i)) (the epilogue's publication) as tagged words inside the grid;
+// layer i + 1 takes it as its residual and, as its input, either the hidden state itself or
+// its RMSNorm times the layer's norm weight. A wave streams the items of later layers into
+// its LDS slots while earlier layers finish, and waits for a layer's input only before its
+// first computation.
+// ---------------------------------------------------------------------------------
+struct ChainRec {                 // one layer; 128 bytes (whole lines), 32 words
+    const ExecDesc* core;         // words 0-1: core descriptors (device-visible)
+    const uint8_t* cache;         // 2-3
+    const uint8_t* staging;       // 4-5
+    const uint16_t* scales;       // 6-7
+    const uint16_t* x;            // 8-9: fp16 [d] input of a layer that is not chained
+    const uint16_t* residual;     // 10-11: fp16 [d] residual of a layer that is not chained (null: x)
+    const uint16_t* norm_weight;  // 12-13: chained layer: input = RMSNorm(previous hidden) * weight
+    uint16_t* y;                  // 14-15: fp16 [d]
+    float* y32;                   // 16-17: optional fp32 [d]
+    uint16_t* hidden;             // 18-19: optional fp16 [d]: fp16(residual + y)
+    uint32_t* hidden_flag;        // 20-21: optional: epoch (system release) once the layer is done
+    uint32_t* bell;               // 22-23: optional: += 1 after the flag
+    uint32_t core_count;          // 24
+    uint32_t cache_groups;        // 25
+    uint32_t staging_groups;      // 26
+    uint32_t physical_groups;     // 27
+    uint32_t epoch;               // 28
+    uint32_t seq;                 // 29: sequence of the layer (h tags, hidden-word tags, done word)
+    uint32_t chained;             // 30: 1 = the input comes from the previous layer's hidden state (seq - 1)
+    float norm_eps;               // 31
+};
+static_assert(sizeof(ChainRec) == 128, "a chain record is one 128-byte line");
+constexpr uint32_t kChainRecWords = 32;
+
+// Chain synchronisation block (device memory, kChainSyncWords words; zero between launches).
+constexpr uint32_t kChainMaxLayers = 512;   // layers of one launch
+enum ChainWord : uint32_t {
+    kChainAvail = 1 * kLine,      // records mirrored into the device ring
+    kChainLayersDone = 2 * kLine, // layers of the launch whose waves have all counted out
+    // kSyncAbort as in a ring slot
+    kChainExit = 8 * kLine,       // + (layer * 8 + g) * kLine: waves of workgroups blk % 8 == g out of the layer
+};
+constexpr uint32_t kChainSyncWords = kChainExit + kChainMaxLayers * 8 * kLine;
+
+struct ChainArgs {
+    const ChainRec* host_recs;    // pinned host memory: records of the launch
+    ChainRec* recs;               // device copy (the supervisor mirrors the records)
+    uint32_t count;               // layers of the launch
+    uint32_t* csync;              // chain synchronisation block
+    uint64_t* hbuf;               // tagged h [slot_capacity][64] (seq << 32 | fp32 bits)
+    unsigned long long* yacc;     // [2][d] fixed-point accumulators, buffer seq & 1; the lane that
+                                  // completes a column resets its word
+    uint32_t* xtag;               // [2][d] hidden words fp16 | tag << 16, buffer seq & 1
+    uint32_t* status;             // host-coherent sticky status word
+    uint32_t* done;               // host-coherent: sequence of the last layer whose waves all counted out
+    uint64_t* stamps;             // optional [count][grid * 4][kStampSlots]
+    uint32_t width;
+    uint32_t slot_capacity;
+    uint32_t grid;                // workers + the supervisor
+    uint64_t spin_limit;
+};
+// Hidden-word tag of a sequence: never 0, period 65535. The backend clears the tagged words
+// at least every 32768 sequences, so no stored tag can match a later sequence.
+constexpr uint32_t chain_tag(uint32_t seq) { return seq % 0xFFFFu + 1u; }
+constexpr uint32_t kChainClearPeriod = 32768;
+
+// Chain phase stamps (per layer and wave; kStampFirstData, kStampFirstDone, kStampHReady,
+// kStampDnComputed, kStampDrained as above).
+enum ChainStamp : uint32_t {
+    kChainStampIssue = 14,        // the wave's first item of the layer issued
+    kChainStampXWait = 15,        // the wave starts waiting for the layer's input
+    kChainStampXIn = 16,          // the wave's part of the input staged in LDS
+    kChainStampCountOut = 17,     // the wave counted out of the layer
+    kChainStampDone = 18,         // supervisor: every wave out of the layer
+};
+
 // Status word bits (host-coherent, sticky until cleared by the host).
 enum StatusBit : uint32_t {
     kStatusTimeout = 1u, kStatusQueueError = 2u, kStatusBadDescriptor = 4u, kStatusRange = 8u,

@@ -38,6 +38,12 @@ struct EpilogueArgs {
     uint32_t width, rows, epoch;
 };
 hipError_t launch_epilogue(const EpilogueArgs&, hipStream_t);
+// Layer chains (chain_mlp.hip): batch 1, 64-neuron groups, widths chain_available().
+bool chain_available(int width);
+uint32_t chain_ring();   // records in the host and device rings of a backend (index seq % ring)
+hipError_t chain_resident(int width, int* per_cu);
+// One persistent launch over args.count layers; `first` = the first layer's sequence % ring.
+hipError_t launch_chain(const ChainArgs& args, uint32_t first, hipStream_t stream);
 // Zeroes both ring slots, both accumulator buffers and the tagged h rows.
 hipError_t clear_sync(uint32_t* sync, uint32_t words, unsigned long long* yacc, uint32_t columns, uint64_t* hbuf,
                       uint32_t hwords, hipStream_t);

@@ -84,6 +84,60 @@ class DeviceLayer:
         s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
         self.backend.enqueue(layer, bucket, epoch, self.x, self.y, s, self.core_ptr(copy), self.k, self.queue, mode)
 
+    def chain_outputs(self, count):
+        """Per-layer output rows of a chain of `count` layers: y (fp16), y32, hidden (fp16)."""
+        torch = self.torch
+        d = self.cfg.width
+        return (torch.empty(count, d, dtype=torch.float16, device="cuda"),
+                torch.empty(count, d, dtype=torch.float32, device="cuda"),
+                torch.empty(count, d, dtype=torch.float16, device="cuda"))
+
+    def chain_norm_weights(self, count, seed=29, lo=0.05, hi=0.15):
+        """Per-layer RMSNorm weights (fp16 U(lo, hi), seeded) for a chain of `count` layers.
+        With random layer weights the layer output grows with the square of its input; inputs
+        of rms ~0.1 keep each layer's output small next to the residual stream, so the stream
+        of 36 layers stays bounded (with weights near 1 it grows past fp16 within six layers
+        of the Ministral-8B shape, in the oracle's arithmetic as on the GPU)."""
+        torch = self.torch
+        rng = np.random.default_rng(seed)
+        w = rng.uniform(lo, hi, (count, self.cfg.width)).astype(np.float16)
+        return torch.from_numpy(w).cuda()
+
+    def chain_layers(self, order, outputs, x=None, epoch0=1, flags=None, output32=True, norm=None, eps=1e-5,
+                     residual=None):
+        """ls_hip_chain_layer blocks of a chain whose layer i runs copy order[i] of this layer:
+        the first reads x (default self.x) and `residual` (default: x); every later one takes
+        the previous hidden state as its residual and as its input, or RMSNorm of it times
+        norm[i] (norm: [count, d] fp16 weights). flags: optional (flag address per layer, bell
+        address) host-coherent words."""
+        y, y32, hidden = outputs
+        n = self.cfg.groups
+        layers = []
+        for i, c in enumerate(order):
+            layer = dict(core=self.core_ptr(c), core_count=self.k, cache=self.cache, cache_groups=self.copies * n,
+                         scales=self.scales, physical_groups=self.copies * n, output=y[i], hidden=hidden[i],
+                         epoch=epoch0 + i, norm_eps=eps)
+            if output32:
+                layer["output32"] = y32[i]
+            if i == 0:
+                layer["input"] = self.x if x is None else x
+                if residual is not None:
+                    layer["residual"] = residual
+            elif norm is not None:
+                layer["norm_weight"] = norm[i]
+            if flags is not None:
+                layer["hidden_flag"] = flags[0] + 4 * i
+                layer["bell"] = flags[1]
+            layers.append(layer)
+        return layers
+
+    def copy_rows(self, copy):
+        """Host (numpy) cache and scales of one copy, and its descriptors relative to it."""
+        n = self.cfg.groups
+        cache = self.cache[copy * n * self.cfg.group_bytes:(copy + 1) * n * self.cfg.group_bytes].cpu().numpy()
+        scales = self.scales[copy * n * self.cfg.scale_words:(copy + 1) * n * self.cfg.scale_words].cpu().numpy()
+        return synth.descriptors(self.cfg, self.logical), cache, scales
+
     def hidden_h(self):
         """h per destination row and neuron (fp32) from the tagged hidden buffer."""
         words = self.hidden.cpu().numpy().view(np.uint32).reshape(-1, 2)[:, 0]

@@ -232,3 +232,22 @@ def test_compute_backend_view_commit_without_hook_is_unsupported():
         assert cb.complete(cb.context, 0)
     finally:
         lib.ls_hip_destroy(h)
+
+
+def test_chain_entry_points_refuse_without_gpu_work():
+    """ls_hip_enqueue_chain and its companions on an unbound backend: argument errors, no
+    launch; the ctypes block has the C layout."""
+    lib = _native.library()
+    assert C.sizeof(_native.ChainLayer) == 120
+    h = lib.ls_hip_create()
+    try:
+        layers = (_native.ChainLayer * 2)()
+        assert lib.ls_hip_enqueue_chain(h, layers, 2, None) == EINVAL     # unbound
+        assert lib.ls_hip_enqueue_chain(h, None, 1, None) == EINVAL
+        assert lib.ls_hip_enqueue_chain(h, layers, 0, None) == EINVAL
+        assert lib.ls_hip_enqueue_chain(None, layers, 1, None) == EINVAL
+        assert lib.ls_hip_set_chain_stamps(h, None, 0) == EINVAL
+        assert lib.ls_hip_chain_workers(h) == 0
+        assert lib.ls_hip_last_seq(h) == 0 and lib.ls_hip_done_seq(h) == 0
+    finally:
+        lib.ls_hip_destroy(h)
