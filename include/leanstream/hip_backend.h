@@ -72,7 +72,8 @@ struct HipLayerBuffers {
 // C++ counterpart; the Triton reduction's PUBLISH path, backends/triton/reduction.py:17-28,
 // and the Ministral RMSNorm, examples/ministral/native/predictor_shared_input.cu:16-41):
 // hidden = fp16(fp32 residual + fp32 y) per row, then optionally RMSNorm(hidden) * weight,
-// then the flags (system-scope release stores of the enqueue's epoch) and the bell.
+// then the flags (system-scope release stores of the enqueue's epoch) and the bell -- withheld
+// for a failed layer (a status bit set, or the queue's error word).
 // Device pointers, [batch][width] rows; the flags may be host-coherent words.
 struct HipEpilogue {
     const void* residual = nullptr;     // fp16 [batch][width]
@@ -141,6 +142,16 @@ public:
     uint32_t last_seq() const;        // sequence of the last enqueued layer
     uint32_t done_seq() const;        // the completion word: sequence of the last finished layer
 
+    // Optional orchestration at the consumer -> reduction boundary, as TritonBackend's
+    // (include/leanstream/triton_cuda.h:30-33, backends/triton/enqueue.cpp:33-36): enqueue
+    // calls arm_final_prediction(arm_context) and records b_done (a hipEvent_t, borrowed)
+    // between the split sequence's stage B and reduction launches, or right after a fused
+    // (or dense) launch, whose consumer and reduction are one kernel. A nonzero arm code is
+    // enqueue's return value; unlike the reference the reduction is still launched, so the
+    // launch completes and can be aborted like any other.
+    void* arm_context = nullptr;
+    int (*arm_final_prediction)(void*) = nullptr;
+    void* b_done = nullptr;
     // Latest caller-supplied selector state (layer is overwritten per enqueue).
     KernelRuntimeState state{};
     // Optional lifecycle hooks (as in the Triton backend): completion proof and cache
@@ -152,6 +163,9 @@ public:
     int (*install_cache)(void*, uint32_t, Span<GroupId>) = nullptr;
 
     uint32_t status() const;       // sticky device status bits (lsamd::StatusBit / LS_STATUS_*)
+    // The error a commit returns for the current status: 0 (no bit set), ETIMEDOUT (a bounded
+    // wait expired) or EIO (a descriptor, the queue or a value was rejected).
+    int status_error() const;
     void clear_status();
     void set_spin_limit_ticks(uint64_t ticks) { spin_limit_ = ticks; }
     uint32_t slices() const { return slices_; }

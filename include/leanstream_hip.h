@@ -84,13 +84,22 @@ int ls_hip_compute_backend(void* backend, void* out_compute_backend, uint64_t ou
 uint32_t ls_hip_status(void* backend);
 void ls_hip_clear_status(void* backend);
 void ls_hip_set_spin_limit(void* backend, uint64_t ticks_100mhz);
+/* TritonBackend::arm_context / arm_final_prediction / b_done (include/leanstream/triton_cuda.h:30-33):
+ * every later enqueue calls arm(context) and records b_done (a hipEvent_t, may be NULL) at the
+ * consumer -> reduction boundary -- between the split sequence's stage B and reduction launches,
+ * after a fused or dense launch. A nonzero arm code is returned by the enqueue, whose launch is
+ * nevertheless whole (the reduction runs, the completion word comes). NULL arm and b_done
+ * remove the hook. EINVAL for a NULL backend. */
+int ls_hip_set_stage_hook(void* backend, int (*arm)(void*), void* context, void* b_done);
 /* Identical to leanstream::runtime::HipEpilogue (include/leanstream/hip_backend.h): the layer
  * epilogue run after every later enqueue on the same stream -- hidden = fp16(residual + y)
  * (the Triton reduction's PUBLISH path, backends/triton/reduction.py:17-28), optionally
  * RMSNorm(hidden) * norm_weight (examples/ministral/native/predictor_shared_input.cu:16-41),
  * then hidden_flag / norm_flag receive the enqueue's epoch (system-scope release) and
- * bell += 1. The completion word of the layer does not cover the epilogue: readers of
- * hidden wait on the flags. NULL removes it. EINVAL for an unbound backend or an
+ * bell += 1. A failed layer -- its launch raised a status bit (sticky until
+ * ls_hip_clear_status) or its queue's error word is set -- gets its rows written but neither
+ * flag nor the bell. The completion word of the layer does not cover the epilogue: readers
+ * of hidden wait on the flags. NULL removes it. EINVAL for an unbound backend or an
  * inconsistent block. */
 typedef struct ls_hip_epilogue {
     const void* residual;

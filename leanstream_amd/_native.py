@@ -87,6 +87,7 @@ _SIGNATURES = [
     ("ls_hip_clear_status", [p], None),
     ("ls_hip_set_spin_limit", [p, u64], None),
     ("ls_hip_set_epilogue", [p, p], C.c_int),
+    ("ls_hip_set_stage_hook", [p, p, p, p], C.c_int),
     ("ls_hip_enqueue_chain", [p, p, u32, p], C.c_int),
     ("ls_hip_set_chain_stamps", [p, p, u32], C.c_int),
     ("ls_hip_chain_workers", [p], u32),

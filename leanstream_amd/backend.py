@@ -13,6 +13,7 @@ from ._native import DeviceQueue, Epilogue, ExecDesc, LayerBuffers
 
 MODE_BATCH_COMPAT, MODE_PROGRESSIVE, MODE_AUTO = 0, 1, 2
 STATUS_TIMEOUT, STATUS_QUEUE_ERROR, STATUS_BAD_DESCRIPTOR, STATUS_RANGE, STATUS_QUEUE_UNCONSUMED = 1, 2, 4, 8, 16
+STAGE_ARM = C.CFUNCTYPE(C.c_int, C.c_void_p)   # int (*arm_final_prediction)(void*)
 QUEUE_CONTROL_BYTES = 128
 
 
@@ -178,6 +179,16 @@ class NativeBackend:
             self._epilogue = (e, residual, hidden, hidden_flag, norm_weight, norm_output, norm_flag, bell)
         if rc:
             raise RuntimeError(f"Native set_epilogue failed: {rc}")
+
+    def set_stage_hook(self, arm=None, b_done=None):
+        """ls_hip_set_stage_hook: `arm` (a Python callable returning an int, or None) runs at
+        the consumer -> reduction boundary of every later enqueue; `b_done` is a hipEvent_t
+        handle recorded there (or None)."""
+        fn = STAGE_ARM(lambda _ctx: int(arm())) if arm is not None else None
+        rc = self.lib.ls_hip_set_stage_hook(self.context, C.cast(fn, C.c_void_p) if fn else None, None, b_done)
+        if rc:
+            raise RuntimeError(f"Native set_stage_hook failed: {rc}")
+        self._stage_hook = fn   # kept alive while the library may call it
 
     def enqueue(self, layer, io_bucket, epoch, x, y, stream, core, core_count, queue, mode=MODE_PROGRESSIVE):
         rc = self.lib.ls_hip_enqueue(self.context, layer, io_bucket, epoch, _ptr(x), _ptr(y), stream, _ptr(core),

@@ -101,6 +101,15 @@ void ls_hip_clear_status(void* p) {
 void ls_hip_set_spin_limit(void* p, uint64_t ticks) {
     if (p) backend(p)->set_spin_limit_ticks(ticks);
 }
+int ls_hip_set_stage_hook(void* p, int (*arm)(void*), void* context, void* b_done) {
+    if (!p) return EINVAL;
+    HipBackend& b = *backend(p);
+    b.arm_final_prediction = arm;
+    b.arm_context = context;
+    b.b_done = b_done;
+    return 0;
+}
+
 int ls_hip_set_epilogue(void* p, const ls_hip_epilogue* e) {
     static_assert(sizeof(ls_hip_epilogue) == sizeof(HipEpilogue), "epilogue block");
     if (!p) return EINVAL;

@@ -349,7 +349,14 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(workers), entry};
     // Batch 5..32: the dense matrix-core path computes the core units (the queue is not
     // consumed: a dense layer's groups are all resident).
-    e = p.dense ? lsamd::launch_dense(a, p.bounds, hs) : lsamd::launch_layer(plan, a, p.bounds, hs);
+    lsamd::StageHook hook{arm_final_prediction, arm_context, static_cast<hipEvent_t>(b_done), 0};
+    lsamd::StageHook* hk = arm_final_prediction || b_done ? &hook : nullptr;
+    if (p.dense) {
+        e = lsamd::launch_dense(a, p.bounds, hs);
+        if (e == hipSuccess) e = lsamd::run_stage_hook(hk, hs);
+    } else {
+        e = lsamd::launch_layer(plan, a, p.bounds, hs, hk);
+    }
     last_candidate_ = static_cast<int>(c.id);
     if (e != hipSuccess) {
         p.needs_clear = true;  // a partial launch may have left a ring slot dirty
@@ -368,6 +375,8 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
         x.norm_flag = ep.norm_flag;
         x.bell = ep.bell;
         x.arrivals = p.arrivals;
+        x.status = p.status;
+        x.queue_error = &q.control->error;
         x.eps = ep.norm_eps;
         x.width = p.buf.width;
         x.rows = p.buf.batch;
@@ -375,7 +384,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
         e = lsamd::launch_epilogue(x, hs);
         if (e != hipSuccess) return static_cast<int>(e);
     }
-    return 0;
+    return hook.rc;   // the arm's code: the layer is launched whole either way
 }
 
 int HipBackend::set_epilogue(const HipEpilogue* ep) {
@@ -396,6 +405,10 @@ int HipBackend::set_epilogue(const HipEpilogue* ep) {
 bool HipBackend::consumes_queue() const { return !impl_->dense; }
 
 uint32_t HipBackend::status() const { return impl_->status ? __atomic_load_n(impl_->status, __ATOMIC_ACQUIRE) : 0; }
+int HipBackend::status_error() const {
+    const uint32_t st = status();
+    return !st ? 0 : st & lsamd::kStatusTimeout ? ETIMEDOUT : EIO;
+}
 void HipBackend::clear_status() {
     // a failed chain launch may have left its synchronisation block dirty: the next chain
     // launch clears it first
@@ -429,7 +442,7 @@ int HipBackend::commit(void* ctx, uint32_t layer, Span<GroupId> ids) {
     // was rejected, a value was out of range) produced no valid output: the layer is not
     // committed, so LayerStep::commit fails and the caller aborts the step. The bits stay
     // set until clear_status().
-    if (const uint32_t st = b.status()) return st & lsamd::kStatusTimeout ? ETIMEDOUT : EIO;
+    if (const int rc = b.status_error()) return rc;
     // Cache installation is application policy: without the application's hook the
     // backend cannot install anything and says so, as LeanStream's Triton backend does
     // (backends/triton/enqueue.cpp:45).

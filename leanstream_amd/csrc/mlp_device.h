@@ -135,8 +135,11 @@ __device__ __forceinline__ void stamp(const MlpArgs& a, uint32_t k) {
         a.stamps[(blockIdx.x * kWaves + (threadIdx.x >> 6)) * kStampSlots + k] = now_ticks();
 }
 
+// Error path only: the bit is ordered before everything the lane stores afterwards (its
+// count-out, a completion word), so a host that sees the launch complete sees the bit.
 __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, uint32_t bit) {
     __hip_atomic_fetch_or(a.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
     st_agent(slot + kSyncAbort, 1u);
 }
 

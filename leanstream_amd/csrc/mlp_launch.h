@@ -18,7 +18,20 @@ bool variant_available(int width);
 // family depends on the batch and, at batch 1, on the group size).
 hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
-hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t);
+// Host work at the boundary between the queue consumer and the reduction (LeanStream's
+// A -> B -> arm -> event -> reduction order, backends/triton/enqueue.cpp:33-36): the split
+// sequence runs it between its stage B and reduction launches; a fused launch, whose
+// consumer and reduction are one kernel, right after that launch. The arm's return code
+// lands in `rc`; the reduction is launched regardless, so the launch's completion word
+// still comes.
+struct StageHook {
+    int (*arm)(void*);
+    void* context;
+    hipEvent_t b_done;   // optional: recorded at the boundary
+    int rc;
+};
+hipError_t run_stage_hook(StageHook* hook, hipStream_t stream);
+hipError_t launch_layer(const LaunchPlan&, const MlpArgs&, const Bounds&, hipStream_t, StageHook* hook = nullptr);
 // Dense batched path (batch > kMaxBatch, core units only): gate/up -> down -> reduction.
 hipError_t launch_dense(const MlpArgs&, const Bounds&, hipStream_t);
 bool dense_available(int width);   // widths the dense (batch > kMaxBatch) path is compiled for
@@ -34,6 +47,8 @@ struct EpilogueArgs {
     uint32_t* norm_flag;          // optional: epoch, after hidden_flag
     uint32_t* bell;               // optional: +1 after the flags
     uint32_t* arrivals;           // device word, zero between launches (the last row block resets it)
+    const uint32_t* status;       // the backend's status word: set bits withhold the flags and the bell
+    const uint32_t* queue_error;  // optional: the launch's queue error word; nonzero withholds them too
     float eps;
     uint32_t width, rows, epoch;
 };

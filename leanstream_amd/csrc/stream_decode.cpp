@@ -79,6 +79,17 @@ struct StreamDecoder {
         return d.engine.poll(d.engine.context, lane);
     }
 
+    // The decoder's commit: this loop installs nothing into a cache (its groups stream every
+    // layer), so a layer commits unless its launch raised a status bit. An application
+    // install_cache hook on the backend still runs. The backend itself is left untouched:
+    // used through its own view after the decoder is gone, it refuses commits without the
+    // hook (ENOTSUP) as before.
+    static int streamed_commit(void* ctx, uint32_t layer, Span<GroupId> ids) {
+        auto& b = *static_cast<HipBackend*>(ctx);
+        if (const int rc = b.status_error()) return rc;
+        return b.install_cache ? b.install_cache(b.lifecycle_context, layer, ids) : 0;
+    }
+
     ~StreamDecoder() {
         runtime.reset();  // drains every layer
         io.reset();       // drains the copy pump
@@ -116,12 +127,11 @@ struct StreamDecoder {
         sc.group_bytes = s.group_bytes;
         sc.staging_stride = s.staging_stride;
         io.reset(new HostStagingIO(sc));
-        // This loop installs nothing into a cache at commit (its groups stream every layer);
-        // a backend without the application's hook would refuse the commit (ENOTSUP).
-        if (!backend->install_cache) backend->install_cache = [](void*, uint32_t, Span<GroupId>) { return 0; };
         ManagerConfig mc{n, s.qd, s.group_bytes, s.staging_stride, 512, static_cast<ConsumerMode>(s.mode)};
         mc.io_backend = io->backend();
-        runtime.reset(new Runtime(mc, backend->view(), s.layers));
+        ComputeBackend view = backend->view();
+        view.commit = streamed_commit;
+        runtime.reset(new Runtime(mc, view, s.layers));
         return 0;
     }
 
@@ -182,24 +192,30 @@ struct StreamDecoder {
         }
         if (done) mark(5);
         if (!rc && !done) rc = ETIMEDOUT;
-        // A launch whose device status is set (a bounded wait expired, a descriptor or the
-        // queue was rejected, a value was out of range) produced no valid output and may
-        // have signalled completion with workgroups still resident: the layer fails.
-        const uint32_t status = backend->status();
-        if (status) {
-            backend->clear_status();
-            if (!rc) rc = status & LS_STATUS_TIMEOUT ? ETIMEDOUT : EIO;
-        }
         if (!rc) {
+            // a launch that raised a status bit (a bounded wait expired, a descriptor or the
+            // queue was rejected, a value was out of range) produced no valid output: the
+            // commit refuses it
             rc = step.commit({});
             mark(6);
             if (!rc) return 0;
         }
-        // failure: wait until the launch stream has drained (every wait in the kernels is
-        // bounded), so no workgroup still reads the staging arena the next layer's copies
-        // will rewrite, then cancel and retire
-        (void)hipStreamSynchronize(static_cast<hipStream_t>(stream));
-        while (step.abort() == EBUSY && now_ns() < deadline + 5000000000ull) std::this_thread::yield();
+        // Failure. First cancel: the queue's error word lets workgroups still waiting for
+        // READY groups leave at once, and abort is EBUSY until the launch is complete. Then
+        // drain the launch stream (its epilogue), so nothing of this layer still reads the
+        // staging arena the next layer's copies rewrite. Only then read and clear the status
+        // bits: every bit this launch raised belongs to this layer, and the next one starts
+        // clean.
+        const uint64_t abort_deadline = now_ns() + 5000000000ull;
+        int aborted;
+        while ((aborted = step.abort()) == EBUSY && now_ns() < abort_deadline) std::this_thread::yield();
+        const hipError_t synced = hipStreamSynchronize(static_cast<hipStream_t>(stream));
+        if (aborted == EBUSY) (void)step.abort();   // the drained stream holds no workgroup
+        if (const int st = backend->status_error()) {
+            backend->clear_status();
+            if (!rc) rc = st;
+        }
+        if (synced != hipSuccess) return EIO;
         return rc;
     }
 };

@@ -842,7 +842,14 @@ hipError_t resident_workers(int width, int entry_point, int batch, int group_siz
     return e;
 }
 
-hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& bounds, hipStream_t stream) {
+hipError_t run_stage_hook(StageHook* hook, hipStream_t stream) {
+    if (!hook) return hipSuccess;
+    if (hook->arm) hook->rc = hook->arm(hook->context);
+    return hook->b_done ? hipEventRecord(hook->b_done, stream) : hipSuccess;
+}
+
+hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& bounds, hipStream_t stream,
+                        StageHook* hook) {
     const Variant* v = find_variant(p.width);
     if (!v || p.workers < 1) return hipErrorInvalidValue;
     MlpArgs a = args;
@@ -856,7 +863,8 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     void* kargs[] = {&a.x, &a.core, &a.cache, &a.scales, &slot, &a.core_count, &a.seq, &grid, &a, &b};
     if (p.entry_point == kEntryFused) {
         a.grid = grid;
-        return hipLaunchKernel(v->fused[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
+        const hipError_t e = hipLaunchKernel(v->fused[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
+        return e == hipSuccess ? run_stage_hook(hook, stream) : e;
     }
     hipError_t e = hipSuccess;
     if (a.core_count) {
@@ -868,6 +876,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     grid = (uint32_t)p.workers + 1;
     a.grid = grid;
     e = hipLaunchKernel(v->stage_b[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);
+    if (e == hipSuccess) e = run_stage_hook(hook, stream);
     if (e != hipSuccess) return e;
     void* rargs[] = {&a};
     return hipLaunchKernel(v->reduce, dim3(p.width * a.batch / kThreads), dim3(kThreads), rargs, 0, stream);
@@ -926,7 +935,10 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
 // fp16(weight * fp16(hidden * inverse)). Products and sums are not contracted into fused
 // multiply-adds, so the result is the oracle's bit for bit. The last row's workgroup to
 // finish publishes the flags with system-scope release stores: hidden_flag, then
-// norm_flag, then bell += 1.
+// norm_flag, then bell += 1 -- unless the layer failed: its launch raised a status bit (a
+// bounded wait expired, a descriptor or a value was rejected) or its queue carries an error
+// (the runtime cancelled the layer; the launch left early). Then y is not the layer's output:
+// the rows are written but nothing announces them.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
 #pragma clang fp contract(off)
@@ -974,6 +986,10 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
         last = before == e.rows - 1;
         if (last) {
             __hip_atomic_store(e.arrivals, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            // the launch before this one on the stream has finished: its status bits are final
+            if (__hip_atomic_load(e.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
+                (e.queue_error && __hip_atomic_load(e.queue_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)))
+                return;
             if (e.hidden_flag) __hip_atomic_store(e.hidden_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             if (e.norm_flag) __hip_atomic_store(e.norm_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             if (e.bell) (void)__hip_atomic_fetch_add(e.bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -983,7 +999,8 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
 
 hipError_t launch_epilogue(const EpilogueArgs& args, hipStream_t stream) {
     EpilogueArgs e = args;
-    if (!e.y || !e.residual || !e.hidden || !e.rows || !e.width || (e.norm_weight && !e.norm_out) || !e.arrivals)
+    if (!e.y || !e.residual || !e.hidden || !e.rows || !e.width || (e.norm_weight && !e.norm_out) || !e.arrivals ||
+        !e.status)
         return hipErrorInvalidValue;
     void* kargs[] = {&e};
     return hipLaunchKernel(reinterpret_cast<const void*>(&epilogue_kernel), dim3(e.rows), dim3(256), kargs, 0, stream);

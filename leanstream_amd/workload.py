@@ -18,7 +18,7 @@ def _check(rc, what):
 
 class DeviceLayer:
     def __init__(self, cfg, copies=1, logical=None, with_y32=True, diagnostics=True, queue_capacity=None,
-                 offline_table=None, stamps=False, claim_log=False):
+                 offline_table=None, stamps=False, claim_log=False, first_compute=False):
         import torch
 
         self.torch = torch
@@ -63,12 +63,15 @@ class DeviceLayer:
         # ranges), at most one range per queue position
         self.claim_log = (torch.zeros(self.queue.capacity * 4, dtype=torch.int32, device=dev) if claim_log
                           else None)
+        # first compute stamp of each destination row (100 MHz device clock)
+        self.first_compute = (torch.zeros(self.slot_capacity, dtype=torch.int64, device=dev) if first_compute
+                              else None)
         self.backend = NativeBackend(offline_table)
         self.backend.bind(d, G, self.slot_capacity, self.cache, self.scales, physical_groups=copies * n,
                           cache_groups=copies * n, staging=self.cache, staging_groups=copies * n,
                           queue_capacity=self.queue.capacity, hidden=self.hidden, y32=self.y32,
                           executions=self.executions, batch=cfg.batch, stamps=self.stamps,
-                          claim_log=self.claim_log)
+                          claim_log=self.claim_log, first_compute=self.first_compute)
         torch.cuda.synchronize()
 
     def core_ptr(self, copy):

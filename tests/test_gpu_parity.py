@@ -245,6 +245,82 @@ def test_modes_orders_and_entry_points_bit_exact(torch_gpu):
         assert np.array_equal(v, base), k
 
 
+def test_split_entry_point_core_before_queue(torch_gpu):
+    """The split entry point launches stage A (the resident core units) and then stage B (the
+    ready-queue consumer) on the stream: every destination gets a first-compute stamp, and
+    every queue destination's is at or after every core destination's -- A precedes B
+    (LeanStream tests/persistent_mlp_test.cu:49 asserts starts[i] >= starts[0]). y matches the
+    oracle."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1"]
+    log("case: split entry point, 6 core units then the queue, first-compute stamps")
+    layer = DeviceLayer(cfg, offline_table=[[4]], first_compute=True)
+    layer.executions.zero_()
+    layer.first_compute.zero_()
+    core_n = 6
+    rows, _ = _queue_run(torch, layer, core_n, MODE_PROGRESSIVE, "delayed", epoch=3)
+    assert layer.backend.last_candidate() == 4
+    starts = layer.first_compute.cpu().numpy()[:len(rows)]
+    core, queue = starts[:core_n], starts[core_n:]
+    log(f"  core stamps {core.min()}..{core.max()}, queue stamps {queue.min()}..{queue.max()}")
+    assert (core > 0).all() and (queue > 0).all()
+    assert queue.min() >= core.max()
+    assert np.all(layer.executions.cpu().numpy()[:len(rows)] == 1)
+    ref = oracle_for(layer, rows)
+    compare(layer.y32.cpu().numpy(), ref["y32"], "split entry point")
+    layer.close()
+
+
+@pytest.mark.parametrize("table", [None, [[4]]], ids=["fused", "split"])
+def test_stage_hook_arm_and_b_done(torch_gpu, table):
+    """TritonBackend's arm_final_prediction / b_done (include/leanstream/triton_cuda.h:30-33)
+    on the HIP backend: the arm runs once per enqueue and b_done is recorded on the launch's
+    stream between a start and an end event (between stage B and the reduction on the split
+    sequence, after the fused launch); a nonzero arm code is what the enqueue returns, while
+    the launch is whole and its y matches the oracle."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS["c1"]
+    log(f"case: stage hook, {'split' if table else 'fused'} entry point")
+    layer = DeviceLayer(cfg, offline_table=table)
+    calls = []
+    code = [0]
+
+    def arm():
+        calls.append(1)
+        return code[0]
+
+    start = torch.cuda.Event(enable_timing=True)
+    b_done = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    b_done.record()   # creates the event
+    torch.cuda.synchronize()
+    layer.backend.set_stage_hook(arm, b_done.cuda_event)
+    rows = synth.descriptors(cfg, layer.logical, source_kind=0, dest_base=0)
+    ref = oracle_for(layer, rows)
+    stream = torch.cuda.current_stream().cuda_stream
+    q = layer.queue
+    for epoch, want in ((3, 0), (4, 61)):
+        code[0] = want
+        q.write_descriptors(rows)
+        q.reset(epoch)
+        q.seal(len(rows))
+        for i in range(len(rows)):
+            q.publish(i)
+        start.record()
+        rc = layer.backend.try_enqueue(0, 0, epoch, layer.x, layer.y, stream, None, 0, q, MODE_PROGRESSIVE)
+        end.record()
+        torch.cuda.synchronize()
+        log(f"  epoch {epoch}: arm code {want}, enqueue rc {rc}, arm calls {len(calls)}")
+        assert rc == want
+        assert len(calls) == epoch - 2
+        assert layer.backend.last_candidate() == (4 if table else 1)
+        assert start.elapsed_time(b_done) >= 0 and b_done.elapsed_time(end) >= 0
+        assert layer.backend.complete() and layer.backend.status() == 0
+        compare(layer.y32.cpu().numpy(), ref["y32"], f"stage hook epoch {epoch}")
+    layer.backend.set_stage_hook(None, None)
+    layer.close()
+
+
 @pytest.mark.parametrize("key", ["c1", "c2", "c1b4"])
 def test_ready_pair_consumption_order(torch_gpu, key):
     """Candidate hip_fused_resident_pairs consumes the queue in LeanStream's ready pairs
