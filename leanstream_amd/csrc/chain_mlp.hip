@@ -91,8 +91,10 @@ __device__ bool chain_wait_records(const ChainArgs& c, const MlpArgs& a) {
     if (lane_id() == 0 && ld_agent(c.csync + kChainAvail) < c.count) {
         Waiter wt(c.spin_limit);
         while (ld_agent(c.csync + kChainAvail) < c.count) {
-            if (ld_agent(c.csync + kSyncAbort)) { ok = 0; break; }
-            if (wt.expired()) { raise_status(a, c.csync, kStatusTimeout); ok = 0; break; }
+            if (wt.due()) {
+                if (ld_agent(c.csync + kSyncAbort)) { ok = 0; break; }
+                if (wt.over()) { raise_status(a, c.csync, kStatusTimeout); ok = 0; break; }
+            }
             __builtin_amdgcn_s_sleep(2);
         }
     }
@@ -295,8 +297,12 @@ __device__ __forceinline__ bool chain_claim(ChainShared& sh, uint32_t s) {
 // 256 sums the squares of columns t, t + 256, ... in that order, the 256 sums meet in a
 // halving tree, inverse = 1 / sqrt(sum / d + eps), fp16 of h * inverse, then the fp16
 // product with the weight. Lane l's 16-byte word quads l + 64 m hold columns 4 l .. 4 l + 3
-// + 256 m, so the lane computes the sums of the norm's threads 4 l .. 4 l + 3 itself; the
-// raw row passes through the input area of LDS. Bit for bit the epilogue's result.
+// + 256 m, so the lane computes the sums of the norm's threads 4 l .. 4 l + 3 itself.
+// Bit for bit the epilogue's result, in fewer instructions: h is fp16, so h * h is exact in
+// fp32 and fma(h, h, sum) rounds once exactly where sum + h * h does; fma(h, inverse, -0)
+// is the rounded product itself (the -0 addend keeps a -0 product's sign); and the fp16
+// product of two fp16 values (v_pk_mul_f16) is the exact product rounded once, as the
+// epilogue's fp32 product rounded to fp16 is.
 template <int D>
 __device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerView& v, u32x4* xl, ChainShared& sh) {
 #pragma clang fp contract(off)
@@ -305,18 +311,21 @@ __device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerV
     constexpr int Q = D / 256;       // word quads (4 columns) per lane: l + 64 m
     static_assert(Xg::N % 64 == 0, "whole pieces per lane");
     const int l = lane_id();
-    u32x4 pc[PL];
     if (!v.chained) {
         const u32x4* src = reinterpret_cast<const u32x4*>(v.x);
+        u32x4 pc[PL];
 #pragma unroll
         for (int j = 0; j < PL; ++j) pc[j] = src[l + 64 * j];
+#pragma unroll
+        for (int j = 0; j < PL; ++j) xl[x_position<D>(l + 64 * j)] = pair_halves(pc[j]);
     } else {
         const uint32_t* words = c.xtag + (size_t)((v.seq - 1u) & 1u) * D;
         const uint32_t tag = chain_tag(v.seq - 1u);
-        u32x4 wt[PL];
-        if (v.norm_weight) {   // read-only: plain loads, in flight while the words are polled
+        u32x2 wt[Q];   // the weights of the lane's columns, as fp16 pairs (read-only: plain loads,
+                       // in flight while the words are polled)
+        if (v.norm_weight) {
 #pragma unroll
-            for (int j = 0; j < PL; ++j) wt[j] = reinterpret_cast<const u32x4*>(v.norm_weight)[l + 64 * j];
+            for (int m = 0; m < Q; ++m) wt[m] = reinterpret_cast<const u32x2*>(v.norm_weight)[l + 64 * m];
         }
         u32x4 q[Q];
         bool have[Q];
@@ -338,27 +347,20 @@ __device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerV
             if (wave_should_stop(a, c.csync, wtime)) return false;
             __builtin_amdgcn_s_sleep(1);
         }
-        // the raw row into the input area (fp16 column order)
-        uint32_t* raw = reinterpret_cast<uint32_t*>(xl);
+        // the lane's columns as fp16 pairs in column order: hv[m] = (4i, 4i + 1), (4i + 2, 4i + 3)
+        u32x2 hv[Q];
 #pragma unroll
-        for (int m = 0; m < Q; ++m) {
-            const u32x4 w = q[m];
-            *reinterpret_cast<u32x2*>(raw + 2 * (l + 64 * m)) =
-                u32x2{(w.x & 0xFFFFu) | (w.y << 16), (w.z & 0xFFFFu) | (w.w << 16)};
-        }
-        float inverse = 0.f;
+        for (int m = 0; m < Q; ++m)
+            hv[m] = u32x2{(q[m].x & 0xFFFFu) | (q[m].y << 16), (q[m].z & 0xFFFFu) | (q[m].w << 16)};
         if (v.norm_weight) {
             float sum[4] = {0.f, 0.f, 0.f, 0.f};   // the norm's threads 4 l + e
 #pragma unroll
             for (int m = 0; m < Q; ++m) {
-                const u32x4 w = q[m];
-                const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float h = (float)half_bits((uint16_t)ws[e]);
-                    const float sq = h * h;
-                    sum[e] = sum[e] + sq;
-                }
+                const h2 lo = as_h2(hv[m].x), hi = as_h2(hv[m].y);
+                sum[0] = __builtin_fmaf((float)lo.x, (float)lo.x, sum[0]);
+                sum[1] = __builtin_fmaf((float)lo.y, (float)lo.y, sum[1]);
+                sum[2] = __builtin_fmaf((float)hi.x, (float)hi.x, sum[2]);
+                sum[3] = __builtin_fmaf((float)hi.y, (float)hi.y, sum[3]);
             }
             *reinterpret_cast<float4*>(sh.partial + 4 * l) = float4{sum[0], sum[1], sum[2], sum[3]};
             __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its loads
@@ -367,39 +369,32 @@ __device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerV
 #pragma unroll
             for (int k = 32; k >= 1; k >>= 1) s2 = s2 + __shfl_xor(s2, k);
             const float total = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s2)));
-            inverse = 1.0f / __builtin_sqrtf(total / (float)D + v.eps);
+            const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + v.eps);
+            auto norm_pair = [&](uint32_t hw, uint32_t ww) -> uint32_t {
+                const h2 hp = as_h2(hw);
+                const h2 n{(_Float16)__builtin_fmaf((float)hp.x, inverse, -0.0f),
+                           (_Float16)__builtin_fmaf((float)hp.y, inverse, -0.0f)};
+                return __builtin_bit_cast(uint32_t, n * as_h2(ww));
+            };
+#pragma unroll
+            for (int m = 0; m < Q; ++m) hv[m] = u32x2{norm_pair(hv[m].x, wt[m].x), norm_pair(hv[m].y, wt[m].y)};
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        // Paired layout (pair_halves): piece p = quad i / 2 holds columns 8p .. 8p + 7 as
+        // (0,4)(1,5)(2,6)(3,7). Quads 2p and 2p + 1 sit on lanes 2k and 2k + 1 (same m): the
+        // even lane keeps halves 0,1 and takes 4,5 from its neighbour, the odd one keeps 6,7 and
+        // takes 2,3; each writes its half of the piece.
+        const bool odd = l & 1;
+        u32x2* xw = reinterpret_cast<u32x2*>(xl);
 #pragma unroll
-        for (int j = 0; j < PL; ++j) pc[j] = xl[l + 64 * j];   // raw pieces: columns 8 i .. 8 i + 7
-        if (v.norm_weight) {
-#pragma unroll
-            for (int j = 0; j < PL; ++j) {
-                const uint32_t hv[4] = {pc[j].x, pc[j].y, pc[j].z, pc[j].w};
-                const uint32_t wv[4] = {wt[j].x, wt[j].y, wt[j].z, wt[j].w};
-                uint32_t o[4];
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    uint32_t packed = 0;
-#pragma unroll
-                    for (int e = 0; e < 2; ++e) {
-                        float p = (float)half_bits((uint16_t)(hv[k] >> (16 * e))) * inverse;
-                        asm volatile("" : "+v"(p));   // the fp32 product, then fp16 (as the epilogue rounds)
-                        const float n = (float)(_Float16)p;
-                        const float w = (float)half_bits((uint16_t)(wv[k] >> (16 * e)));
-                        packed |= (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(w * n)) << (16 * e);
-                    }
-                    o[k] = packed;
-                }
-                pc[j] = u32x4{o[0], o[1], o[2], o[3]};
-            }
+        for (int m = 0; m < Q; ++m) {
+            const uint32_t got =
+                (uint32_t)__builtin_amdgcn_mov_dpp((int)(odd ? hv[m].x : hv[m].y), 0xB1, 0xF, 0xF, false);
+            const uint32_t lo = odd ? got : hv[m].x, hi = odd ? hv[m].y : got;
+            const uint32_t piece = (uint32_t)(l >> 1) + 32u * m;
+            xw[2 * x_position<D>(piece) + (odd ? 1 : 0)] =
+                u32x2{__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u)};
         }
-        // every raw piece of the wave is read (its LDS operations execute in order) before the
-        // paired pieces below overwrite them
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
-#pragma unroll
-    for (int j = 0; j < PL; ++j) xl[x_position<D>(l + 64 * j)] = pair_halves(pc[j]);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its count
     if (lane_id() == 0) __hip_atomic_fetch_add(&sh.xcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return true;
@@ -551,8 +546,10 @@ __device__ bool chain_wait_layers(const ChainArgs& c, const MlpArgs& a, uint32_t
     if (lane_id() == 0 && ld_agent(c.csync + kChainLayersDone) < layers) {
         Waiter wt(c.spin_limit);
         while (ld_agent(c.csync + kChainLayersDone) < layers) {
-            if (ld_agent(c.csync + kSyncAbort)) { ok = 0; break; }
-            if (wt.expired()) { raise_status(a, c.csync, kStatusTimeout); ok = 0; break; }
+            if (wt.due()) {
+                if (ld_agent(c.csync + kSyncAbort)) { ok = 0; break; }
+                if (wt.over()) { raise_status(a, c.csync, kStatusTimeout); ok = 0; break; }
+            }
             __builtin_amdgcn_s_sleep(2);
         }
     }
@@ -613,7 +610,12 @@ __device__ void chain_worker(const ChainArgs& c, uint32_t first, ChainShared& sh
         if (chain_wg_items<D>(blockIdx.x, role.nw, v.core_count)) {
             ++staged;
             if (chain_claim(sh, staged)) {
-                if (!(ok = chain_stage_x<D>(c, a, v, xl, sh))) break;
+                // every wave of the workgroup waits for this one: it takes the SIMD's issue
+                // slots ahead of the co-resident wave meanwhile
+                __builtin_amdgcn_s_setprio(3);
+                ok = chain_stage_x<D>(c, a, v, xl, sh);
+                __builtin_amdgcn_s_setprio(0);
+                if (!ok) break;
                 chain_stamp(c, i, kChainStampXIn);
             }
         }

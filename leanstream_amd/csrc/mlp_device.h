@@ -124,10 +124,27 @@ __device__ __forceinline__ void wait_vector_loads() {
 // ---------------------------------------------------------------------------------
 // bounded waiting
 // ---------------------------------------------------------------------------------
+// A bounded wait. The 100 MHz clock is a scalar memory read (s_memrealtime) whose latency
+// under a loaded memory system approaches a microsecond, and while one is in flight the
+// wave's next LDS access waits too (both count in lgkmcnt). So a wait reads the clock -- and
+// looks at its abort flag, where it has one -- only on every kWaitStride-th check (due()):
+// a wait that ends sooner reads neither, a long one pays one clock read per kWaitStride
+// polls. The bound runs from the first clock read.
+constexpr uint32_t kWaitStride = 16;
 struct Waiter {
-    uint64_t start, limit;
-    __device__ Waiter(uint64_t lim) : start(now_ticks()), limit(lim) {}
-    __device__ bool expired() const { return now_ticks() - start > limit; }
+    uint64_t start = 0, limit;
+    uint32_t n = 0;
+    __device__ explicit Waiter(uint64_t lim) : limit(lim) {}
+    __device__ bool due() { return (++n & (kWaitStride - 1u)) == 0u; }
+    __device__ bool over() {   // on a due check: has the bound passed?
+        const uint64_t t = now_ticks();
+        if (!start) {
+            start = t;
+            return false;
+        }
+        return t - start > limit;
+    }
+    __device__ bool expired() { return due() && over(); }
 };
 
 __device__ __forceinline__ void stamp(const MlpArgs& a, uint32_t k) {
@@ -143,14 +160,16 @@ __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, u
     st_agent(slot + kSyncAbort, 1u);
 }
 
-// Lane 0 of the wave checks whether a wait must be abandoned (abort flag or spin limit
-// exceeded; the latter raises the timeout status). Wave-uniform result.
-__device__ __forceinline__ bool wave_should_stop(const MlpArgs& a, uint32_t* slot, const Waiter& wt) {
+// Lane 0 of the wave checks, on a due check of the wait, whether it must be abandoned (abort
+// flag or spin limit exceeded; the latter raises the timeout status). Wave-uniform result:
+// every lane counts the same checks.
+__device__ __forceinline__ bool wave_should_stop(const MlpArgs& a, uint32_t* slot, Waiter& wt) {
+    if (!wt.due()) return false;
     uint32_t st = 0;
     if (lane_id() == 0) {
         if (ld_agent(slot + kSyncAbort)) {
             st = 1;
-        } else if (wt.expired()) {
+        } else if (wt.over()) {
             raise_status(a, slot, kStatusTimeout);
             st = 1;
         }
@@ -649,8 +668,10 @@ __device__ __forceinline__ bool await_epoch(const MlpArgs& a, uint32_t* slot, Ep
         asm volatile("" : "+v"(word) : : "memory");
         Waiter wt(a.spin_limit);
         while (!(word & 3u)) {
-            if (ld_agent(slot + kSyncAbort)) { word = 2; break; }
-            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); word = 2; break; }
+            if (wt.due()) {
+                if (ld_agent(slot + kSyncAbort)) { word = 2; break; }
+                if (wt.over()) { raise_status(a, slot, kStatusTimeout); word = 2; break; }
+            }
             __builtin_amdgcn_s_sleep(2);
             word = ld_agent(slot + kSyncEpoch);
         }
@@ -933,8 +954,10 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
         if (lane_id() == 0) {
             Waiter wt(a.spin_limit);
             while ((ready = ld_agent(slot + kSyncReady)) < need) {
-                if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
-                if (wt.expired()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+                if (wt.due()) {
+                    if (ld_agent(slot + kSyncAbort)) { ok = 0; break; }
+                    if (wt.over()) { raise_status(a, slot, kStatusTimeout); ok = 0; break; }
+                }
                 __builtin_amdgcn_s_sleep(1);
             }
         }
