@@ -14,9 +14,11 @@ Printed: one JSON line (rank 0). value = microseconds per layer in the back-to-b
 pipeline (HIP events on the launch stream around the timed steps, divided by steps).
 roofline.achieved = algorithmic bytes per layer / that per-layer time.
 
-The default run also times every other workload of the path with fewer steps (C1, C4 at
-batch 1 and 4, the Group2 Ministral-3 shape, C5 dense batch 32, and a few C3 decode steps),
-reported under "secondary" in the same JSON line.
+The default run also times the layer stack of a decode step as one launch per step (36
+distinct C2 layers, and 36 of C1, chained through the epilogue: "pipelined"), and every
+other workload of the path with fewer steps (C1, C4 at batch 1 and 4, the Group2
+Ministral-3 shape, C5 dense batch 32, and a few C3 decode steps: "secondary"), in the same
+JSON line.
 
 --workload c3 instead measures a streaming decode step: 36 layers of the d_model 1024
 shape whose 16 active groups per layer are staged from pinned host memory by SDMA
@@ -253,7 +255,8 @@ def timed_chain(cfg, steps, warmup, layers=36, isolated=0, stamps=False):
     try:
         outputs = layer.chain_outputs(layers)
         norm = layer.chain_norm_weights(layers)
-        blocks = layer.chain_layers(list(range(layers)), outputs, output32=False, norm=norm)
+        blocks = layer.backend.chain_blocks(layer.chain_layers(list(range(layers)), outputs, output32=False,
+                                                               norm=norm))
         stream = torch.cuda.current_stream()
         sid = stream.cuda_stream
         for _ in range(warmup):
@@ -323,6 +326,27 @@ def secondary_workloads():
                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
         except Exception as exc:  # noqa: BLE001 -- reported in the line, not fatal to it
             print(f"[bench] {key} failed: {exc!r}", file=sys.stderr, flush=True)
+            out[key] = {"error": repr(exc)[:300]}
+    return out
+
+
+def pipelined_workloads():
+    """The decode step's layer stack in one launch per step (ls_hip_enqueue_chain): 36 distinct
+    C2 layers and 36 distinct C1 layers chained through the epilogue (hidden state as the next
+    residual, its RMSNorm as the next input), microseconds per layer of back-to-back launches."""
+    from leanstream_amd import synth
+
+    out = {}
+    for key, layers in (("c2", 36), ("c1", 36)):
+        cfg = synth.CONFIGS[key]
+        try:
+            r = timed_chain(cfg, 20, 3, layers=layers)
+            gbs = cfg.algorithmic_bytes() / r["us"] / 1e3
+            out[key] = {"workload": f"chain{layers}_{cfg.name}", "layers_per_launch": layers,
+                        "us_per_layer": round(r["us"], 3), "steps": 20, "achieved_GBps": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        except Exception as exc:  # noqa: BLE001 -- reported in the line, not fatal to it
+            print(f"[bench] chain {key} failed: {exc!r}", file=sys.stderr, flush=True)
             out[key] = {"error": repr(exc)[:300]}
     return out
 
@@ -516,6 +540,7 @@ def main():
         },
     }
     if a.workload == "c2" and a.candidate is None and not a.copies and not a.no_secondary:
+        result["pipelined"] = pipelined_workloads()
         result["secondary"] = secondary_workloads()
     if not a.no_cpu:
         try:

@@ -5,6 +5,7 @@ Device memory and streams come from PyTorch; every computation runs in the HIP
 library through its C ABI. Errors from the library raise RuntimeError.
 """
 import ctypes as C
+import time
 
 import numpy as np
 
@@ -13,6 +14,7 @@ from ._native import DeviceQueue, Epilogue, ExecDesc, LayerBuffers
 
 MODE_BATCH_COMPAT, MODE_PROGRESSIVE, MODE_AUTO = 0, 1, 2
 STATUS_TIMEOUT, STATUS_QUEUE_ERROR, STATUS_BAD_DESCRIPTOR, STATUS_RANGE, STATUS_QUEUE_UNCONSUMED = 1, 2, 4, 8, 16
+EBUSY = 16
 STAGE_ARM = C.CFUNCTYPE(C.c_int, C.c_void_p)   # int (*arm_final_prediction)(void*)
 QUEUE_CONTROL_BYTES = 128
 
@@ -200,19 +202,33 @@ class NativeBackend:
         return self.lib.ls_hip_enqueue(self.context, layer, io_bucket, epoch, _ptr(x), _ptr(y), stream, _ptr(core),
                                        core_count, C.byref(queue.view), mode)
 
-    def try_enqueue_chain(self, layers, stream):
-        """ls_hip_enqueue_chain over a list of dicts with ls_hip_chain_layer's field names
-        (device tensors or integer addresses); returns the library's code."""
+    @staticmethod
+    def chain_blocks(layers):
+        """ls_hip_chain_layer blocks (a ctypes array) from a list of dicts with the struct's
+        field names (device tensors or integer addresses); reusable across enqueues."""
         arr = (_native.ChainLayer * len(layers))()
         for dst, src in zip(arr, layers):
             for name, kind in _native.ChainLayer._fields_:
                 if name in src:
                     v = src[name]
                     setattr(dst, name, _ptr(v) if kind is _native.p else float(v) if kind is C.c_float else int(v))
-        return self.lib.ls_hip_enqueue_chain(self.context, arr, len(layers), stream)
+        return arr
 
-    def enqueue_chain(self, layers, stream):
-        rc = self.try_enqueue_chain(layers, stream)
+    def try_enqueue_chain(self, layers, stream):
+        """ls_hip_enqueue_chain over `layers` (dicts, or blocks from chain_blocks); returns the
+        library's code."""
+        arr = layers if isinstance(layers, C.Array) else self.chain_blocks(layers)
+        return self.lib.ls_hip_enqueue_chain(self.context, arr, len(arr), stream)
+
+    def enqueue_chain(self, layers, stream, wait_busy=True):
+        """As try_enqueue_chain, raising on failure. EBUSY (more records in flight than the
+        ring holds) is waited out while earlier launches complete, unless wait_busy is False."""
+        arr = layers if isinstance(layers, C.Array) else self.chain_blocks(layers)
+        while True:
+            rc = self.try_enqueue_chain(arr, stream)
+            if rc != EBUSY or not wait_busy:
+                break
+            time.sleep(0)
         if rc:
             raise RuntimeError(f"Native enqueue_chain failed: {rc}")
 

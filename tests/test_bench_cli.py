@@ -47,3 +47,21 @@ def test_a_failing_secondary_workload_does_not_lose_the_others(monkeypatch):
     assert set(out) == {k for k, _, _ in bench.SECONDARY}
     assert "error" in out["c4"] and "error" in out["c4b4"] and "error" in out["c3"]
     assert out["c1"]["us_per_layer"] == 10.0 and out["c5"]["us_per_layer"] == 10.0
+
+
+def test_a_failing_chain_does_not_lose_the_other(monkeypatch):
+    """The default run's pipelined figures: one per shape, each failure reported in its own
+    entry while the other stands."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    def fake_chain(cfg, steps, warmup, layers=36, **kw):
+        if cfg.width == 1024:
+            raise AssertionError("device status 1")
+        return {"us": 12.0}
+
+    monkeypatch.setattr(bench, "timed_chain", fake_chain)
+    out = bench.pipelined_workloads()
+    assert set(out) == {"c2", "c1"}
+    assert out["c2"]["us_per_layer"] == 12.0 and out["c2"]["layers_per_launch"] == 36
+    assert "error" in out["c1"]
