@@ -162,6 +162,21 @@ def cpu_baseline(cfg, budget_s):
     }
 
 
+def control_plane_timing(groups=64, active=16, seconds=2.0):
+    """The C1 layer's control plane on one host thread (leanstream_amd/control_plane_timing:
+    Runtime/LayerStep, WeightManager, ExecutionQueue; begin, prediction update, enqueue,
+    finalize, READY publication of every active group, commit), µs per layer."""
+    exe = ROOT / "leanstream_amd" / "control_plane_timing"
+    if not exe.is_file():
+        subprocess.run(["make", "-s", "-C", str(ROOT / "leanstream_amd" / "csrc")], check=True)
+    out = subprocess.run([str(exe), str(groups), str(active), str(seconds)], check=True, capture_output=True,
+                         text=True, timeout=60 + seconds).stdout
+    r = json.loads(out.strip().splitlines()[-1])
+    r["what"] = ("Runtime::begin_layer + update_prediction + enqueue_compute (no launch) + finalize + READY "
+                 "publication of every active group + commit, host memory, one thread")
+    return r
+
+
 def decode_steps(sc, steps, warmup, **kw):
     """`steps` timed decode steps of the streaming shape `sc` (after `warmup` untimed ones):
     (arrival schedule, wall seconds per step, per-layer host times, per-group stamps)."""
@@ -547,6 +562,11 @@ def main():
             result["cpu_baseline"] = cpu_baseline(cfg, a.cpu_seconds)
         except Exception as exc:  # the GPU figure stands on its own
             result["cpu_baseline"] = {"value": None, "error": str(exc)}
+        if a.workload == "c2":
+            try:
+                result["cpu_baseline"]["control_plane_c1"] = control_plane_timing()
+            except Exception as exc:  # noqa: BLE001 -- reported, not fatal
+                result["cpu_baseline"]["control_plane_c1"] = {"error": repr(exc)[:300]}
     print(json.dumps(result), flush=True)
 
 

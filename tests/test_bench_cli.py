@@ -65,3 +65,14 @@ def test_a_failing_chain_does_not_lose_the_other(monkeypatch):
     assert set(out) == {"c2", "c1"}
     assert out["c2"]["us_per_layer"] == 12.0 and out["c2"]["layers_per_launch"] == 36
     assert "error" in out["c1"]
+
+
+def test_control_plane_timing_runs_on_the_host():
+    """The C1 layer's control plane (Runtime / WeightManager / ExecutionQueue, no GPU) times on
+    one host thread and reports every active group published."""
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    r = bench.control_plane_timing(seconds=0.2)
+    assert r["groups"] == 64 and r["active"] == 16 and r["threads"] == 1
+    assert r["layers"] > 0 and 0 < r["us_per_layer"] < 1000
