@@ -11,7 +11,9 @@ projection, compact reduction). Steps rotate over independent copies of the laye
 active bytes total more than the 256 MB Infinity Cache, so every step reads HBM.
 
 Printed: one JSON line (rank 0). value = microseconds per layer in the back-to-back
-pipeline (HIP events on the launch stream around the timed steps, divided by steps).
+pipeline (HIP events on the launch stream around the timed steps, divided by steps; the
+first steps are queued behind a bounded hold of the stream before the region starts, so
+the host's submission latency is not inside it: timed_steps).
 roofline.achieved = algorithmic bytes per layer / that per-layer time.
 
 The default run also times the layer stack of a decode step as one launch per step (36
@@ -203,6 +205,42 @@ def decode_steps(sc, steps, warmup, **kw):
         sd.close()
 
 
+def timed_steps(stream, submit, steps, queued=64):
+    """Milliseconds of `steps` calls of submit(i) back to back on `stream`, from HIP events on
+    the stream around them. The GPU is idle when this starts; the stream is held by a bounded
+    one-wave kernel (ls_hold_stream) while the start event and the first `queued` steps are
+    queued behind it, then released: the region holds exactly the steps, back to back,
+    without the host's submission latency before the first (the later ones are submitted
+    while the queued ones run)."""
+    import numpy as np
+    import torch
+
+    from leanstream_amd import _native
+    from leanstream_amd.backend import Mapped
+
+    lib = _native.library()
+    flag = Mapped(1, np.uint32)
+    try:
+        flag.host[0] = 0
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        rc = lib.ls_hold_stream(stream.cuda_stream, flag.ptr, 100_000_000)   # released well within 1 s
+        if rc:
+            raise RuntimeError(f"ls_hold_stream failed: {rc}")
+        start.record(stream)
+        first = min(steps, queued)
+        for i in range(first):
+            submit(i)
+        flag.release(0, 1)
+        for i in range(first, steps):
+            submit(i)
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop)
+    finally:
+        flag.close()
+
+
 def timed_layer(cfg, steps, warmup, copies=0, table=None, isolated=0):
     """One layer shape, every group resident and ready before launch: microseconds per layer
     back to back (HIP events on the launch stream around `steps` launches that rotate over
@@ -226,14 +264,7 @@ def timed_layer(cfg, steps, warmup, copies=0, table=None, isolated=0):
         assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
         print(f"[bench] warmup done, timing {steps} steps", file=sys.stderr, flush=True)
         # back-to-back pipeline: events on the launch stream around the timed steps
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for i in range(steps):
-            layer.run_core(copy=i % copies, epoch=1)
-        stop.record(stream)
-        torch.cuda.synchronize()
-        ms_total = start.elapsed_time(stop)
+        ms_total = timed_steps(stream, lambda i: layer.run_core(copy=i % copies, epoch=1), steps)
         # isolated layers: one event pair per launch, idle GPU between launches
         iso = []
         for i in range(isolated):
@@ -279,14 +310,7 @@ def timed_chain(cfg, steps, warmup, layers=36, isolated=0, stamps=False):
         torch.cuda.synchronize()
         assert layer.backend.status() == 0, f"device status {layer.backend.status()}"
         print(f"[bench] chain warmup done, timing {steps} launches", file=sys.stderr, flush=True)
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for _ in range(steps):
-            layer.backend.enqueue_chain(blocks, sid)
-        stop.record(stream)
-        torch.cuda.synchronize()
-        ms_total = start.elapsed_time(stop)
+        ms_total = timed_steps(stream, lambda i: layer.backend.enqueue_chain(blocks, sid), steps, queued=8)
         iso = []
         for _ in range(isolated):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -310,6 +334,48 @@ def timed_chain(cfg, steps, warmup, layers=36, isolated=0, stamps=False):
     assert status == 0, f"device status {status}"
     out.update({"us": ms_total * 1000.0 / (steps * layers), "ms_total": ms_total, "iso": iso, "layers": layers})
     return out
+
+
+def timed_dependent(cfg, steps, warmup, layers=36):
+    """The same decode-step stack as timed_chain, one launch per layer: layer i's enqueue (x =
+    layer i - 1's RMSNorm output) followed by its epilogue (hidden state and RMSNorm times layer
+    i + 1's weight, the next layer's input), in stream order, so each layer waits for the one
+    before it -- the per-launch path with the decode step's dependency. µs per layer."""
+    import torch
+
+    from leanstream_amd.backend import MODE_PROGRESSIVE
+    from leanstream_amd.workload import DeviceLayer
+
+    print(f"[bench] dependent per-launch stack {cfg.name}: {layers} layers", file=sys.stderr, flush=True)
+    layer = DeviceLayer(cfg, copies=layers, with_y32=False, diagnostics=False)
+    try:
+        d = cfg.width
+        norm = layer.chain_norm_weights(layers + 1)
+        xs = torch.empty(layers + 1, d, dtype=torch.float16, device="cuda")
+        xs[0].copy_(layer.x)
+        hidden = torch.empty(layers + 1, d, dtype=torch.float16, device="cuda")
+        hidden[0].copy_(layer.x)
+        ys = torch.empty(layers, d, dtype=torch.float16, device="cuda")
+        layer.seal_empty_queue(1)
+        stream = torch.cuda.current_stream()
+        sid = stream.cuda_stream
+        be = layer.backend
+
+        def step(_):
+            for i in range(layers):
+                be.set_epilogue(hidden[i], hidden[i + 1], norm_weight=norm[i + 1], norm_output=xs[i + 1], eps=1e-5)
+                be.enqueue(0, 0, 1, xs[i], ys[i], sid, layer.core_ptr(i), layer.k, layer.queue, MODE_PROGRESSIVE)
+
+        for i in range(warmup):
+            step(i)
+        torch.cuda.synchronize()
+        ms_total = timed_steps(stream, step, steps, queued=steps)
+        be.set_epilogue(None, None)
+        status = be.status()
+    finally:
+        layer.close()
+    assert status == 0, f"device status {status}"
+    return {"us": ms_total * 1000.0 / (steps * layers), "ms_total": ms_total}
 
 
 # Shorter back-to-back runs of the other workloads, in the default run's JSON line:
@@ -348,7 +414,8 @@ def secondary_workloads():
 def pipelined_workloads():
     """The decode step's layer stack in one launch per step (ls_hip_enqueue_chain): 36 distinct
     C2 layers and 36 distinct C1 layers chained through the epilogue (hidden state as the next
-    residual, its RMSNorm as the next input), microseconds per layer of back-to-back launches."""
+    residual, its RMSNorm as the next input), microseconds per layer of back-to-back launches;
+    beside it the same stack launched layer by layer with the epilogue between layers."""
     from leanstream_amd import synth
 
     out = {}
@@ -360,6 +427,8 @@ def pipelined_workloads():
             out[key] = {"workload": f"chain{layers}_{cfg.name}", "layers_per_launch": layers,
                         "us_per_layer": round(r["us"], 3), "steps": 20, "achieved_GBps": round(gbs, 1),
                         "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            dep = timed_dependent(cfg, 5, 1, layers=layers)
+            out[key]["per_launch_dependent_us_per_layer"] = round(dep["us"], 3)
         except Exception as exc:  # noqa: BLE001 -- reported in the line, not fatal to it
             print(f"[bench] chain {key} failed: {exc!r}", file=sys.stderr, flush=True)
             out[key] = {"error": repr(exc)[:300]}

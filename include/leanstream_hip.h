@@ -268,6 +268,11 @@ int ls_synth_bytes(void* dst, uint64_t bytes, uint64_t seed, void* stream);
 int ls_synth_uniform_f16(void* dst, uint64_t count, uint64_t seed, double lo, double hi, void* stream);
 int ls_synth_normal_f16(void* dst, uint64_t count, uint64_t seed, void* stream);
 int ls_synth_normal_bf16(void* dst, uint64_t count, uint64_t seed, void* stream);
+/* No reference counterpart; a benchmark utility: holds `stream` (one wave) until the host sets
+ * the host-coherent word *flag nonzero, or limit_ticks of the 100 MHz device clock pass. Work
+ * queued behind it starts back to back once it is released, without the host's submission
+ * latency in between. EINVAL for a NULL flag or a zero limit. */
+int ls_hold_stream(void* stream, const uint32_t* flag, uint64_t limit_ticks);
 
 #ifdef __cplusplus
 }

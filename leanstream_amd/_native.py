@@ -126,6 +126,7 @@ _SIGNATURES = [
     ("ls_synth_uniform_f16", [p, u64, u64, C.c_double, C.c_double, p], C.c_int),
     ("ls_synth_normal_f16", [p, u64, u64, p], C.c_int),
     ("ls_synth_normal_bf16", [p, u64, u64, p], C.c_int),
+    ("ls_hold_stream", [p, p, u64], C.c_int),
 ]
 
 EXPORTED = tuple(name for name, _, _ in _SIGNATURES)

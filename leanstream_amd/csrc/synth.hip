@@ -148,6 +148,18 @@ __global__ void synth_normal_kernel(uint16_t* dst, uint64_t count, uint64_t seed
         dst[i] = f64_to_f16_bits(box_muller(seed, i));
 }
 
+// One wave holds its stream until the host sets *flag (a host-coherent word) or the bound
+// (in ticks of the 100 MHz clock) passes, whichever comes first.
+__global__ void hold_kernel(const uint32_t* flag, uint64_t limit) {
+    if (threadIdx.x != 0) return;
+    const uint64_t start = wall_clock64();
+    uint32_t n = 0;
+    while (!__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)) {
+        __builtin_amdgcn_s_sleep(8);
+        if ((++n & 15u) == 0 && wall_clock64() - start > limit) break;
+    }
+}
+
 static unsigned grid_for(uint64_t n) {
     uint64_t g = (n + 255) / 256;
     return (unsigned)(g > 65536 ? 65536 : (g ? g : 1));
@@ -186,6 +198,12 @@ int ls_synth_normal_f16(void* dst, uint64_t count, uint64_t seed, void* stream) 
     if (!count) return 0;
     hipLaunchKernelGGL(lsamd::synth_normal_kernel, dim3(lsamd::grid_for(count)), dim3(256), 0, (hipStream_t)stream,
                        (uint16_t*)dst, count, seed);
+    return (int)hipPeekAtLastError();
+}
+
+int ls_hold_stream(void* stream, const uint32_t* flag, uint64_t limit_ticks) {
+    if (!flag || !limit_ticks) return EINVAL;
+    hipLaunchKernelGGL(lsamd::hold_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, flag, limit_ticks);
     return (int)hipPeekAtLastError();
 }
 

@@ -61,9 +61,11 @@ def test_a_failing_chain_does_not_lose_the_other(monkeypatch):
         return {"us": 12.0}
 
     monkeypatch.setattr(bench, "timed_chain", fake_chain)
+    monkeypatch.setattr(bench, "timed_dependent", lambda cfg, steps, warmup, layers=36: {"us": 20.0})
     out = bench.pipelined_workloads()
     assert set(out) == {"c2", "c1"}
     assert out["c2"]["us_per_layer"] == 12.0 and out["c2"]["layers_per_launch"] == 36
+    assert out["c2"]["per_launch_dependent_us_per_layer"] == 20.0
     assert "error" in out["c1"]
 
 
