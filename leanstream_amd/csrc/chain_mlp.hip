@@ -134,8 +134,9 @@ __device__ __forceinline__ LayerView record_view(uint32_t w) {
 struct ChainShared {
     alignas(16) uint16_t hs[kWaves][kDnRows];   // a down item's h, per wave
     alignas(16) float partial[kThreads];        // RMSNorm: the sums of squares of the norm's 256 threads
-    uint32_t xclaim;  // layers whose input staging a wave of the workgroup has taken on
-    uint32_t xcount;  // layers whose input is staged in LDS
+    uint32_t xcount;  // the waves' staged parts of the input, kWaves per staged layer
+    uint32_t pcount;  // the waves' sums written to `partial`, kWaves per normalised layer
+    uint32_t pread;   // the waves done reading `partial`, kWaves per normalised layer
 };
 
 template <int D>
@@ -277,57 +278,44 @@ __device__ __forceinline__ bool chain_wait_count(const MlpArgs& a, uint32_t* slo
     return true;
 }
 
-// Whether this wave stages the workgroup's input of its staged-layer number s (1, 2, ...):
-// the first wave of the workgroup to get there takes it on.
-__device__ __forceinline__ bool chain_claim(ChainShared& sh, uint32_t s) {
-    uint32_t won = 0;
-    if (lane_id() == 0) {
-        uint32_t expected = s - 1;
-        won = __hip_atomic_compare_exchange_strong(&sh.xclaim, &expected, s, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    return wave_bcast(won) != 0;
-}
-
-// Stages layer v's whole input into the workgroup's LDS (paired as stage_x does), by one wave,
-// then raises the input count. The first layer reads its input. A chained layer reads the
-// previous sequence's hidden words, each until it carries that sequence's tag, and takes
-// them as they are or (with a norm weight) their RMSNorm times the weight in the Ministral
-// epilogue's order (examples/ministral/native/predictor_shared_input.cu:16-41): thread t of
-// 256 sums the squares of columns t, t + 256, ... in that order, the 256 sums meet in a
-// halving tree, inverse = 1 / sqrt(sum / d + eps), fp16 of h * inverse, then the fp16
-// product with the weight. Lane l's 16-byte word quads l + 64 m hold columns 4 l .. 4 l + 3
-// + 256 m, so the lane computes the sums of the norm's threads 4 l .. 4 l + 3 itself.
-// Bit for bit the epilogue's result, in fewer instructions: h is fp16, so h * h is exact in
-// fp32 and fma(h, h, sum) rounds once exactly where sum + h * h does; fma(h, inverse, -0)
-// is the rounded product itself (the -0 addend keeps a -0 product's sign); and the fp16
-// product of two fp16 values (v_pk_mul_f16) is the exact product rounded once, as the
-// epilogue's fp32 product rounded to fp16 is.
+// Stages this wave's part of layer v's input into the workgroup's LDS (the paired layout of
+// stage_x) and raises the input count; the four waves of the workgroup together stage it
+// all. The parts follow the RMSNorm of the Ministral epilogue
+// (examples/ministral/native/predictor_shared_input.cu:16-41), whose thread t of 256 sums the
+// squares of columns t, t + 256, ... in that order: wave w takes threads 64 w .. 64 w + 63,
+// lane l thread t = 64 w + l and its columns t + 256 m, so every thread's sum stays one lane's
+// sequential sum. The first layer reads its input. A chained layer reads the previous
+// sequence's hidden words, each until it carries that sequence's tag, and takes them as they
+// are or (with a norm weight) their RMSNorm times the weight: the 256 sums meet in LDS, every
+// wave forms the epilogue's halving tree and inverse = 1 / sqrt(sum / d + eps) from them, then
+// fp16 of h * inverse, then the fp16 product with the weight. Bit for bit the epilogue's
+// result: h is fp16, so h * h is exact in fp32 and fma(h, h, sum) rounds where sum + h * h
+// does, and the fp16 product of two fp16 values is the exact product rounded once, as the
+// epilogue's fp32 product rounded to fp16 is. `normed` counts the normalised layers staged so
+// far, this one included.
+//
+// Overwriting the input area is safe once any word of the layer carries the new tag: a column
+// of layer l completes only after every unit's down item for it, each after its unit's h, so
+// every gate/up item of layer l -- the only readers of the area -- is done by then.
 template <int D>
-__device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerView& v, u32x4* xl, ChainShared& sh) {
+__device__ bool chain_stage_part(const ChainArgs& c, const MlpArgs& a, const LayerView& v, uint32_t normed, u32x4* xl,
+                                 ChainShared& sh) {
 #pragma clang fp contract(off)
-    using Xg = XGeom<D>;
-    constexpr int PL = Xg::N / 64;   // pieces (8 columns) per lane: l + 64 j
-    constexpr int Q = D / 256;       // word quads (4 columns) per lane: l + 64 m
-    static_assert(Xg::N % 64 == 0, "whole pieces per lane");
-    const int l = lane_id();
+    constexpr int Q = D / kThreads;   // columns per lane: t + 256 m
+    const uint32_t l = lane_id(), t = 64u * wave_id() + l;
+    uint32_t hv[Q];                   // fp16 bits of the lane's columns
     if (!v.chained) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(v.x);
-        u32x4 pc[PL];
 #pragma unroll
-        for (int j = 0; j < PL; ++j) pc[j] = src[l + 64 * j];
-#pragma unroll
-        for (int j = 0; j < PL; ++j) xl[x_position<D>(l + 64 * j)] = pair_halves(pc[j]);
+        for (int m = 0; m < Q; ++m) hv[m] = v.x[t + kThreads * m];
     } else {
         const uint32_t* words = c.xtag + (size_t)((v.seq - 1u) & 1u) * D;
         const uint32_t tag = chain_tag(v.seq - 1u);
-        u32x2 wt[Q];   // the weights of the lane's columns, as fp16 pairs (read-only: plain loads,
-                       // in flight while the words are polled)
+        uint32_t wt[Q];   // read-only weights: plain loads, in flight while the words are polled
         if (v.norm_weight) {
 #pragma unroll
-            for (int m = 0; m < Q; ++m) wt[m] = reinterpret_cast<const u32x2*>(v.norm_weight)[l + 64 * m];
+            for (int m = 0; m < Q; ++m) wt[m] = v.norm_weight[t + kThreads * m];
         }
-        u32x4 q[Q];
+        uint32_t q[Q];
         bool have[Q];
 #pragma unroll
         for (int m = 0; m < Q; ++m) have[m] = false;
@@ -335,68 +323,62 @@ __device__ bool chain_stage_x(const ChainArgs& c, const MlpArgs& a, const LayerV
         for (;;) {
 #pragma unroll
             for (int m = 0; m < Q; ++m)
-                if (!have[m]) q[m] = ld_agent16(words, 16 * (l + 64 * m));
+                if (!have[m]) q[m] = ld_agent(words + t + kThreads * m);
             bool all = true;
 #pragma unroll
             for (int m = 0; m < Q; ++m) {
-                const u32x4 w = q[m];
-                have[m] = have[m] || ((w.x >> 16) == tag && (w.y >> 16) == tag && (w.z >> 16) == tag && (w.w >> 16) == tag);
+                have[m] = have[m] || (q[m] >> 16) == tag;
                 all = all && have[m];
             }
             if (__all(all)) break;
             if (wave_should_stop(a, c.csync, wtime)) return false;
             __builtin_amdgcn_s_sleep(1);
         }
-        // the lane's columns as fp16 pairs in column order: hv[m] = (4i, 4i + 1), (4i + 2, 4i + 3)
-        u32x2 hv[Q];
+        // the input is here: every wave of the workgroup waits for its staging, which now takes
+        // the SIMD's issue slots ahead of the co-resident wave (the poll above did not)
+        __builtin_amdgcn_s_setprio(3);
 #pragma unroll
-        for (int m = 0; m < Q; ++m)
-            hv[m] = u32x2{(q[m].x & 0xFFFFu) | (q[m].y << 16), (q[m].z & 0xFFFFu) | (q[m].w << 16)};
+        for (int m = 0; m < Q; ++m) hv[m] = q[m] & 0xFFFFu;
         if (v.norm_weight) {
-            float sum[4] = {0.f, 0.f, 0.f, 0.f};   // the norm's threads 4 l + e
+            float sum = 0.f;   // thread t's sum of squares
 #pragma unroll
             for (int m = 0; m < Q; ++m) {
-                const h2 lo = as_h2(hv[m].x), hi = as_h2(hv[m].y);
-                sum[0] = __builtin_fmaf((float)lo.x, (float)lo.x, sum[0]);
-                sum[1] = __builtin_fmaf((float)lo.y, (float)lo.y, sum[1]);
-                sum[2] = __builtin_fmaf((float)hi.x, (float)hi.x, sum[2]);
-                sum[3] = __builtin_fmaf((float)hi.y, (float)hi.y, sum[3]);
+                const float h = (float)half_bits((uint16_t)hv[m]);
+                sum = __builtin_fmaf(h, h, sum);
             }
-            *reinterpret_cast<float4*>(sh.partial + 4 * l) = float4{sum[0], sum[1], sum[2], sum[3]};
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its loads
+            // the sums of the previous normalised layer have been read by every wave
+            if (!chain_wait_count(a, c.csync, &sh.pread, kWaves * (normed - 1))) return false;
+            sh.partial[t] = sum;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS store lands before its count
+            if (l == 0) __hip_atomic_fetch_add(&sh.pcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (!chain_wait_count(a, c.csync, &sh.pcount, kWaves * normed)) return false;
             // halving tree: (p[l] + p[l + 128]) + (p[l + 64] + p[l + 192]), then strides 32 .. 1
             float s2 = (sh.partial[l] + sh.partial[l + 128]) + (sh.partial[l + 64] + sh.partial[l + 192]);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the reads above happen before the count below
+            if (l == 0) __hip_atomic_fetch_add(&sh.pread, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 #pragma unroll
             for (int k = 32; k >= 1; k >>= 1) s2 = s2 + __shfl_xor(s2, k);
             const float total = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s2)));
             const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + v.eps);
-            auto norm_pair = [&](uint32_t hw, uint32_t ww) -> uint32_t {
-                const h2 hp = as_h2(hw);
-                const h2 n{(_Float16)__builtin_fmaf((float)hp.x, inverse, -0.0f),
-                           (_Float16)__builtin_fmaf((float)hp.y, inverse, -0.0f)};
-                return __builtin_bit_cast(uint32_t, n * as_h2(ww));
-            };
 #pragma unroll
-            for (int m = 0; m < Q; ++m) hv[m] = u32x2{norm_pair(hv[m].x, wt[m].x), norm_pair(hv[m].y, wt[m].y)};
-        }
-        // Paired layout (pair_halves): piece p = quad i / 2 holds columns 8p .. 8p + 7 as
-        // (0,4)(1,5)(2,6)(3,7). Quads 2p and 2p + 1 sit on lanes 2k and 2k + 1 (same m): the
-        // even lane keeps halves 0,1 and takes 4,5 from its neighbour, the odd one keeps 6,7 and
-        // takes 2,3; each writes its half of the piece.
-        const bool odd = l & 1;
-        u32x2* xw = reinterpret_cast<u32x2*>(xl);
-#pragma unroll
-        for (int m = 0; m < Q; ++m) {
-            const uint32_t got =
-                (uint32_t)__builtin_amdgcn_mov_dpp((int)(odd ? hv[m].x : hv[m].y), 0xB1, 0xF, 0xF, false);
-            const uint32_t lo = odd ? got : hv[m].x, hi = odd ? hv[m].y : got;
-            const uint32_t piece = (uint32_t)(l >> 1) + 32u * m;
-            xw[2 * x_position<D>(piece) + (odd ? 1 : 0)] =
-                u32x2{__builtin_amdgcn_perm(hi, lo, 0x05040100u), __builtin_amdgcn_perm(hi, lo, 0x07060302u)};
+            for (int m = 0; m < Q; ++m) {
+                float p = (float)half_bits((uint16_t)hv[m]) * inverse;
+                asm volatile("" : "+v"(p));   // the fp32 product, then fp16 (as the epilogue rounds)
+                const _Float16 n = (_Float16)p;
+                hv[m] = __builtin_bit_cast(uint16_t, (_Float16)(half_bits((uint16_t)wt[m]) * n));
+            }
         }
     }
+    // Paired layout: piece p = column / 8 holds (8p + j, 8p + j + 4) in its word j, so column
+    // 8p + k is half 2 (k & 3) + (k >> 2) of the piece's 16 bytes.
+    uint16_t* xh = reinterpret_cast<uint16_t*>(xl);
+#pragma unroll
+    for (int m = 0; m < Q; ++m) {
+        const uint32_t col = t + kThreads * m;
+        xh[8 * x_position<D>(col >> 3) + 2 * (col & 3) + ((col >> 2) & 1)] = (uint16_t)hv[m];
+    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's LDS stores land before its count
-    if (lane_id() == 0) __hip_atomic_fetch_add(&sh.xcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (l == 0) __hip_atomic_fetch_add(&sh.xcount, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return true;
 }
 
@@ -571,9 +553,9 @@ __device__ void chain_worker(const ChainArgs& c, uint32_t first, ChainShared& sh
     u32x4* sl_cur = stage + (2 * wave) * kSlotStride;
     u32x4* sl_nxt = sl_cur + kSlotStride;
     ChainItem cur{}, nxt{};
-    if (threadIdx.x == 0) sh.xcount = sh.xclaim = 0;
+    if (threadIdx.x == 0) sh.xcount = sh.pcount = sh.pread = 0;
     __syncthreads();
-    uint32_t issued = 0, computed = 0, staged = 0, out = 0;
+    uint32_t issued = 0, computed = 0, staged = 0, normed = 0, out = 0;
     // `owed`: the layer this wave has finished but not yet counted out of. Its last stores
     // (the outputs of completed columns) went out before the wave's next item loads, so the
     // wait for the next item's data covers them; the count follows that wait instead of a
@@ -609,15 +591,11 @@ __device__ void chain_worker(const ChainArgs& c, uint32_t first, ChainShared& sh
         chain_stamp(c, i, kChainStampXWait);
         if (chain_wg_items<D>(blockIdx.x, role.nw, v.core_count)) {
             ++staged;
-            if (chain_claim(sh, staged)) {
-                // every wave of the workgroup waits for this one: it takes the SIMD's issue
-                // slots ahead of the co-resident wave meanwhile
-                __builtin_amdgcn_s_setprio(3);
-                ok = chain_stage_x<D>(c, a, v, xl, sh);
-                __builtin_amdgcn_s_setprio(0);
-                if (!ok) break;
-                chain_stamp(c, i, kChainStampXIn);
-            }
+            if (v.chained && v.norm_weight) ++normed;
+            ok = chain_stage_part<D>(c, a, v, normed, xl, sh);
+            __builtin_amdgcn_s_setprio(0);
+            if (!ok) break;
+            chain_stamp(c, i, kChainStampXIn);
         }
         a.seq = v.seq;
         const ChainOut o{v.y, v.y32, v.hidden, c.xtag + (size_t)(v.seq & 1u) * D, c.yacc + (size_t)(v.seq & 1u) * D,
@@ -630,7 +608,7 @@ __device__ void chain_worker(const ChainArgs& c, uint32_t first, ChainShared& sh
         for (uint32_t k = 0; ok && k < il.K; ++k) {
             const bool behind = issued > computed + 1;   // the next item's loads are in flight behind this one
             if (cur.gu) {
-                if (!(ok = chain_wait_count(a, c.csync, &sh.xcount, staged))) break;
+                if (!(ok = chain_wait_count(a, c.csync, &sh.xcount, kWaves * staged))) break;
                 if (behind) chain_gu_dots<D, kStageOps>(sl_cur, xl, cur, v.seq);
                 else chain_gu_dots<D, 0>(sl_cur, xl, cur, v.seq);
                 settle();
