@@ -306,14 +306,14 @@ __device__ bool chain_stage_part(const ChainArgs& c, const MlpArgs& a, const Lay
     uint32_t hv[Q];                   // fp16 bits of the lane's columns
     if (!v.chained) {
 #pragma unroll
-        for (int m = 0; m < Q; ++m) hv[m] = v.x[t + kThreads * m];
+        for (int m = 0; m < Q; ++m) hv[m] = glb(v.x)[t + kThreads * m];
     } else {
         const uint32_t* words = c.xtag + (size_t)((v.seq - 1u) & 1u) * D;
         const uint32_t tag = chain_tag(v.seq - 1u);
         uint32_t wt[Q];   // read-only weights: plain loads, in flight while the words are polled
         if (v.norm_weight) {
 #pragma unroll
-            for (int m = 0; m < Q; ++m) wt[m] = v.norm_weight[t + kThreads * m];
+            for (int m = 0; m < Q; ++m) wt[m] = glb(v.norm_weight)[t + kThreads * m];
         }
         uint32_t q[Q];
         bool have[Q];
@@ -412,14 +412,14 @@ __device__ __forceinline__ void chain_output(const ChainOut& o, int col, unsigne
     const long long sum = (long long)(word & kAccValueMask) - (long long)rows * kAccBias;
     const float v = (float)((double)sum * kAccInv);
     const _Float16 y16 = (_Float16)v;
-    if (o.y32) o.y32[col] = v;
-    o.y[col] = __builtin_bit_cast(uint16_t, y16);
+    if (o.y32) glb(o.y32)[col] = v;
+    glb(o.y)[col] = __builtin_bit_cast(uint16_t, y16);
     float ab = (float)half_bits((uint16_t)res) + (float)y16;
     asm volatile("" : "+v"(ab));   // an fp32 sum rounded to fp16 (no mixed-precision fused form)
     const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)ab);
-    __hip_atomic_store(o.xout + col, (o.tag << 16) | h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(glb(o.xout) + col, (o.tag << 16) | h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // system scope: the layer's flag publishes the row to other agents
-    if (o.hidden) __hip_atomic_store(o.hidden + col, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (o.hidden) __hip_atomic_store(glb(o.hidden) + col, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     st_agent_u64(o.acc + col, 0ull);
 }
 
@@ -447,7 +447,7 @@ __device__ __forceinline__ void chain_add_columns(const MlpArgs& a, uint32_t* sl
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const unsigned long long t = acc_term(a, slot, cs[i]);
-        n[i] = __hip_atomic_fetch_add(o.acc + (col + kTileColOff[i]), t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t;
+        n[i] = __hip_atomic_fetch_add(glb(o.acc) + (col + kTileColOff[i]), t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + t;
     }
     chain_check_pending(o, pd, U);
 #pragma unroll
@@ -495,7 +495,7 @@ __device__ __forceinline__ bool chain_dn(const ChainArgs& c, const MlpArgs& a, C
 #pragma unroll
         for (int i = 0; i < 4; ++i) res[i] = ld_agent(o.prev + col + kTileColOff[i]);
     } else {
-        const uint16_t* r = v.residual ? v.residual : v.x;
+        const LS_GLOBAL uint16_t* r = glb(v.residual ? v.residual : v.x);
 #pragma unroll
         for (int i = 0; i < 4; ++i) res[i] = r[col + kTileColOff[i]];
     }
@@ -518,7 +518,7 @@ __device__ __forceinline__ bool chain_dn(const ChainArgs& c, const MlpArgs& a, C
 // counters: a wave may leave a later layer before an earlier one).
 __device__ __forceinline__ void chain_count_out(const ChainArgs& c, uint32_t i) {
     if (lane_id() == 0)
-        (void)__hip_atomic_fetch_add(c.csync + kChainExit + (i * 8u + blockIdx.x % 8u) * kLine, 1u, __ATOMIC_RELAXED,
+        (void)__hip_atomic_fetch_add(glb(c.csync) + kChainExit + (i * 8u + blockIdx.x % 8u) * kLine, 1u, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -727,11 +727,11 @@ __device__ void chain_supervisor(const ChainArgs& c, uint32_t first) {
         chain_stamp(c, i, kChainStampDone);
         if (lane == 0) {
             // a layer that raised a status bit produced no valid output: its flag and bell stay
-            const bool clean = !failed && __hip_atomic_load(c.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0;
-            if (clean && flag) __hip_atomic_store(flag, epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (clean && bell) (void)__hip_atomic_fetch_add(bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            const bool clean = !failed && __hip_atomic_load(glb(c.status), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 0;
+            if (clean && flag) __hip_atomic_store(glb(flag), epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (clean && bell) (void)__hip_atomic_fetch_add(glb(bell), 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
             st_agent(c.csync + kChainLayersDone, i + 1);
-            __hip_atomic_store(c.done, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(glb(c.done), seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
     if (failed) return;   // waves may still be running: the host clears the block before the next launch

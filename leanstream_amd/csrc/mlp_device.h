@@ -34,11 +34,27 @@ static_assert(kDnCols == 256, "a down item is two scale blocks wide");
 // ---------------------------------------------------------------------------------
 // memory helpers
 // ---------------------------------------------------------------------------------
+// The global-memory view of a pointer (device or host-mapped memory, never LDS). A pointer
+// whose address space the compiler cannot infer -- one read from memory, or rebuilt from
+// its scalar halves -- is accessed with flat instructions, and flat loads, stores and
+// atomics count in lgkmcnt as well as vmcnt: a wave's wait for its own LDS accesses would
+// then also wait for them to complete in memory. Through this view they are global
+// instructions, counted in vmcnt only.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define LS_GLOBAL __attribute__((address_space(1)))
+#else
+#define LS_GLOBAL   // the host pass compiles no device code; address space 1 means something else there
+#endif
+template <class T>
+__device__ __forceinline__ LS_GLOBAL T* glb(T* p) {
+    return (LS_GLOBAL T*)p;
+}
+
 __device__ __forceinline__ uint32_t ld_agent(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(glb(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_agent(uint32_t* p, uint32_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ float ldf_agent(const float* p) {
     return __uint_as_float(ld_agent(reinterpret_cast<const uint32_t*>(p)));
@@ -47,13 +63,13 @@ __device__ __forceinline__ void stf_agent(float* p, float v) {
     st_agent(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
 }
 __device__ __forceinline__ uint32_t ld_sys(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load(glb(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ uint64_t ld_sys64(const uint32_t* p) {
-    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    return __hip_atomic_load(glb(reinterpret_cast<const uint64_t*>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 __device__ __forceinline__ uint32_t add_agent(uint32_t* p, uint32_t v) {
-    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_fetch_add(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // All of this thread's earlier memory operations have completed at their point of
 // coherence (stores acknowledged, loads returned).
@@ -65,16 +81,16 @@ __device__ __forceinline__ void drain_vmem() {
 __device__ __forceinline__ uint64_t now_ticks() { return wall_clock64(); }
 
 __device__ __forceinline__ u32x4 ld_stream16(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4*>(p)));
 }
 // A plain (L2-retained) 16-byte load, for weight lines that are consumed by several
 // instructions (a streaming load may drop the line after its first piece is read).
-__device__ __forceinline__ u32x4 ld_cached16(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ u32x4 ld_cached16(const uint8_t* p) { return *glb(reinterpret_cast<const u32x4*>(p)); }
 __device__ __forceinline__ u32x2 ld_stream8(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return __builtin_nontemporal_load(glb(reinterpret_cast<const u32x2*>(p)));
 }
 __device__ __forceinline__ uint32_t ld_stream4(const uint8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+    return __builtin_nontemporal_load(glb(reinterpret_cast<const uint32_t*>(p)));
 }
 
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
@@ -155,7 +171,7 @@ __device__ __forceinline__ void stamp(const MlpArgs& a, uint32_t k) {
 // Error path only: the bit is ordered before everything the lane stores afterwards (its
 // count-out, a completion word), so a host that sees the launch complete sees the bit.
 __device__ __forceinline__ void raise_status(const MlpArgs& a, uint32_t* slot, uint32_t bit) {
-    __hip_atomic_fetch_or(a.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_fetch_or(glb(a.status), bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
     st_agent(slot + kSyncAbort, 1u);
 }
@@ -239,7 +255,7 @@ __device__ __forceinline__ u32x4 pair_halves(u32x4 w) {   // (0,1)(2,3)(4,5)(6,7
 template <int D>
 __device__ __forceinline__ void load_x(const uint16_t* x, uint32_t batch, XPart<D>& xp, u32x4* xl) {
     using Xg = XGeom<D>;
-    const u32x4* src = reinterpret_cast<const u32x4*>(x);
+    const LS_GLOBAL u32x4* src = glb(reinterpret_cast<const u32x4*>(x));
 #pragma unroll
     for (int j = 0; j < Xg::PER; ++j) {
         const int i = threadIdx.x + j * kThreads;
@@ -251,7 +267,8 @@ __device__ __forceinline__ void load_x(const uint16_t* x, uint32_t batch, XPart<
         const uint32_t row = 1 + j / Xg::INSTR, pos = (j % Xg::INSTR) * 64 + lane;
         if (pos < (uint32_t)Xg::N) {
             typedef __attribute__((address_space(3))) void* lds_ptr;
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + (size_t)row * Xg::N + x_raw<D>(pos)),
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const void*>(reinterpret_cast<const u32x4*>(x) + (size_t)row * Xg::N + x_raw<D>(pos)),
                                              (lds_ptr)(xl + row * Xg::N + (pos - lane)), 16, 0, 0);
         }
     }
@@ -349,7 +366,7 @@ __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc,
 #pragma unroll
         for (int p = Hf::P0; p < Hf::P1; ++p) {
             const uint8_t* row = uniform_ptr(grp + (size_t)(n0 + p * Gm::NPW) * (3 * D / 2));
-            const uint16_t* srow = uniform_ptr(sc + (size_t)(n0 + p * Gm::NPW) * 3 * Gm::BLOCKS);
+            const LS_GLOBAL uint16_t* srow = glb(uniform_ptr(sc + (size_t)(n0 + p * Gm::NPW) * 3 * Gm::BLOCKS));
             const uint32_t wo = (uint32_t)sub * (3 * D / 2) + 16 * r, so = (uint32_t)sub * 3 * Gm::BLOCKS + (r >> 2);
 #pragma unroll
             for (int k = Hf::K0; k < Hf::K1; ++k) {
@@ -367,7 +384,7 @@ __device__ __forceinline__ void gu_issue(const uint8_t* grp, const uint16_t* sc,
         const bool ok = nu < nvalid;
         const int n = n0 + (ok ? nu : 0);
         const uint8_t* row = grp + (size_t)n * (3 * D / 2);
-        const uint16_t* srow = sc + (size_t)n * 3 * Gm::BLOCKS;
+        const LS_GLOBAL uint16_t* srow = glb(sc + (size_t)n * 3 * Gm::BLOCKS);
 #pragma unroll
         for (int k = Hf::K0; k < Hf::K1; ++k) {
             const int chunk = r + Gm::LPR * k;
@@ -498,7 +515,7 @@ struct DnItem {
 };
 
 __device__ __forceinline__ uint64_t ld_agent_u64(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(glb(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D>
@@ -514,7 +531,7 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
 #pragma unroll
         for (int j = 0; j < 8; ++j) it.w[j] = ld_stream16(base + wo + j * RB);
         const uint16_t* srow = uniform_ptr(sc + (size_t)r0 * 3 * BLOCKS + 2 * BLOCKS + 2 * tile);
-        it.s = *reinterpret_cast<const uint32_t*>(srow + (uint32_t)lane * 3 * BLOCKS);
+        it.s = *glb(reinterpret_cast<const uint32_t*>(srow + (uint32_t)lane * 3 * BLOCKS));
         it.h = ld_agent_u64(uniform_ptr(hrow + r0) + lane);
         return;
     }
@@ -525,7 +542,7 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
         it.w[j] = n < G ? ld_stream16(base + (size_t)n * RB) : u32x4{0, 0, 0, 0};
     }
     const int n = r0 + lane;
-    it.s = n < G ? *reinterpret_cast<const uint32_t*>(sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile) : 0u;
+    it.s = n < G ? *glb(reinterpret_cast<const uint32_t*>(sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile)) : 0u;
     it.h = n < G ? ld_agent_u64(hrow + n) : (uint64_t)seq << 32;
 }
 
@@ -688,7 +705,7 @@ __device__ __forceinline__ bool await_epoch(const MlpArgs& a, uint32_t* slot, Ep
 // Compact reduction by deterministic fixed-point accumulation (kAccOne in mlp_args.h).
 // ---------------------------------------------------------------------------------
 __device__ __forceinline__ void st_agent_u64(unsigned long long* p, unsigned long long v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned long long word, uint32_t rows) {
@@ -969,7 +986,7 @@ __device__ __forceinline__ bool fetch_descs(const MlpArgs& a, uint32_t* slot, ui
     if (lane < 5 * count) {
         const uint32_t j = lane / 5, w = lane - 5 * j;
         const uint32_t g = u0 + item_unit(il.item(k0 + j), il.NG, ipu, T, nb, P, nu);
-        word = g < a.core_count ? reinterpret_cast<const uint32_t*>(a.core)[5 * g + w]
+        word = g < a.core_count ? glb(reinterpret_cast<const uint32_t*>(a.core))[5 * g + w]
                                 : ld_agent(a.qmirror + 5 * (g - a.core_count) + w);
     }
     return true;
@@ -1040,7 +1057,7 @@ __device__ __forceinline__ bool dn_issue_pack(const MlpArgs& a, uint32_t* slot, 
         const uint8_t* p = reinterpret_cast<const uint8_t*>((uint64_t)hi << 32 | lo);
         it.w[k] = (uint32_t)r / G < units ? ld_stream16(p + dc * 16) : u32x4{0, 0, 0, 0};
     }
-    it.s = valid ? *reinterpret_cast<const uint32_t*>(u.sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile) : 0u;
+    it.s = valid ? *glb(reinterpret_cast<const uint32_t*>(u.sc + (size_t)n * 3 * BLOCKS + 2 * BLOCKS + 2 * tile)) : 0u;
     pl.hp = a.hbuf + (size_t)u.dest * G + n;
     pl.unit = g0 + j;
     pl.dest = u.dest;
