@@ -25,7 +25,13 @@ namespace leanstream::runtime {
 // queue's items and waits for each item's position to be published (a newly ready group
 // is computed by many waves at once); n > 0 = a workgroup claims up to n ready positions
 // at a time and its four waves compute them (the ready-pair claim of
-// backends/triton/persistent.py:77-86 for n = 2).
+// backends/triton/persistent.py:77-86 for n = 2). The tile axis of the grid
+// (docs/kernel_selection.md:13-19, kernel_selector.h KernelCandidate): unroll = items in
+// flight per wave at batch 1 -- 0 the shape's own walk (two, through LDS slots, for
+// 64-neuron groups at d <= 4096), 1 the plain walk (one, in registers); tile_size = the
+// staged walk's down-item width -- 0 its own choice (64-column quarters when every item
+// gets a wave, d <= 2048), 256 whole tiles. A candidate whose axis a shape lacks launches
+// as the default does.
 inline constexpr uint32_t kAllResident = 1u << 16;
 inline constexpr KernelCandidate kHipCandidates[] = {
     {0, 256, "hip_fused_w256", 0, 0, 0, 0, 0},
@@ -34,8 +40,10 @@ inline constexpr KernelCandidate kHipCandidates[] = {
     {3, 256, "hip_split_w256", 0, 0, 0, 0, 1},
     {4, kAllResident, "hip_split_resident", 0, 0, 0, 0, 1},
     {5, kAllResident, "hip_fused_resident_pairs", 0, 0, 0, 2, 0},
+    {6, kAllResident, "hip_fused_resident_plain", 0, 0, 1, 0, 0},
+    {7, kAllResident, "hip_fused_resident_tiles", 0, 256, 0, 0, 0},
 };
-inline constexpr uint32_t kHipCandidateCount = 6;
+inline constexpr uint32_t kHipCandidateCount = 8;
 inline constexpr KernelCandidate kHipDefault = kHipCandidates[1];
 inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexcept {
     return KernelSelector(offline_table, {kHipCandidates, kHipCandidateCount}, kHipDefault);

@@ -47,6 +47,7 @@ struct HipBackend::Impl {
     bool needs_clear = true;
     uint32_t seq = 0;
     int cus = 0, per_cu_fused = 0, per_cu_split = 0;
+    int per_cu_fused_plain = 0, per_cu_split_plain = 0;   // the plain walk's kernels at batch 1
     bool bound = false;
 
     void release() {
@@ -135,6 +136,12 @@ int HipBackend::bind(const HipLayerBuffers& b) {
     if (e == hipSuccess)
         e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, static_cast<int>(rows), gs, &p.per_cu_split);
     if (e == hipSuccess && (p.per_cu_fused < 1 || p.per_cu_split < 1 || p.cus * std::min(p.per_cu_fused, p.per_cu_split) < 3))
+        e = hipErrorInvalidConfiguration;
+    if (e == hipSuccess && !dense && b.batch == 1)
+        e = lsamd::resident_workers(b.width, lsamd::kEntryFused, 1, gs, &p.per_cu_fused_plain, 1);
+    if (e == hipSuccess && !dense && b.batch == 1)
+        e = lsamd::resident_workers(b.width, lsamd::kEntrySplit, 1, gs, &p.per_cu_split_plain, 1);
+    if (e == hipSuccess && !dense && b.batch == 1 && std::min(p.per_cu_fused_plain, p.per_cu_split_plain) < 1)
         e = hipErrorInvalidConfiguration;
     // layer chains: the geometry of the staged batch-1 kernels
     const bool chains = !dense && b.batch == 1 && b.group_size == 64 && lsamd::chain_available(static_cast<int>(b.width));
@@ -311,7 +318,10 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     if ((core.size && !core.data) || core.size > p.buf.slot_capacity || q.capacity > p.buf.queue_capacity) return EINVAL;
     const KernelCandidate c = selector_.candidate(selector_.select(s));
     const int entry = c.entry_point == lsamd::kEntrySplit ? lsamd::kEntrySplit : lsamd::kEntryFused;
-    const int per_cu = entry == lsamd::kEntryFused ? p.per_cu_fused : p.per_cu_split;
+    // unroll = items in flight per wave: 1 asks for the plain walk (batch 1)
+    const bool plain = c.unroll == 1 && !p.dense && p.buf.batch == 1;
+    const int per_cu = entry == lsamd::kEntryFused ? (plain ? p.per_cu_fused_plain : p.per_cu_fused)
+                                                   : (plain ? p.per_cu_split_plain : p.per_cu_split);
     // Persistent workers (plus the mirror workgroup) must be co-resident: a worker's
     // down-projection share waits for h published by other workers.
     const uint32_t resident = static_cast<uint32_t>(p.cus * per_cu) - 1;
@@ -329,6 +339,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     a.epoch = epoch;
     a.batch_mode = mode == ConsumerMode::Progressive ? 0u : 1u;
     a.claim_batch = c.group_batch;
+    a.dn_tile = c.tile_size == lsamd::kDnCols ? lsamd::kDnCols : 0u;
     a.spin_limit = spin_limit_;
     auto hs = static_cast<hipStream_t>(stream);
     hipError_t e = hipSuccess;
@@ -346,7 +357,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     p.seq = p.seq == UINT32_MAX ? 1u : p.seq + 1;
     a.seq = p.seq;
     a.done = p.done;
-    const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(workers), entry};
+    const lsamd::LaunchPlan plan{static_cast<int>(p.buf.width), static_cast<int>(workers), entry, plain ? 1 : 0};
     // Batch 5..32: the dense matrix-core path computes the core units (the queue is not
     // consumed: a dense layer's groups are all resident).
     lsamd::StageHook hook{arm_final_prediction, arm_context, static_cast<hipEvent_t>(b_done), 0};

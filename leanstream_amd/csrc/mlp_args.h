@@ -203,6 +203,8 @@ struct MlpArgs {
     uint32_t epoch;
     uint32_t seq;                 // launch sequence number (selects the ring slot)
     uint32_t batch_mode;          // 1: wait for batch_epoch before consuming the queue
+    uint32_t dn_tile;             // staged walk's down items: 0 = its own choice (quarters when every item
+                                  // gets a wave, d <= 2048), 256 = whole 256-column tiles
     uint32_t claim_batch;         // progressive path: 0 = every wave takes its stripe of the queue
                                   // positions, waiting for each to be published; n > 0 = workgroups
                                   // claim up to n ready positions at a time

@@ -1668,9 +1668,10 @@ template <int D>
 constexpr bool kStagedQuarters = D <= 2048;
 
 template <int D>
-__device__ __forceinline__ uint32_t staged_down_items(const WaveRole& r, uint32_t nu) {
+__device__ __forceinline__ uint32_t staged_down_items(const WaveRole& r, uint32_t nu, uint32_t dn_tile) {
     constexpr uint32_t T = D / kDnCols, ipu = kStagedGroup / GuGeom<D>::NPI;
     if constexpr (!kStagedQuarters<D>) return T;
+    if (dn_tile == kDnCols) return T;   // the candidate asks for whole tiles
     const uint32_t ng = (nu * ipu + 3u) & ~3u;
     return ng + 4 * T * nu <= r.nw ? 4 * T : T;
 }
@@ -1682,7 +1683,7 @@ __device__ __forceinline__ void prefetch_core_descs(const MlpArgs& a, uint32_t* 
     p.valid = false;
     p.word = 0;
     if (!a.core_count) return;
-    const uint32_t TQ = staged_down_items<D>(role, a.core_count);
+    const uint32_t TQ = staged_down_items<D>(role, a.core_count, a.dn_tile);
     const ItemList il = make_staged_items(role, a.core_count * ipu, a.core_count * TQ);
     if (!il.K) return;
     uint32_t seen = 0;
@@ -1703,7 +1704,7 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
     constexpr uint32_t ipu = G / Gm::NPI;   // gate/up items per unit
     const uint32_t nu = u1 - u0;
     const uint32_t NG = nu * ipu;
-    const uint32_t TQ = staged_down_items<D>(role, nu);   // down items per unit
+    const uint32_t TQ = staged_down_items<D>(role, nu, a.dn_tile);   // down items per unit
     const bool quarters = kStagedQuarters<D> && TQ != T;
     const ItemList il = make_staged_items(role, NG, nu * TQ);
     const uint32_t K = il.K, KG = il.KG;

@@ -11,12 +11,13 @@ struct LaunchPlan {
     int width;        // d
     int workers;      // persistent workgroups
     int entry_point;  // kEntryFused or kEntrySplit
+    int walk = 0;     // 0: the shape's own walk; 1: the plain walk at batch 1 (one item in flight per wave)
 };
 
 bool variant_available(int width);
 // Maximum co-resident workgroups per CU for the kernels of an entry point (the kernel
 // family depends on the batch and, at batch 1, on the group size).
-hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu);
+hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu, int walk = 0);
 // Fused: one persistent launch. Split: stage A (if core) -> stage B -> reduction.
 // Host work at the boundary between the queue consumer and the reduction (LeanStream's
 // A -> B -> arm -> event -> reduction order, backends/triton/enqueue.cpp:33-36): the split

@@ -808,8 +808,9 @@ Variant make_variant() {
 // Kernel family of a launch: 0 batch 1, 1 batch 2 .. kMaxBatch, 2 staged (batch 1,
 // 64-neuron groups, widths where two workgroups' slots fit a CU's LDS), 3 packed (batch 1,
 // groups of at most 32 neurons).
-int family(int width, int batch, int group_size) {
+int family(int width, int batch, int group_size, int walk = 0) {
     if (batch > 1) return 1;
+    if (walk == 1) return 0;   // the plain walk serves every batch-1 shape
     if (group_size == (int)kStagedGroup && staged_width(width)) return 2;
     return group_size <= (int)kDnRows / 2 ? 3 : 0;
 }
@@ -826,10 +827,10 @@ const Variant* find_variant(int width) {
 
 bool variant_available(int width) { return find_variant(width) != nullptr; }
 
-hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu) {
+hipError_t resident_workers(int width, int entry_point, int batch, int group_size, int* per_cu, int walk) {
     const Variant* v = find_variant(width);
     if (!v || batch < 1 || batch > (int)kMaxBatch) return hipErrorInvalidValue;
-    const int nb = family(width, batch, group_size);
+    const int nb = family(width, batch, group_size, walk);
     const void* k = entry_point == kEntryFused ? v->fused[nb] : v->stage_b[nb];
     int n = 0;
     hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kThreads, 0);
@@ -855,7 +856,7 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     MlpArgs a = args;
     Bounds b = bounds;
     if (a.batch < 1 || a.batch > kMaxBatch) return hipErrorInvalidValue;
-    const int nb = family(p.width, (int)a.batch, (int)a.group_size);
+    const int nb = family(p.width, (int)a.batch, (int)a.group_size, p.walk);
     a.pack = nb == 3 ? kDnRows / a.group_size : 1u;   // units per down item (pack_units)
     // the persistent kernels' leading scalars (LS_HOT_PARAMS), then the argument blocks
     uint32_t grid = (uint32_t)p.workers + 1;

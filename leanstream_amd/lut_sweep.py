@@ -33,18 +33,36 @@ from .backend import MODE_PROGRESSIVE
 BUCKETS = 8
 MALL_BYTES = 256 * 2 ** 20
 # kHipCandidates (include/leanstream/hip_backend.h): name, workers (0: all resident), entry
-# point (0 fused, 1 split), group_batch
+# point (0 fused, 1 split), group_batch, walk (unroll: 1 = the plain walk), down tile
+# (tile_size: 256 = whole tiles)
 CANDIDATES = ("hip_fused_w256", "hip_fused_resident", "hip_fused_w1024", "hip_split_w256", "hip_split_resident",
-              "hip_fused_resident_pairs")
-CONFIGS = ((256, 0, 0), (0, 0, 0), (1024, 0, 0), (256, 1, 0), (0, 1, 0), (0, 0, 2))
+              "hip_fused_resident_pairs", "hip_fused_resident_plain", "hip_fused_resident_tiles")
+CONFIGS = ((256, 0, 0, 0, 0), (0, 0, 0, 0, 0), (1024, 0, 0, 0, 0), (256, 1, 0, 0, 0), (0, 1, 0, 0, 0),
+           (0, 0, 2, 0, 0), (0, 0, 0, 1, 0), (0, 0, 0, 0, 256))
 DEFAULT_CANDIDATE = 1
+STAGED_MAX_WIDTH, QUARTERS_MAX_WIDTH, STAGED_GROUP = 4096, 2048, 64
 
 
-def effective_configs(resident):
-    """(workers, entry, group_batch) each candidate launches with on this device (worker
-    counts are clamped to the co-resident maximum), and for each candidate the first
-    candidate id with the same launch -- identical launches are measured once."""
-    eff = [(min(w, resident) if w else resident, e, b) for w, e, b in CONFIGS]
+def shape_walk(width, group_size):
+    """The walk a batch-1 shape takes by default: staged (64-neuron groups, d <= 4096),
+    packed (groups of at most 32 neurons) or plain."""
+    if group_size == STAGED_GROUP and width <= STAGED_MAX_WIDTH:
+        return "staged"
+    return "packed" if group_size <= 32 else "plain"
+
+
+def effective_configs(resident, width=4096, group_size=64):
+    """(workers, entry, group_batch, walk, tile) each candidate launches with for a batch-1
+    shape on this device -- worker counts clamped to the co-resident maximum, a walk or tile
+    the shape does not offer replaced by what it launches instead -- and for each candidate
+    the first candidate id with the same launch: identical launches are measured once. (The
+    plain walk's own co-resident count may differ; it is always a launch of its own.)"""
+    walk = shape_walk(width, group_size)
+    eff = []
+    for w, e, b, pw, tile in CONFIGS:
+        plain = 1 if pw == 1 and walk != "plain" else 0
+        tiles = 256 if tile == 256 and walk == "staged" and width <= QUARTERS_MAX_WIDTH and not plain else 0
+        eff.append((min(w, resident) if w else resident, e, b, plain, tiles))
     first = [eff.index(x) for x in eff]
     return eff, first
 
@@ -81,7 +99,7 @@ def sweep(workload, trials=25, gap_ns=5000, copies=0, log=print):
     for c in range(copies):
         rows[c][:, 1] += c * cfg.groups
         rows[c][:, 2] += c * cfg.groups
-    eff, first = effective_configs(layer.backend.max_workers)
+    eff, first = effective_configs(layer.backend.max_workers, cfg.width, cfg.group_size)
     measured = sorted(set(first))
     rng = np.random.default_rng(0x5EED)
     epoch = 100
@@ -183,6 +201,43 @@ def write_header(path, results):
     Path(path).write_text("\n".join(lines))
 
 
+def write_markdown(path, results, commands):
+    """The sweep summary of profiles/: per shape, the median latency of every candidate per
+    bucket and the winner."""
+    lines = ["# Kernel candidate sweep per io bucket (offline CDNA4 LUT)", "",
+             "Command (one MI355X, each workload in its own process):", ""]
+    lines += [f"    {c}" for c in commands]
+    lines += ["", "Figure: median host wall time (µs) from the enqueue call to the layer's completion word, "
+              f"{results[0]['trials']} trials in a fresh random candidate order each, over layer copies exceeding the "
+              "Infinity Cache. Bucket q: all k groups go through the ready queue, rem_q = floor((q + 1/2) k / 8) of "
+              "them unpublished at enqueue and then published 5 µs apart. Candidates whose launch is the same on "
+              "MI355X for the shape are measured once (\"same as\"). Winner: fastest median, the default (1) when "
+              "within 2%.", ""]
+    for r in results:
+        lines += [f"## {r['name']} (d = {r['width']}, groups of {r['group_size']}, k = {r['active']})", ""]
+        same = [f"{CANDIDATES[c]} = {CANDIDATES[f]}" for c, f in enumerate(r["same_launch_as"]) if f != c]
+        if same:
+            lines += ["Same launch: " + "; ".join(same) + ".", ""]
+        lines.append("| bucket | unpublished | " + " | ".join(CANDIDATES) + " | winner |")
+        lines.append("|---" * (len(CANDIDATES) + 3) + "|")
+        w = winners(r)
+        for q, med in enumerate(r["median_us"]):
+            lines.append(f"| {q} | {r['remaining'][q]} | " + " | ".join(f"{v:.1f}" for v in med) + f" | {w[q]} |")
+        lines.append("")
+        med = np.asarray(r["median_us"])
+        gain = (med[:, DEFAULT_CANDIDATE] / med.min(axis=1) - 1) * 100
+        arrival = np.asarray(r["remaining"]) * r["gap_ns"] / 1e3
+        if all(x == DEFAULT_CANDIDATE for x in w):
+            lines += [f"Every bucket keeps the default: no candidate beats it by more than {gain.max():.1f}% "
+                      f"(the 2% tie margin). The latency follows the last publication "
+                      f"({arrival[0]:.0f}-{arrival[-1]:.0f} µs after the enqueue across the buckets), which no "
+                      "launch configuration can move.", ""]
+        else:
+            lines += [f"Buckets {[q for q, x in enumerate(w) if x != DEFAULT_CANDIDATE]} select another candidate "
+                      f"(up to {gain.max():.1f}% below the default's median).", ""]
+    Path(path).write_text("\n".join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--workload", default="c2")
@@ -190,11 +245,19 @@ def main():
     ap.add_argument("--gap-ns", type=int, default=5000)
     ap.add_argument("--out")
     ap.add_argument("--header", help="write the C++ header from the sweep files given as arguments")
+    ap.add_argument("--markdown", help="write the sweep summary from the sweep files given as arguments")
     ap.add_argument("sweeps", nargs="*")
     a = ap.parse_args()
-    if a.header:
+    if a.header or a.markdown:
         results = [json.loads(Path(p).read_text()) for p in a.sweeps]
-        write_header(a.header, results)
+        if a.header:
+            write_header(a.header, results)
+        if a.markdown:
+            cmds = [f"python -m leanstream_amd.lut_sweep --workload {r['workload']} --out {p}"
+                    for r, p in zip(results, a.sweeps)]
+            cmds.append("python -m leanstream_amd.lut_sweep --header include/leanstream/hip_kernel_lut.h "
+                        "--markdown profiles/kernel_lut_sweep.md " + " ".join(a.sweeps))
+            write_markdown(a.markdown, results, cmds)
         return
     r = sweep(a.workload, trials=a.trials, gap_ns=a.gap_ns, log=lambda m: print(m, flush=True))
     r["winners"] = winners(r)

@@ -271,6 +271,37 @@ def test_split_entry_point_core_before_queue(torch_gpu):
     layer.close()
 
 
+@pytest.mark.parametrize("key", ["c1", "c2", "g2"])
+def test_walk_and_tile_candidates_give_the_default_bits(torch_gpu, key):
+    """The tile axis of the candidate grid: hip_fused_resident_plain (the plain walk, one item
+    in flight per wave) and hip_fused_resident_tiles (the staged walk's down items as whole
+    256-column tiles) launch different kernels or item lists than the default where the
+    shape has them (C1: both; C2: the plain walk; Group2: the plain walk instead of the
+    packed one), through the ready queue, with the default's y32 bit for bit -- every walk
+    sums a column's contributions in the same order -- and the oracle's within tolerance."""
+    torch = torch_gpu
+    cfg = synth.CONFIGS[key]
+    log(f"case: walk / tile candidates {cfg.name}")
+    outs = {}
+    for cand in (1, 6, 7):
+        layer = DeviceLayer(cfg, offline_table=[[cand]])
+        layer.executions.zero_()
+        rows, _ = _queue_run(torch, layer, 0, MODE_PROGRESSIVE, "delayed", epoch=3)
+        assert layer.backend.last_candidate() == cand
+        assert np.all(layer.executions.cpu().numpy()[:len(rows)] == 1)
+        outs[cand] = layer.y32.cpu().numpy().copy()
+        if cand == 1:
+            ref = oracle_for(layer, rows)
+        layer.close()
+    if key == "g2":
+        # packed down items sum several units' rows per item: within tolerance of the plain walk
+        compare(outs[6], ref["y32"], f"{cfg.name} plain walk")
+        assert np.array_equal(outs[7], outs[1])
+    else:
+        assert np.array_equal(outs[6], outs[1]) and np.array_equal(outs[7], outs[1])
+    compare(outs[1], ref["y32"], f"{cfg.name} default")
+
+
 @pytest.mark.parametrize("table", [None, [[4]]], ids=["fused", "split"])
 def test_stage_hook_arm_and_b_done(torch_gpu, table):
     """TritonBackend's arm_final_prediction / b_done (include/leanstream/triton_cuda.h:30-33)

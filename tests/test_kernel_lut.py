@@ -25,9 +25,26 @@ def _header_rows():
     return rows
 
 
-def test_sweeps_cover_the_c1_c3_and_c2_shapes():
-    widths = {json.loads(p.read_text())["width"] for p in SWEEPS}
-    assert {1024, 4096} <= widths
+def test_sweeps_cover_the_four_batch1_shapes():
+    """C1/C3 (d 1024), C2 (d 4096), C4 (d 8192) and Group2 (d 4096, groups of 2)."""
+    shapes = {(json.loads(p.read_text())["width"], json.loads(p.read_text())["group_size"]) for p in SWEEPS}
+    assert {(1024, 64), (4096, 64), (8192, 64), (4096, 2)} <= shapes
+
+
+def test_identical_launches_are_measured_once():
+    """The plain-walk candidate is the default's launch where the shape walks plain already
+    (d 8192), and the whole-tile candidate where the staged walk never takes quarters
+    (d > 2048) or does not run (groups of 2)."""
+    resident = 511
+    _, first = lut_sweep.effective_configs(resident, 8192, 64)
+    assert first[6] == 1 and first[7] == 1
+    _, first = lut_sweep.effective_configs(resident, 4096, 64)
+    assert first[6] == 6 and first[7] == 1
+    _, first = lut_sweep.effective_configs(resident, 1024, 64)
+    assert first[6] == 6 and first[7] == 7
+    _, first = lut_sweep.effective_configs(resident, 4096, 2)
+    assert first[6] == 6 and first[7] == 1
+    assert first[4] == 4 and first[3] == 3   # split entry points stay launches of their own
 
 
 @pytest.mark.parametrize("path", SWEEPS, ids=lambda p: p.stem)
