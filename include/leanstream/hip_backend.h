@@ -21,11 +21,13 @@ namespace leanstream::runtime {
 // takes a share of both the gate/up and the down-projection work; entry_point 0 = one
 // fused launch (core + ready queue + compact reduction), entry_point 1 = split launches
 // (stage A -> stage B -> reduction kernel). group_batch selects how a launch consumes
-// positions published after it started: 0 = every wave takes its fixed stripe of the
-// queue's items and waits for each item's position to be published (a newly ready group
-// is computed by many waves at once); n > 0 = a workgroup claims up to n ready positions
-// at a time and its four waves compute them (the ready-pair claim of
-// backends/triton/persistent.py:77-86 for n = 2). The tile axis of the grid
+// positions: 0 = every wave takes its fixed stripe of the queue's items and waits for
+// each item's position to be published (a newly ready group is computed by many waves at
+// once); n > 0 = the positions are taken in the reference's ranges of n (the ready pairs of
+// backends/triton/persistent.py:59-90 for n = 2) -- static descriptor-index ranges when all
+// were ready at launch, [head, min(head + n, ready)) claimed in publication order by the
+// queue mirror otherwise, every range logged -- and every range's items are dealt to all
+// waves as with n = 0. The tile axis of the grid
 // (docs/kernel_selection.md:13-19, kernel_selector.h KernelCandidate): unroll = items in
 // flight per wave at batch 1 -- 0 the shape's own walk (two, through LDS slots, for
 // 64-neuron groups at d <= 4096), 1 the plain walk (one, in registers); tile_size = the
@@ -44,7 +46,10 @@ inline constexpr KernelCandidate kHipCandidates[] = {
     {7, kAllResident, "hip_fused_resident_tiles", 0, 256, 0, 0, 0},
 };
 inline constexpr uint32_t kHipCandidateCount = 8;
-inline constexpr KernelCandidate kHipDefault = kHipCandidates[1];
+// The default consumes the queue in the reference's ready pairs (persistent.py:59-90): static
+// descriptor-index pairs when every position was ready, claimed [head, min(head + 2, ready))
+// ranges otherwise, each range's items dealt to every wave.
+inline constexpr KernelCandidate kHipDefault = kHipCandidates[5];
 inline KernelSelector hip_selector(KernelDecisionTable offline_table = {}) noexcept {
     return KernelSelector(offline_table, {kHipCandidates, kHipCandidateCount}, kHipDefault);
 }

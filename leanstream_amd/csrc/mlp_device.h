@@ -1866,6 +1866,19 @@ __device__ __forceinline__ bool process_items_staged(const MlpArgs& a, Shared& s
 // per round trip, one per lane) and advances a device-side ready count. Workers only
 // poll device memory.
 // ---------------------------------------------------------------------------------
+// One claim log entry (kClaimLogWords), written by one lane of the worker or mirror that takes the range.
+__device__ __forceinline__ void log_claim(const MlpArgs& a, uint32_t* slot, uint32_t first, uint32_t count,
+                                          uint32_t ready) {
+    if (!a.claim_log) return;
+    const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
+    if (seq >= a.claim_log_cap) return;
+    uint32_t* e = a.claim_log + (size_t)seq * kClaimLogWords;
+    e[0] = first;
+    e[1] = count;
+    e[2] = ready;
+    e[3] = blockIdx.x;
+}
+
 // Runs on wave 0 of the mirror workgroup. `pre` is lane 0's early 64-bit load of
 // (total_count, epoch): adjacent words (byte offsets 8 and 12), read as one pair.
 __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, uint64_t pre) {
@@ -1945,6 +1958,17 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
                 }
             }
             drain_vmem();  // the whole wave's copies are complete before the count moves
+            // Pair-claiming candidates (claim_batch > 0) on the progressive path: the newly
+            // ready positions are claimed here, in publication order, as the ranges
+            // [head, min(head + claim_batch, ready)) of backends/triton/persistent.py:71-87 --
+            // by one claimer, so no two workgroups race for the head -- and logged; every
+            // wave then computes the claimed positions' items, as the striped path does.
+            if (lane == 0 && a.claim_batch && !by_index)
+                for (uint32_t head = mirrored; head < ready;) {
+                    const uint32_t end = min(head + a.claim_batch, ready);
+                    log_claim(a, slot, head, end - head, ready);
+                    head = end;
+                }
             if (lane == 0) st_agent(slot + kSyncReady, ready);
             mirrored = ready;
             wt = Waiter(a.spin_limit);  // the bound applies to waiting without progress
@@ -1956,57 +1980,6 @@ __device__ __forceinline__ void mirror_queue(const MlpArgs& a, uint32_t* slot, u
             __builtin_amdgcn_s_sleep(2);
         }
     }
-}
-
-// One claim log entry (kClaimLogWords), written by one lane of the claiming workgroup.
-__device__ __forceinline__ void log_claim(const MlpArgs& a, uint32_t* slot, uint32_t first, uint32_t count,
-                                          uint32_t ready) {
-    if (!a.claim_log) return;
-    const uint32_t seq = add_agent(slot + kSyncClaims, 1u);
-    if (seq >= a.claim_log_cap) return;
-    uint32_t* e = a.claim_log + (size_t)seq * kClaimLogWords;
-    e[0] = first;
-    e[1] = count;
-    e[2] = ready;
-    e[3] = blockIdx.x;
-}
-
-// Claim the next ready positions [head, min(head + claim_batch, ready)) against the
-// mirrored ready count (claim_batch = 2: the ready pair of backends/triton/persistent.py:73-87). Every wave of the workgroup takes part; `ok` is this
-// wave's success so far. Returns the number of claimed positions (0 = leave, also when
-// any wave of the workgroup failed).
-__device__ __forceinline__ uint32_t claim_pair(const MlpArgs& a, Shared& sh, uint32_t* slot, uint32_t total, bool ok) {
-    if (lane_id() == 0) sh.wfail[wave_id()] = ok ? 0u : 1u;
-    __syncthreads();  // failure flags written; previous readers of sh.word[5..6] are done
-    if (threadIdx.x == 0) {
-        uint32_t got = 0, head = 0;
-        bool failed = false;
-        for (int w = 0; w < kWaves; ++w) failed = failed || sh.wfail[w];
-        Waiter wt(a.spin_limit);
-        while (!failed) {
-            if (ld_agent(slot + kSyncAbort)) break;
-            const uint32_t ready = ld_agent(slot + kSyncReady);
-            head = ld_agent(slot + kSyncClaimHead);
-            if (head >= total) break;
-            if (head < ready) {
-                const uint32_t end = min(head + a.claim_batch, min(ready, total));
-                uint32_t expected = head;
-                if (__hip_atomic_compare_exchange_strong(slot + kSyncClaimHead, &expected, end, __ATOMIC_RELAXED,
-                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                    got = end - head;
-                    log_claim(a, slot, head, got, ready);
-                    break;
-                }
-                continue;
-            }
-            if (wt.expired()) { raise_status(a, slot, kStatusTimeout); break; }
-            __builtin_amdgcn_s_sleep(2);
-        }
-        sh.word[5] = head;
-        sh.word[6] = got;
-    }
-    __syncthreads();
-    return __builtin_amdgcn_readfirstlane(sh.word[6]);
 }
 
 }  // namespace lsamd

@@ -82,9 +82,8 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
     if (threadIdx.x == 0) sh.xcount = 0;   // waves count themselves in once their part of x is staged
     __syncthreads();
     bool ok = true;
-    enum : uint32_t { kCore, kDecide, kClaim, kPairs, kDone };
+    enum : uint32_t { kCore, kDecide, kDone };
     uint32_t phase = CORE ? kCore : kDecide;
-    uint32_t pair = blockIdx.x;   // kPairs: this worker's next static range, in units of claim_batch
     for (;;) {
         uint32_t u0 = 0, u1 = 0, e = early;
         WaveRole r = role;
@@ -104,41 +103,22 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
                 if (sh.wpath[w] != path) path = 0;
             path = __builtin_amdgcn_readfirstlane(path);
             // All positions published before the launch (path 2), or published while it
-            // runs with striped consumption (path 1, claim_batch 0): every wave walks its
-            // stripe of the queue's items, waiting for each item's position as needed.
-            // With claim_batch > 0 the workgroups take ranges of claim_batch positions:
-            // static ranges of descriptor indices when all were ready (persistent.py:63-69),
-            // claimed ready ranges otherwise (persistent.py:71-90).
-            if (path == 2 && a.claim_batch) {
-                phase = kPairs;
-                continue;
-            } else if (path == 2 || (path == 1 && a.claim_batch == 0)) {
+            // runs (path 1): every wave walks its stripe of the queue's items, waiting for
+            // each item's position as needed. Pair-claiming candidates (claim_batch > 0)
+            // take the positions in the reference's ranges -- static ranges of descriptor
+            // indices when all were ready (persistent.py:63-69), logged here by the worker
+            // that owns them; claimed ready ranges otherwise (persistent.py:71-90), taken by
+            // the queue mirror -- and deal every range's items to all waves the same way.
+            if (path == 2 && a.claim_batch && threadIdx.x == 0)
+                for (uint32_t first = blockIdx.x * a.claim_batch; first < ep.total; first += W * a.claim_batch)
+                    log_claim(a, slot, first, min(a.claim_batch, ep.total - first), kClaimStatic);
+            if (path == 2 || path == 1) {
                 u0 = a.core_count;
                 u1 = u0 + ep.total;
                 phase = kDone;
-            } else if (path == 1) {
-                phase = kClaim;
-                continue;
             } else {
                 break;
             }
-        } else if (phase == kPairs) {
-            const uint32_t first = pair * a.claim_batch;
-            if (!ok || first >= ep.total) break;
-            const uint32_t got = min(a.claim_batch, ep.total - first);
-            if (threadIdx.x == 0) log_claim(a, slot, first, got, kClaimStatic);
-            u0 = a.core_count + first;
-            u1 = u0 + got;
-            pair += W;
-            r = WaveRole{wave, kWaves, 0};
-            e = 0;
-        } else if (phase == kClaim) {
-            const uint32_t got = claim_pair(a, sh, slot, ep.total, ok);
-            if (!got) break;
-            u0 = a.core_count + __builtin_amdgcn_readfirstlane(sh.word[5]);
-            u1 = u0 + got;
-            r = WaveRole{wave, kWaves, 0};
-            e = 0;
         } else {
             break;
         }

@@ -8,7 +8,9 @@ All-ready launches (ready == STATIC): worker w takes the descriptor-index ranges
 [batch (w + k W), +batch) for k = 0, 1, ... (persistent.py:63-69, batch 2).
 Progressive launches: a worker claims [head, min(head + batch, ready)) of the publication
 positions by compare-and-swap on the claim head (persistent.py:71-87), so the heads rise
-in claim order and the ranges are contiguous; which worker wins is timing-dependent.
+in claim order and the ranges are contiguous; which worker wins is timing-dependent (a
+consumer may also take them with one claimer -- logged as worker index `workers`, the
+queue mirror of the MI355X kernels -- and deal their items to every worker).
 """
 import numpy as np
 
@@ -35,7 +37,7 @@ def check_claim_log(log_words, total, batch, workers):
     order = np.argsort(e[:, 0], kind="stable")
     e = e[order]
     first, count, ready, worker = (e[:, i].astype(np.int64) for i in range(4))
-    assert np.all(worker < workers), "worker index out of range"
+    assert np.all(worker < (workers if static else workers + 1)), "worker index out of range"
     # every position exactly once, union [0, total)
     covered = np.zeros(total, dtype=np.int64)
     for f, c in zip(first, count):

@@ -31,6 +31,19 @@ def _mutate(log, fn):
     return e.astype(np.uint64).reshape(-1)
 
 
+def test_single_claimer_log_passes():
+    """Claimed ranges taken by one claimer (worker index W, the queue mirror) as positions
+    become ready: the reference's ranges, in publication order."""
+    e = []
+    head = 0
+    for ready in (3, 4, 9, 16):
+        while head < ready:
+            end = min(head + 2, ready)
+            e.append((head, end - head, ready, 4))
+            head = end
+    assert check_claim_log(np.asarray(e, dtype=np.uint64).reshape(-1), 16, 2, 4) == "claimed"
+
+
 def test_planted_mistakes_fail():
     rng = np.random.default_rng(7)
     log = simulate_claims(16, 2, 4, [3, 9, 16], rng)
@@ -40,7 +53,7 @@ def test_planted_mistakes_fail():
         "triple": lambda e: e.__setitem__((0, 1), 3),
         "short claim": lambda e: e.__setitem__((0, 2), 16) if e[0, 1] == 1 else e.__setitem__((0, 1), 1),
         "not ready": lambda e: e.__setitem__((0, 2), e[0, 0]),
-        "worker": lambda e: e.__setitem__((0, 3), 4),
+        "worker": lambda e: e.__setitem__((0, 3), 5),   # 4 = the single claimer (the mirror) is allowed
     }
     for name, fn in bad.items():
         with pytest.raises(AssertionError):
@@ -48,6 +61,7 @@ def test_planted_mistakes_fail():
             raise RuntimeError(f"{name} not detected")
     st = static_log(16, 2, 4)
     for name, fn in {"owner": lambda e: e.__setitem__((0, 3), (e[0, 3] + 1) % 4),
+                     "mirror owns a static range": lambda e: e.__setitem__((0, 3), 4),
                      "odd start": lambda e: (e.__setitem__((0, 0), 1), e.__setitem__((0, 1), 1)),
                      "mixed paths": lambda e: e.__setitem__((0, 2), 16)}.items():
         with pytest.raises(AssertionError):

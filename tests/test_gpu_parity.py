@@ -344,7 +344,7 @@ def test_stage_hook_arm_and_b_done(torch_gpu, table):
         log(f"  epoch {epoch}: arm code {want}, enqueue rc {rc}, arm calls {len(calls)}")
         assert rc == want
         assert len(calls) == epoch - 2
-        assert layer.backend.last_candidate() == (4 if table else 1)
+        assert layer.backend.last_candidate() == (4 if table else 5)
         assert start.elapsed_time(b_done) >= 0 and b_done.elapsed_time(end) >= 0
         assert layer.backend.complete() and layer.backend.status() == 0
         compare(layer.y32.cpu().numpy(), ref["y32"], f"stage hook epoch {epoch}")
@@ -357,14 +357,16 @@ def test_ready_pair_consumption_order(torch_gpu, key):
     """Candidate hip_fused_resident_pairs consumes the queue in LeanStream's ready pairs
     (backends/triton/persistent.py:59-90): static descriptor-index pairs (2w + 2kW, +1) when
     every position was published before the launch, claimed [head, min(head + 2, ready))
-    ranges of publication positions otherwise. Every logged range is checked (tests/claims.py),
-    every descriptor runs exactly once, and y is bit-identical to the default candidate's."""
+    ranges of publication positions otherwise (taken by the queue mirror as positions become
+    ready). Every logged range is checked (tests/claims.py), every descriptor runs exactly
+    once, y is bit-identical to the striped candidate's (hip_fused_resident), and the pair
+    candidate is the backend's default."""
     from claims import check_claim_log
 
     torch = torch_gpu
     cfg = synth.CONFIGS[key]
     log(f"case: ready-pair consumption order {cfg.name}")
-    base = DeviceLayer(cfg)
+    base = DeviceLayer(cfg, offline_table=[[1]])
     want = {}
     for publish in ("before", "delayed"):
         _queue_run(torch, base, 0, MODE_PROGRESSIVE, publish, epoch=3)
@@ -384,6 +386,11 @@ def test_ready_pair_consumption_order(torch_gpu, key):
         assert np.all(layer.executions.cpu().numpy() == 1)
         assert np.array_equal(layer.y32.cpu().numpy(), want[publish])
     layer.close()
+    default = DeviceLayer(cfg)
+    _queue_run(torch, default, 0, MODE_PROGRESSIVE, "delayed", epoch=5)
+    assert default.backend.last_candidate() == 5
+    assert np.array_equal(default.y32.cpu().numpy(), want["delayed"])
+    default.close()
 
 
 def test_queue_error_stops_after_published_prefix(torch_gpu):

@@ -99,13 +99,13 @@ def test_hip_selector_table_and_fallback():
     try:
         assert [lib.ls_hip_select(ctx, 0, b) for b in range(5)] == [0, 1, 2, 3, 4]
         default = lib.ls_hip_select(ctx, 0, 5)
-        assert default == 1
+        assert default == 5   # kHipDefault: the ready-pair candidate
         assert lib.ls_hip_select(ctx, 1, 0) == default and lib.ls_hip_select(ctx, 0, 6) == default
         assert lib.ls_hip_last_candidate(ctx) == -1      # nothing enqueued yet
     finally:
         lib.ls_hip_destroy(ctx)
     ctx = lib.ls_hip_create()
-    assert lib.ls_hip_select(ctx, 3, 3) == 1
+    assert lib.ls_hip_select(ctx, 3, 3) == 5
     lib.ls_hip_destroy(ctx)
 
 
