@@ -271,3 +271,48 @@ def test_rmsnorm_closed_forms_and_planted_mistake():
     normal = np.abs(got.astype(np.float32)) >= 2.0 ** -14
     assert normal.sum() > 4000
     assert np.array_equal(twice[normal], got.astype(np.float32)[normal] * 2)
+
+
+# ---------------------------------------------------------------- tolerance vs arithmetic
+def test_exact_products_leave_the_stated_tolerance_at_c2():
+    """Why the kernels form fp16(q*s) per weight (int4_format.py:21-28, streaming_mlp.cu:11-15)
+    instead of taking the scale and the nibble bias out of the sums: at the C2 shape
+    LeanStream's own per-weight rounding moves y32 further from exact arithmetic than the
+    stated max-abs 2e-2, so a kernel computing exact products (a factored dequantisation)
+    would fail the tolerance against the oracle, while one that rounds each weight like the
+    reference differs only by fp32 summation order. Exact products in float64: g and u of
+    every active neuron, its h with the reference's fp16 roundings, y = sum h * (q * s)."""
+    cfg = synth.CONFIGS["c2"]
+    hl = synth.host_layer(cfg)
+    logical = synth.active_groups(cfg)
+    rows = synth.descriptors(cfg, logical)
+    d, G = cfg.width, cfg.group_size
+    ref = oracle.layer(rows, len(rows), hl.cache, hl.scales, hl.x, d, G, threads=8)["y32"].astype(np.float64)
+    xv = hl.x.astype(np.float64)
+    gb, sw = cfg.group_bytes, G * 3 * (d // 128)
+    exact = np.zeros(d)
+    rounded = np.zeros(d)
+    for row in rows:
+        grp = hl.cache[int(row[2]) * gb:(int(row[2]) + 1) * gb].reshape(G, 3, d // 2)
+        sc = hl.scales[int(row[1]) * sw:(int(row[1]) + 1) * sw].reshape(G, 3, d // 128)
+        q = np.empty((G, 3, d), dtype=np.int8)
+        q[..., 0::2] = (grp & 15).astype(np.int8)
+        q[..., 1::2] = (grp >> 4).astype(np.int8)
+        q[q >= 8] -= 16
+        s = np.repeat(sc.astype(np.float32), 128, axis=2)
+        for name, w in (("exact", q * s.astype(np.float64)),
+                        ("rounded", (q.astype(np.float32) * s).astype(np.float16).astype(np.float64))):
+            g = (w[:, 0] @ xv).astype(np.float16).astype(np.float64)
+            u = (w[:, 1] @ xv).astype(np.float16).astype(np.float64)
+            silu = (g / (1.0 + np.exp(-g))).astype(np.float16).astype(np.float64)
+            h = (silu * u).astype(np.float16).astype(np.float64)
+            if name == "exact":
+                exact += h @ w[:, 2]
+            else:
+                rounded += h @ w[:, 2]
+    rel = lambda a: np.linalg.norm(a - ref) / np.linalg.norm(ref)
+    # per-weight rounding: the oracle's arithmetic up to summation order
+    assert rel(rounded) < 1e-5 and np.abs(rounded - ref).max() < 1e-3
+    # exact products: inside rel-L2 1e-3, outside max-abs 2e-2
+    assert rel(exact) < 1e-3
+    assert np.abs(exact - ref).max() > 2e-2
