@@ -41,8 +41,8 @@ def test_device_bf16_generator_matches_host(torch_gpu):
         layer.close()
 
 
-@pytest.mark.parametrize("key,rows", [("c1d32", None), ("c5", (0, 7, 16, 31))])
-def test_dense_layer_matches_oracle(torch_gpu, key, rows):
+@pytest.mark.parametrize("key", ["c1d32", "c5"])
+def test_dense_layer_matches_oracle(torch_gpu, key):
     torch = torch_gpu
     cfg = synth.CONFIGS[key]
     log(f"case: dense layer {cfg.name} k={cfg.active} batch={cfg.batch}")
@@ -60,7 +60,7 @@ def test_dense_layer_matches_oracle(torch_gpu, key, rows):
         assert np.all(layer.executions.cpu().numpy() == 1)
         hl = synth.host_layer(cfg)
         desc = layer.core_rows[0]
-        for b in (range(cfg.batch) if rows is None else rows):
+        for b in range(cfg.batch):
             ref = oracle.layer(desc, len(desc), hl.cache, hl.scales, hl.x[b * d:(b + 1) * d], d, cfg.group_size,
                                threads=8)
             compare(y32[b], ref["y32"], f"{cfg.name} row {b}")
