@@ -1080,6 +1080,50 @@ __device__ __forceinline__ bool wait_h_lanes(const MlpArgs& a, uint32_t* slot, c
     }
 }
 
+// The persistent kernels' ninth leading scalar: what a worker's first loads depend on beyond
+// the other eight -- the group size, the batch rows and whether the staged walk's down items
+// are whole tiles (MlpArgs::group_size <= 256, batch <= kMaxBatch, dn_tile).
+__host__ __device__ constexpr uint32_t launch_shape(uint32_t group_size, uint32_t batch, uint32_t dn_tile) {
+    return group_size | batch << 16 | (dn_tile == (uint32_t)kDnCols ? 1u << 31 : 0u);
+}
+__device__ __forceinline__ uint32_t shape_group(uint32_t shape) { return shape & 0xFFFFu; }
+__device__ __forceinline__ uint32_t shape_batch(uint32_t shape) { return (shape >> 16) & 0xFFu; }
+__device__ __forceinline__ bool shape_tiles(uint32_t shape) { return shape >> 31; }
+
+// The first descriptor batch of the resident range, fetched at the worker's start.
+struct Prefetched {
+    uint32_t word;
+    bool valid;
+};
+
+// The first descriptor batch of the resident range on the plain and packed walks, from the
+// preloaded arguments alone (process_items' item list for units [0, core_count): G neurons
+// per unit, nb batch rows, packs of 64 / G core units on the packed walk).
+template <int D, int NB, bool PACKED>
+__device__ __forceinline__ void prefetch_core_descs_plain(const ExecDesc* core, uint32_t core_count, uint32_t G,
+                                                          uint32_t batch, const WaveRole& role, Prefetched& p) {
+    using Gm = GuGeom<D>;
+    constexpr uint32_t T = D / kDnCols;
+    p.valid = false;
+    p.word = 0;
+    if (!core_count || !G) return;
+    const uint32_t nb = NB == 1 ? 1u : batch;
+    const uint32_t ipu = (G + Gm::NPI - 1) / Gm::NPI;
+    const uint32_t dnb = NB > 1 && nb > 1 && G <= (uint32_t)kDnRows ? 1u : nb;
+    const uint32_t P = PACKED ? (uint32_t)kDnRows / G : 1u;
+    const uint32_t NP = (core_count + P - 1) / P;
+    const ItemList il = make_items(role, core_count * ipu, NP * dnb * T);
+    if (!il.K) return;
+    const uint32_t count = min(il.K, (uint32_t)kDescItems);
+    const uint32_t lane = lane_id();
+    if (lane < 5 * count) {
+        const uint32_t j = lane / 5, w = lane - 5 * j;
+        const uint32_t g = item_unit(il.item(j), il.NG, ipu, T, dnb, P, core_count);
+        p.word = glb(reinterpret_cast<const uint32_t*>(core))[5 * g + w];
+    }
+    p.valid = true;
+}
+
 // Wave-uniform bookkeeping of an item in flight.
 struct ItemMeta {
     const uint8_t* grp;
@@ -1098,7 +1142,7 @@ template <int D, bool FUSED, int NB, bool PACKED>
 __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x4* stage, uint32_t* slot, const Bounds& b,
                                               unsigned long long* yacc, XPart<D>& xp, u32x4* xl, Epoch& ep,
                                               uint32_t early, Pending& pd, uint32_t u0, uint32_t u1,
-                                              const WaveRole& role) {
+                                              const WaveRole& role, const Prefetched& first) {
     using Gm = GuGeom<D>;
     constexpr uint32_t T = D / kDnCols;
     const uint32_t G = a.group_size;
@@ -1124,8 +1168,8 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
     uint32_t seen = 0;   // mirrored ready count this wave last observed
     // Descriptors first, then x: loads complete in issue order, so the first item's
     // address computation waits for the descriptors only.
-    uint32_t word = 0, k0 = 0;
-    if (!fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, dnb, word, P, nu))
+    uint32_t word = first.word, k0 = 0;
+    if (!first.valid && !fetch_descs(a, slot, u0, seen, il, 0, min(K, (uint32_t)kDescItems), ipu, T, dnb, word, P, nu))
         return leave(false);
     // x was loaded before the descriptors, so (in-order completion) it is in too
     stage_x<D>(xp, NB == 1 ? 1u : a.batch, xl, &sh.xcount);
@@ -1652,11 +1696,6 @@ __device__ __forceinline__ void gu_dots_staged(const u32x4* sl, const u32x4* xl,
     }
 }
 
-// The first descriptor batch of the resident range, fetched at the worker's start.
-struct Prefetched {
-    uint32_t word;
-    bool valid;
-};
 
 // Down items per unit of a staged range of nu units: 64-column quarters when every item
 // of the range gets a wave of its own (the 4 quarters of a tile on the 4 waves of a
@@ -1676,19 +1715,27 @@ __device__ __forceinline__ uint32_t staged_down_items(const WaveRole& r, uint32_
     return ng + 4 * T * nu <= r.nw ? 4 * T : T;
 }
 
+// From the preloaded arguments alone (core, core_count, dn_tile): resident units are never
+// waited for and never mirrored, so the batch is the fetch_descs one of the range's first
+// items, read from the core table.
 template <int D>
-__device__ __forceinline__ void prefetch_core_descs(const MlpArgs& a, uint32_t* slot, const WaveRole& role,
-                                                    Prefetched& p) {
+__device__ __forceinline__ void prefetch_core_descs(const ExecDesc* core, uint32_t core_count, uint32_t dn_tile,
+                                                    const WaveRole& role, Prefetched& p) {
     constexpr uint32_t ipu = kStagedGroup / GuGeom<D>::NPI;
     p.valid = false;
     p.word = 0;
-    if (!a.core_count) return;
-    const uint32_t TQ = staged_down_items<D>(role, a.core_count, a.dn_tile);
-    const ItemList il = make_staged_items(role, a.core_count * ipu, a.core_count * TQ);
+    if (!core_count) return;
+    const uint32_t TQ = staged_down_items<D>(role, core_count, dn_tile);
+    const ItemList il = make_staged_items(role, core_count * ipu, core_count * TQ);
     if (!il.K) return;
-    uint32_t seen = 0;
-    // resident units are never waited for: this cannot fail
-    p.valid = fetch_descs(a, slot, 0, seen, il, 0, min(il.K, (uint32_t)kDescItems), ipu, TQ, 1u, p.word);
+    const uint32_t count = min(il.K, (uint32_t)kDescItems);
+    const uint32_t lane = lane_id();
+    if (lane < 5 * count) {
+        const uint32_t j = lane / 5, w = lane - 5 * j;
+        const uint32_t g = item_unit(il.item(j), il.NG, ipu, TQ, 1u);
+        p.word = glb(reinterpret_cast<const uint32_t*>(core))[5 * g + w];
+    }
+    p.valid = true;
 }
 
 // This wave's items of units [u0, u1) through its two LDS slots (stage: kWaves x 2 slots).

@@ -35,6 +35,7 @@
 // write-back). Every wait is bounded by a wall-clock limit; on expiry the status word
 // records a timeout and every worker leaves.
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 #include "mlp_args.h"
 #include "mlp_launch.h"
@@ -55,25 +56,45 @@ namespace lsamd {
 // most 32 neurons at batch 1: the plain walk with down items over packs of core units).
 enum Walk : int { kWalkPlain = 0, kWalkStaged = 1, kWalkPacked = 2 };
 
-template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, int WALK>
-__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, u32x4* stage,
-                                       uint32_t* slot) {
-    constexpr bool STAGED = WALK == kWalkStaged;
-    const uint32_t W = QUEUE ? a.grid - 1 : a.grid;
-    const uint32_t wave = wave_id();
+// A worker's first loads, from the preloaded arguments only (the kernel then reads its
+// argument block): its role, x (one row at batch 1) and, on the staged walk, the first
+// descriptor batch of the resident range.
+template <int D>
+struct WorkerStart {
+    WaveRole role;
+    XPart<D> xp;
+    Prefetched first;
+};
+
+template <int D, bool CORE, bool QUEUE, int NB, int WALK>
+__device__ __forceinline__ void start_worker(const uint16_t* x, const ExecDesc* core, uint32_t core_count,
+                                             uint32_t grid, uint32_t shape, u32x4* xl, WorkerStart<D>& st) {
+    const uint32_t W = QUEUE ? grid - 1 : grid;
     // Roles by workgroup: the first gu_wgs workgroups take the gate/up items, the others
     // the down items (one workgroup alone takes both).
     const uint32_t gu_wgs = kSplitRoles && W >= 2 ? (W + 1) / 2 : 0;
-    const WaveRole role{blockIdx.x * kWaves + wave, W * kWaves, gu_wgs * kWaves};
+    st.role = WaveRole{blockIdx.x * kWaves + wave_id(), W * kWaves, gu_wgs * kWaves};
+    const uint32_t G = shape_group(shape), batch = shape_batch(shape);
+    load_x<D>(x, NB == 1 ? 1u : batch, st.xp, xl);   // the NB = 1 kernels hold one row of x
+    st.first = Prefetched{0, false};
+    if constexpr (CORE) {
+        if constexpr (WALK == kWalkStaged)
+            prefetch_core_descs<D>(core, core_count, shape_tiles(shape) ? kDnCols : 0u, st.role, st.first);
+        else
+            prefetch_core_descs_plain<D, NB, WALK == kWalkPacked>(core, core_count, G, batch, st.role, st.first);
+    }
+}
+
+template <int D, bool FUSED, bool CORE, bool QUEUE, int NB, int WALK>
+__device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared& sh, u32x4* xl, u32x4* stage,
+                                       uint32_t* slot, WorkerStart<D>& st) {
+    constexpr bool STAGED = WALK == kWalkStaged;
+    const WaveRole role = st.role;
+    const uint32_t W = QUEUE ? a.grid - 1 : a.grid;
+    const uint32_t wave = wave_id();
     unsigned long long* yacc = launch_acc(a);
-    XPart<D> xp;
-    const uint32_t xrows = NB == 1 ? 1u : a.batch;   // the NB = 1 kernels hold one row of x
-    load_x<D>(a.x, xrows, xp, xl);
-    // The staged walk's first descriptors of the resident range go out with x, before the
-    // workgroup's first barrier: that barrier also waits for the argument block's scalar
-    // loads, which the loads above (preloaded arguments only) do not need.
-    Prefetched first{};
-    if constexpr (STAGED && CORE) prefetch_core_descs<D>(a, slot, role, first);
+    XPart<D>& xp = st.xp;
+    Prefetched first = st.first;
     Epoch ep = {0, 0, 0, 0};
     Pending pd;
     pd.col = -1;
@@ -128,7 +149,8 @@ __device__ __forceinline__ void worker(const MlpArgs& a, const Bounds& b, Shared
                 first.valid = false;   // only the resident range's first batch is prefetched
             } else {
                 ok = process_items<D, FUSED, NB, WALK == kWalkPacked>(a, sh, stage, slot, b, yacc, xp, xl, ep, e, pd,
-                                                                      u0, u1, r);
+                                                                      u0, u1, r, first);
+                first.valid = false;
             }
         }
     }
@@ -224,13 +246,14 @@ struct StageArea {
 };
 
 // The arguments a persistent worker needs before its first loads (x, its descriptors,
-// the weight arenas, its ring slot, the grid) lead the kernel's argument list as scalars,
-// so they can be preloaded into SGPRs at wave start (-amdgpu-kernarg-preload-count); the
-// block of the remaining arguments is read from the kernel-argument segment while the
-// first loads are in flight.
+// the weight arenas, its ring slot, the grid, the launch shape) lead the kernel's argument
+// list as scalars, so they can be preloaded into SGPRs at wave start
+// (-amdgpu-kernarg-preload-count); the blocks of the remaining arguments are read from
+// the kernel-argument segment (late_params) once x and the first descriptors are in flight.
 #define LS_HOT_PARAMS                                                                                     \
     const uint16_t *hot_x, const ExecDesc *hot_core, const uint8_t *hot_cache, const uint16_t *hot_scales, \
-        uint32_t *slot, uint32_t hot_core_count, uint32_t hot_seq, uint32_t hot_grid, MlpArgs args, Bounds b
+        uint32_t *slot, uint32_t hot_core_count, uint32_t hot_seq, uint32_t hot_grid, uint32_t hot_shape,     \
+        MlpArgs args, Bounds b
 __device__ __forceinline__ MlpArgs with_hot(const MlpArgs& args, const uint16_t* x, const ExecDesc* core,
                                             const uint8_t* cache, const uint16_t* scales, uint32_t core_count,
                                             uint32_t seq, uint32_t grid) {
@@ -244,25 +267,62 @@ __device__ __forceinline__ MlpArgs with_hot(const MlpArgs& args, const uint16_t*
     a.grid = grid;
     return a;
 }
+
+// The persistent kernels' argument segment: LS_HOT_PARAMS in order, each at its natural
+// alignment (the code object's argument offsets: args at 56, b at 336).
+struct PersistentParams {
+    const uint16_t* x;
+    const ExecDesc* core;
+    const uint8_t* cache;
+    const uint16_t* scales;
+    uint32_t* slot;
+    uint32_t core_count, seq, grid, shape;
+    MlpArgs args;
+    Bounds b;
+};
+static_assert(offsetof(PersistentParams, args) == 56 && offsetof(PersistentParams, b) == 336,
+              "argument segment layout of LS_HOT_PARAMS");
+
+// The argument blocks, read where this is called. The compiler loads a kernel's arguments
+// at its entry, and the ones it then keeps in vector lanes (more scalars than fit) make the
+// wave wait for those loads there, before anything else is issued. Read through an address
+// the compiler cannot see through, the blocks' loads follow the ones issued before this call.
+__device__ __forceinline__ const PersistentParams* late_params() {
+#ifdef __HIP_DEVICE_COMPILE__
+    uint64_t p = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
+    asm volatile("" : "+s"(p));
+    // a constant-address-space pointer: the loads through it stay scalar loads
+    return (const PersistentParams*)reinterpret_cast<const __attribute__((address_space(4))) PersistentParams*>(p);
+#else
+    return nullptr;
+#endif
+}
 // `slot` (this launch's ring slot, sync + (seq & 1) slot_words) is a parameter of its own.
-#define LS_HOT_ARGS with_hot(args, hot_x, hot_core, hot_cache, hot_scales, hot_core_count, hot_seq, hot_grid)
+#define LS_HOT_ARGS                                                                                   \
+    with_hot(late_params()->args, hot_x, hot_core, hot_cache, hot_scales, hot_core_count, hot_seq, hot_grid)
+#define LS_LATE_BOUNDS Bounds(late_params()->b)
+#define LS_WORKER_START(CORE, QUEUE) \
+    start_worker<D, CORE, QUEUE, NB, WALK>(hot_x, hot_core, hot_core_count, hot_grid, hot_shape, xl, st)
 
 // Fused layer: resident (core) units, queue consumption and the compact reduction (the
 // contribution completing a column writes it), one persistent launch.
 template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_PARAMS) {
     static_assert(WALK == kWalkPlain || NB == 1, "the staged and packed walks serve batch 1");
-    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
-    if (blockIdx.x == a.grid - 1) {
+    if (blockIdx.x == hot_grid - 1) {
+        const MlpArgs a = LS_HOT_ARGS;
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         if (threadIdx.x < 64) await_workers(a, slot, a.grid - 1);
     } else {
+        WorkerStart<D> st;
+        LS_WORKER_START(true, true);
+        const MlpArgs a = LS_HOT_ARGS;
         stamp(a, kStampEntry);
-        worker<D, true, true, true, NB, WALK>(a, b, sh, xl, stage, slot);
+        worker<D, true, true, true, NB, WALK>(a, LS_LATE_BOUNDS, sh, xl, stage, slot, st);
         stamp(a, kStampExit);
         count_out(slot);
     }
@@ -271,26 +331,31 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_
 // Split path, stage A: resident (core) units only; no queue, no conversion.
 template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_a_kernel(LS_HOT_PARAMS) {
-    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
-    worker<D, false, true, false, NB, WALK>(a, b, sh, xl, stage, slot);
+    WorkerStart<D> st;
+    LS_WORKER_START(true, false);
+    const MlpArgs a = LS_HOT_ARGS;
+    worker<D, false, true, false, NB, WALK>(a, LS_LATE_BOUNDS, sh, xl, stage, slot, st);
 }
 
 // Split path, stage B: persistent ready-queue consumer (last block mirrors).
 template <int D, int NB, int WALK>
 __global__ __launch_bounds__(kThreads, kWgPerCu) void stage_b_kernel(LS_HOT_PARAMS) {
-    const MlpArgs a = LS_HOT_ARGS;
     __shared__ Shared sh;
     __shared__ u32x4 xl[NB * XGeom<D>::N];
     __shared__ u32x4 stage[StageArea<WALK == kWalkStaged, NB>::VECS];
-    if (blockIdx.x == a.grid - 1) {
+    if (blockIdx.x == hot_grid - 1) {
+        const MlpArgs a = LS_HOT_ARGS;
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
         return;
     }
-    worker<D, false, false, true, NB, WALK>(a, b, sh, xl, stage, slot);
+    WorkerStart<D> st;
+    LS_WORKER_START(false, true);
+    const MlpArgs a = LS_HOT_ARGS;
+    worker<D, false, false, true, NB, WALK>(a, LS_LATE_BOUNDS, sh, xl, stage, slot, st);
 }
 
 // Split path, compact reduction (streaming_mlp.cu:80-84): converts every column's
@@ -841,7 +906,8 @@ hipError_t launch_layer(const LaunchPlan& p, const MlpArgs& args, const Bounds& 
     // the persistent kernels' leading scalars (LS_HOT_PARAMS), then the argument blocks
     uint32_t grid = (uint32_t)p.workers + 1;
     uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    void* kargs[] = {&a.x, &a.core, &a.cache, &a.scales, &slot, &a.core_count, &a.seq, &grid, &a, &b};
+    uint32_t shape = launch_shape(a.group_size, a.batch, a.dn_tile);
+    void* kargs[] = {&a.x, &a.core, &a.cache, &a.scales, &slot, &a.core_count, &a.seq, &grid, &shape, &a, &b};
     if (p.entry_point == kEntryFused) {
         a.grid = grid;
         const hipError_t e = hipLaunchKernel(v->fused[nb], dim3(grid), dim3(kThreads), kargs, 0, stream);

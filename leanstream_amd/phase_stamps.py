@@ -138,11 +138,12 @@ def main():
     ap.add_argument("--workload", default="c2", help="a layer configuration, or chain / c1chain")
     ap.add_argument("--reps", type=int, default=10)
     ap.add_argument("--layers", type=int, default=36, help="chain workloads: layers per launch")
+    ap.add_argument("--copies", type=int, default=8, help="layer copies the warm launches rotate over")
     a = ap.parse_args()
     if a.workload in ("chain", "c1chain"):
         chain_main(a)
         return
-    cfg, waves, status, phases, spans, reps = timeline(a.workload, a.reps)
+    cfg, waves, status, phases, spans, reps = timeline(a.workload, a.reps, copies=a.copies)
     print(f"{cfg.name}: {waves} waves, status {status}; µs after the first wave's start")
     print("| phase | waves per launch | p10 | p50 | p90 | max |")
     print("|---|---|---|---|---|---|")
