@@ -287,16 +287,18 @@ static_assert(offsetof(PersistentParams, args) == 56 && offsetof(PersistentParam
 // at its entry, and the ones it then keeps in vector lanes (more scalars than fit) make the
 // wave wait for those loads there, before anything else is issued. Read through an address
 // the compiler cannot see through, the blocks' loads follow the ones issued before this call.
-__device__ __forceinline__ const PersistentParams* late_params() {
+template <class P>
+__device__ __forceinline__ const P* late_params_as() {
 #ifdef __HIP_DEVICE_COMPILE__
     uint64_t p = reinterpret_cast<uint64_t>(__builtin_amdgcn_kernarg_segment_ptr());
     asm volatile("" : "+s"(p));
     // a constant-address-space pointer: the loads through it stay scalar loads
-    return (const PersistentParams*)reinterpret_cast<const __attribute__((address_space(4))) PersistentParams*>(p);
+    return (const P*)reinterpret_cast<const __attribute__((address_space(4))) P*>(p);
 #else
     return nullptr;
 #endif
 }
+__device__ __forceinline__ const PersistentParams* late_params() { return late_params_as<PersistentParams>(); }
 // `slot` (this launch's ring slot, sync + (seq & 1) slot_words) is a parameter of its own.
 #define LS_HOT_ARGS                                                                                   \
     with_hot(late_params()->args, hot_x, hot_core, hot_cache, hot_scales, hot_core_count, hot_seq, hot_grid)
@@ -440,12 +442,14 @@ __device__ __forceinline__ uint32_t x16_piece(uint32_t row, uint32_t c) {   // 1
     return 64 * f + l;
 }
 
-__global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
-    const uint32_t D = a.width, groups = D / 8;
+// Its arguments are scalars preloaded into SGPRs: the load goes out at once.
+__global__ __launch_bounds__(kThreads) void dense_x_kernel(const uint16_t* x, uint16_t* x16, uint32_t width,
+                                                           uint32_t batch) {
+    const uint32_t D = width, groups = D / 8;
     const uint32_t idx = blockIdx.x * kThreads + threadIdx.x;   // row * groups + group
     const uint32_t row = idx / groups, grp = idx - row * groups;
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (row < a.batch) v = *reinterpret_cast<const u32x4*>(a.x + (size_t)row * D + 8 * grp);
+    if (row < batch) v = *glb(reinterpret_cast<const u32x4*>(x + (size_t)row * D + 8 * grp));
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
     h8 o;
 #pragma unroll
@@ -453,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
         o[2 * i] = bf16_to_f16((w[i >> 1] >> (16 * (i & 1))) & 0xffffu);
         o[2 * i + 1] = bf16_to_f16((w[(i + 4) >> 1] >> (16 * (i & 1))) & 0xffffu);
     }
-    reinterpret_cast<h8*>(a.x16)[x16_piece(row, 8 * grp)] = o;
+    glb(reinterpret_cast<h8*>(x16))[x16_piece(row, 8 * grp)] = o;
 }
 
 // Gate/up of one 32-neuron half of one unit for all batch rows. Wave w reduces the
@@ -463,35 +467,52 @@ __global__ __launch_bounds__(kThreads) void dense_x_kernel(MlpArgs a) {
 // d = 4096 the kernel stays within 128 registers (four waves per SIMD: two workgroups per
 // CU, so the whole layer's workgroups are resident at once) with the weights of
 // kDenseGuWindow steps in flight per wave.
+// The dense kernels' argument segments (each parameter at its natural alignment): the
+// leading scalars are preloaded into SGPRs, the blocks are read late (late_params_as).
+struct DenseGuParams {
+    const ExecDesc* core;
+    const uint16_t* x16;
+    MlpArgs args;
+    Bounds b;
+};
+static_assert(offsetof(DenseGuParams, args) == 16 && offsetof(DenseGuParams, b) == 296,
+              "argument segment layout of dense_gate_up_kernel");
+
+// The unit's descriptor and the first x16 steps go out from the preloaded arguments; the
+// argument blocks are read behind them.
 template <int NI>
-__global__ __launch_bounds__(64 * kDenseGuWaves, NI <= 8 ? 4 : 2) void dense_gate_up_kernel(MlpArgs a, Bounds b) {
+__global__ __launch_bounds__(64 * kDenseGuWaves, NI <= 8 ? 4 : 2) void dense_gate_up_kernel(
+    const ExecDesc* hot_core, const uint16_t* hot_x16, MlpArgs args, Bounds b) {
     __shared__ float red[kDenseGuWaves / 2][2][16][64];   // 32 KB: two workgroups per CU fit
     constexpr uint32_t D = NI * 64 * kDenseGuWaves;
     constexpr uint32_t kq = D / kDenseGuWaves;
-    const uint32_t G = a.group_size;
     const uint32_t unit = blockIdx.x >> 1, half = blockIdx.x & 1;
-    const Unit u = resolve(a, b, a.core[unit], (int)D);
+    const ExecDesc desc = hot_core[unit];
     const int lane = lane_id();
     const uint32_t w = wave_id();
     const uint32_t n = half * 32 + (lane & 31), hh = lane >> 5, row = lane & 31;
+    // x16 of step t (four 16-byte fragments per lane, each wave-contiguous) is loaded two
+    // steps ahead, from a ring of three; steps 0 and 1 go out before the weights. Loads
+    // complete in issue order, so each step waits only for what it uses.
+    const LS_GLOBAL u32x4* xf = glb(reinterpret_cast<const u32x4*>(hot_x16));
+    u32x4 xq[3][4];
+    auto issue_x = [&](int t, u32x4 (&dst)[4]) {
+        const uint32_t k0 = w * kq + 64 * t + 32 * hh;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dst[j] = xf[x16_piece(row, k0 + 8 * j)];
+    };
+    issue_x(0, xq[0]);
+    if (NI > 1) issue_x(1, xq[1]);
+    const MlpArgs a = late_params_as<DenseGuParams>()->args;
+    const Bounds bd = late_params_as<DenseGuParams>()->b;
+    const uint32_t G = a.group_size;
+    const Unit u = resolve(a, bd, desc, (int)D);
     f32x16 cg = {}, cu = {};
     if (u.ok) {
         const uint8_t* wg = u.grp + (size_t)(n * 3) * (D / 2);
         const uint8_t* wu = wg + D / 2;
         const uint16_t* sg = u.sc + (size_t)(n * 3) * (D / 128);
         const uint16_t* su = sg + D / 128;
-        const u32x4* xf = reinterpret_cast<const u32x4*>(a.x16);
-        // x16 of step t (four 16-byte fragments per lane, each wave-contiguous) is loaded
-        // two steps ahead, from a ring of three; steps 0 and 1 go out before the weights.
-        // Loads complete in issue order, so each step waits only for what it uses.
-        u32x4 xq[3][4];
-        auto issue_x = [&](int t, u32x4 (&dst)[4]) {
-            const uint32_t k0 = w * kq + 64 * t + 32 * hh;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dst[j] = xf[x16_piece(row, k0 + 8 * j)];
-        };
-        issue_x(0, xq[0]);
-        if (NI > 1) issue_x(1, xq[1]);
         // The weights of WIN steps are in flight: step t's pieces go out into the slot
         // step t - WIN has just been computed from.
         constexpr int WIN = NI < kDenseGuWindow ? NI : kDenseGuWindow;
@@ -615,12 +636,11 @@ struct DenseDnLoad {
 // at the first word of the h rows for every lane (one line per instruction instead of a
 // unit's 8 KB tile again; the h rows are not written by this kernel), with ok = false.
 // h rows >= batch are zero (cleared at bind).
-__device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b, uint32_t un, uint32_t u0,
-                                               uint32_t u1, uint32_t c0, DenseDnLoad& L) {
+__device__ __forceinline__ void dense_dn_issue_desc(const MlpArgs& a, const Bounds& b, ExecDesc d, bool in, uint32_t c0,
+                                                    DenseDnLoad& L) {
     const uint32_t D = a.width, G = a.group_size, t = threadIdx.x;
     const uint32_t nq = t >> 5, o = t & 31, hr = t >> 4, hp = t & 15;
-    const bool in = un < u1;
-    const Unit u = resolve(a, b, a.core[in ? un : u0], (int)D);
+    const Unit u = resolve(a, b, d, (int)D);
     L.ok = in && u.ok;   // an invalid descriptor is reported by the gate/up kernel
     const uint8_t* grp = L.ok ? u.grp : reinterpret_cast<const uint8_t*>(a.h16);
     const uint16_t* sc = L.ok ? u.sc : a.h16;
@@ -633,6 +653,12 @@ __device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b
         L.sb[r] = sc[on * ((size_t)(n * 3 + 2) * (D / 128) + col / 128)];
     }
     L.hv = *reinterpret_cast<const u32x2*>(a.h16 + on * ((size_t)hr * a.slot_capacity * G + u.dest * G + 4 * hp));
+}
+
+__device__ __forceinline__ void dense_dn_issue(const MlpArgs& a, const Bounds& b, uint32_t un, uint32_t u0,
+                                               uint32_t u1, uint32_t c0, DenseDnLoad& L) {
+    const bool in = un < u1;
+    dense_dn_issue_desc(a, b, a.core[in ? un : u0], in, c0, L);
 }
 
 // LDS position (in halves) of the 8-neuron granule gr of tile column col: rows of 64
@@ -651,10 +677,24 @@ __device__ __forceinline__ uint32_t dn_tile_pos(uint32_t col, uint32_t gr) {
 // read) and stages the unit's h rows; wave w then runs four MFMAs for columns
 // 32 w .. 32 w + 31. The loads of the next kDensePrefetch units are in flight while a
 // unit is computed.
-__global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs a, Bounds b) {
+struct DenseDnParams {
+    const ExecDesc* core;
+    uint32_t core_count, dsplits, width;
+    MlpArgs args;
+    Bounds b;
+};
+static_assert(offsetof(DenseDnParams, args) == 24 && offsetof(DenseDnParams, b) == 304,
+              "argument segment layout of dense_down_kernel");
+
+// The split's first descriptors go out from the preloaded arguments; the argument blocks
+// are read behind them.
+__global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(const ExecDesc* hot_core,
+                                                                        uint32_t hot_core_count,
+                                                                        uint32_t hot_dsplits, uint32_t hot_width,
+                                                                        MlpArgs args, Bounds b) {
     __shared__ alignas(16) _Float16 wl[kDenseCols * 64];
     __shared__ alignas(16) _Float16 hl[32][kDensePitch];
-    const uint32_t D = a.width;
+    const uint32_t D = hot_width;
     const uint32_t tiles = D / kDenseCols;
     // XCD-aware order: workgroup blk runs on XCD blk % 8; the tiles of a split go to one
     // XCD (kDenseSplits is a multiple of 8), so the split's h rows and down-scale lines
@@ -663,8 +703,13 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs 
     const uint32_t xcd = blockIdx.x % 8u, j = blockIdx.x / 8u;
     const uint32_t split = xcd + 8u * (j / tiles), ct = j % tiles;
     const uint32_t c0 = ct * kDenseCols;
-    const uint32_t per = (a.core_count + a.dsplits - 1) / a.dsplits;
-    const uint32_t u0 = min(a.core_count, split * per), u1 = min(a.core_count, u0 + per);
+    const uint32_t per = (hot_core_count + hot_dsplits - 1) / hot_dsplits;
+    const uint32_t u0 = min(hot_core_count, split * per), u1 = min(hot_core_count, u0 + per);
+    ExecDesc first[kDensePrefetch];
+#pragma unroll
+    for (int s = 0; s < kDensePrefetch; ++s) first[s] = hot_core[u0 + s < u1 ? u0 + s : min(u0, u1 - 1)];
+    const MlpArgs a = late_params_as<DenseDnParams>()->args;
+    const Bounds bd = late_params_as<DenseDnParams>()->b;
     const uint32_t t = threadIdx.x;
     const int lane = lane_id();
     const uint32_t w = wave_id();
@@ -674,7 +719,7 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs 
     DenseDnLoad buf[kDensePrefetch];
     if (u0 < u1) {
 #pragma unroll
-        for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue(a, b, u0 + s, u0, u1, c0, buf[s]);
+        for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue_desc(a, bd, first[s], u0 + s < u1, c0, buf[s]);
         for (uint32_t base = u0; base < u1; base += kDensePrefetch) {
 #pragma unroll
             for (int s = 0; s < kDensePrefetch; ++s) {
@@ -708,7 +753,7 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs 
                         acc = mfma32(ha, wb, acc);
                     }
                 }
-                dense_dn_issue(a, b, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
+                dense_dn_issue(a, bd, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
             }
         }
     }
@@ -744,9 +789,22 @@ __device__ __forceinline__ void check_dense_queue(const MlpArgs& a, uint32_t* sl
     }
 }
 
-__global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
-    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
-    if (blockIdx.x == gridDim.x - 1) {
+struct DenseReduceParams {
+    const float* dpart;
+    uint32_t width, batch, dsplits;
+    MlpArgs args;
+};
+static_assert(offsetof(DenseReduceParams, args) == 24, "argument segment layout of dense_reduce_kernel");
+
+// The column blocks' split loads go out from the preloaded arguments; the argument block is
+// read behind them.
+__global__ __launch_bounds__(kThreads) void dense_reduce_kernel(const float* hot_dpart, uint32_t hot_width,
+                                                                uint32_t hot_batch, uint32_t hot_dsplits,
+                                                                MlpArgs args) {
+    // the launch's last block (the column blocks are counted from the preloaded arguments)
+    if (blockIdx.x == (hot_batch * hot_width / 4 + kThreads - 1) / kThreads) {
+        const MlpArgs a = late_params_as<DenseReduceParams>()->args;
+        uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
         // The last block only clears the next launch's ring slot (its last user, the previous
         // launch, has finished: stream order) and checks the layer's queue (a read of host
         // memory), in parallel with the column blocks; this kernel runs in every dense
@@ -760,14 +818,16 @@ __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
     // four consecutive columns of one row per thread (width is a multiple of 256): every
     // split's 16-byte load in flight
     const uint32_t idx = 4 * (blockIdx.x * kThreads + threadIdx.x);   // row * D + column
-    if (idx < a.batch * a.width) {
-        const uint32_t tk = idx / a.width, col = idx - tk * a.width;
-        float4 v = {0.f, 0.f, 0.f, 0.f};
-        if (a.dsplits == kDenseSplits) {
+    const uint32_t W = hot_width;
+    const LS_GLOBAL float4* parts = glb(reinterpret_cast<const float4*>(hot_dpart));
+    float4 v = {0.f, 0.f, 0.f, 0.f};
+    const bool mine = idx < hot_batch * W;
+    if (mine) {
+        const uint32_t tk = idx / W, col = idx - tk * W;
+        if (hot_dsplits == kDenseSplits) {
             float4 p[kDenseSplits];
 #pragma unroll
-            for (uint32_t s = 0; s < kDenseSplits; ++s)
-                p[s] = *reinterpret_cast<const float4*>(a.dpart + ((size_t)s * 32 + tk) * a.width + col);
+            for (uint32_t s = 0; s < kDenseSplits; ++s) p[s] = parts[(((size_t)s * 32 + tk) * W + col) / 4];
 #pragma unroll
             for (uint32_t s = 0; s < kDenseSplits; ++s) {
                 v.x += p[s].x;
@@ -776,14 +836,18 @@ __global__ __launch_bounds__(kThreads) void dense_reduce_kernel(MlpArgs a) {
                 v.w += p[s].w;
             }
         } else {
-            for (uint32_t s = 0; s < a.dsplits; ++s) {
-                const float4 q = *reinterpret_cast<const float4*>(a.dpart + ((size_t)s * 32 + tk) * a.width + col);
+            for (uint32_t s = 0; s < hot_dsplits; ++s) {
+                const float4 q = parts[(((size_t)s * 32 + tk) * W + col) / 4];
                 v.x += q.x;
                 v.y += q.y;
                 v.z += q.z;
                 v.w += q.w;
             }
         }
+    }
+    const MlpArgs a = late_params_as<DenseReduceParams>()->args;
+    uint32_t* slot = a.sync + (a.seq & 1) * a.slot_words;
+    if (mine) {
         if (a.y32) *reinterpret_cast<float4*>(a.y32 + idx) = v;
         const uint32_t lo = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.x) |
                             (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v.y) << 16;
@@ -951,22 +1015,27 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
     if (a.group_size != 64 || !gate_up || a.batch <= kMaxBatch || a.batch > kMaxDenseBatch || !a.dsplits ||
         !a.h16 || !a.dpart || !a.x16)
         return hipErrorInvalidValue;
-    void* kargs[] = {&a, &b};
-    void* rargs[] = {&a};
     hipError_t e = hipSuccess;
     if (a.core_count) {
+        uint16_t* x16 = a.x16;
+        void* xargs[] = {&a.x, &x16, &a.width, &a.batch};
         e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_x_kernel), dim3(32 * a.width / 8 / kThreads),
-                            dim3(kThreads), rargs, 0, stream);
+                            dim3(kThreads), xargs, 0, stream);
+        const uint16_t* cx16 = a.x16;
+        void* gargs[] = {&a.core, &cx16, &a, &b};
         if (e == hipSuccess)
-            e = hipLaunchKernel(gate_up, dim3(2 * a.core_count), dim3(64 * kDenseGuWaves), kargs, 0, stream);
+            e = hipLaunchKernel(gate_up, dim3(2 * a.core_count), dim3(64 * kDenseGuWaves), gargs, 0, stream);
+        void* dargs[] = {&a.core, &a.core_count, &a.dsplits, &a.width, &a, &b};
         if (e == hipSuccess)
             e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_down_kernel),
-                                dim3(a.width / kDenseCols * a.dsplits), dim3(64 * kDenseDnWaves), kargs, 0, stream);
+                                dim3(a.width / kDenseCols * a.dsplits), dim3(64 * kDenseDnWaves), dargs, 0, stream);
     } else {
         a.dsplits = 0;   // nothing to sum: y = 0
     }
     if (e != hipSuccess) return e;
     // four columns per thread, plus one block for the ring slot and the queue check
+    const float* dpart = a.dpart;
+    void* rargs[] = {&dpart, &a.width, &a.batch, &a.dsplits, &a};
     return hipLaunchKernel(reinterpret_cast<const void*>(&dense_reduce_kernel),
                            dim3((a.batch * a.width / 4 + kThreads - 1) / kThreads + 1), dim3(kThreads), rargs, 0,
                            stream);
