@@ -677,24 +677,10 @@ __device__ __forceinline__ uint32_t dn_tile_pos(uint32_t col, uint32_t gr) {
 // read) and stages the unit's h rows; wave w then runs four MFMAs for columns
 // 32 w .. 32 w + 31. The loads of the next kDensePrefetch units are in flight while a
 // unit is computed.
-struct DenseDnParams {
-    const ExecDesc* core;
-    uint32_t core_count, dsplits, width;
-    MlpArgs args;
-    Bounds b;
-};
-static_assert(offsetof(DenseDnParams, args) == 24 && offsetof(DenseDnParams, b) == 304,
-              "argument segment layout of dense_down_kernel");
-
-// The split's first descriptors go out from the preloaded arguments; the argument blocks
-// are read behind them.
-__global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(const ExecDesc* hot_core,
-                                                                        uint32_t hot_core_count,
-                                                                        uint32_t hot_dsplits, uint32_t hot_width,
-                                                                        MlpArgs args, Bounds b) {
+__global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(MlpArgs a, Bounds b) {
     __shared__ alignas(16) _Float16 wl[kDenseCols * 64];
     __shared__ alignas(16) _Float16 hl[32][kDensePitch];
-    const uint32_t D = hot_width;
+    const uint32_t D = a.width;
     const uint32_t tiles = D / kDenseCols;
     // XCD-aware order: workgroup blk runs on XCD blk % 8; the tiles of a split go to one
     // XCD (kDenseSplits is a multiple of 8), so the split's h rows and down-scale lines
@@ -703,13 +689,8 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(const Ex
     const uint32_t xcd = blockIdx.x % 8u, j = blockIdx.x / 8u;
     const uint32_t split = xcd + 8u * (j / tiles), ct = j % tiles;
     const uint32_t c0 = ct * kDenseCols;
-    const uint32_t per = (hot_core_count + hot_dsplits - 1) / hot_dsplits;
-    const uint32_t u0 = min(hot_core_count, split * per), u1 = min(hot_core_count, u0 + per);
-    ExecDesc first[kDensePrefetch];
-#pragma unroll
-    for (int s = 0; s < kDensePrefetch; ++s) first[s] = hot_core[u0 + s < u1 ? u0 + s : min(u0, u1 - 1)];
-    const MlpArgs a = late_params_as<DenseDnParams>()->args;
-    const Bounds bd = late_params_as<DenseDnParams>()->b;
+    const uint32_t per = (a.core_count + a.dsplits - 1) / a.dsplits;
+    const uint32_t u0 = min(a.core_count, split * per), u1 = min(a.core_count, u0 + per);
     const uint32_t t = threadIdx.x;
     const int lane = lane_id();
     const uint32_t w = wave_id();
@@ -719,7 +700,7 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(const Ex
     DenseDnLoad buf[kDensePrefetch];
     if (u0 < u1) {
 #pragma unroll
-        for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue_desc(a, bd, first[s], u0 + s < u1, c0, buf[s]);
+        for (int s = 0; s < kDensePrefetch; ++s) dense_dn_issue(a, b, u0 + s, u0, u1, c0, buf[s]);
         for (uint32_t base = u0; base < u1; base += kDensePrefetch) {
 #pragma unroll
             for (int s = 0; s < kDensePrefetch; ++s) {
@@ -753,7 +734,7 @@ __global__ __launch_bounds__(64 * kDenseDnWaves) void dense_down_kernel(const Ex
                         acc = mfma32(ha, wb, acc);
                     }
                 }
-                dense_dn_issue(a, bd, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
+                dense_dn_issue(a, b, base + kDensePrefetch + s, u0, u1, c0, buf[s]);
             }
         }
     }
@@ -1025,7 +1006,7 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
         void* gargs[] = {&a.core, &cx16, &a, &b};
         if (e == hipSuccess)
             e = hipLaunchKernel(gate_up, dim3(2 * a.core_count), dim3(64 * kDenseGuWaves), gargs, 0, stream);
-        void* dargs[] = {&a.core, &a.core_count, &a.dsplits, &a.width, &a, &b};
+        void* dargs[] = {&a, &b};
         if (e == hipSuccess)
             e = hipLaunchKernel(reinterpret_cast<const void*>(&dense_down_kernel),
                                 dim3(a.width / kDenseCols * a.dsplits), dim3(64 * kDenseDnWaves), dargs, 0, stream);
