@@ -86,7 +86,9 @@ struct HipLayerBuffers {
 // and the Ministral RMSNorm, examples/ministral/native/predictor_shared_input.cu:16-41):
 // hidden = fp16(fp32 residual + fp32 y) per row, then optionally RMSNorm(hidden) * weight,
 // then the flags (system-scope release stores of the enqueue's epoch) and the bell -- withheld
-// for a failed layer (a status bit set, or the queue's error word).
+// for a failed layer (a status bit set, or the queue's error word). A fused launch computes it
+// in its own last workgroup once every worker is out (its completion word follows); the split
+// entry point and the dense path launch it as a kernel after the layer.
 // Device pointers, [batch][width] rows; the flags may be host-coherent words.
 struct HipEpilogue {
     const void* residual = nullptr;     // fp16 [batch][width]

@@ -96,11 +96,13 @@ int ls_hip_set_stage_hook(void* backend, int (*arm)(void*), void* context, void*
  * (the Triton reduction's PUBLISH path, backends/triton/reduction.py:17-28), optionally
  * RMSNorm(hidden) * norm_weight (examples/ministral/native/predictor_shared_input.cu:16-41),
  * then hidden_flag / norm_flag receive the enqueue's epoch (system-scope release) and
- * bell += 1. A failed layer -- its launch raised a status bit (sticky until
- * ls_hip_clear_status) or its queue's error word is set -- gets its rows written but neither
- * flag nor the bell. The completion word of the layer does not cover the epilogue: readers
- * of hidden wait on the flags. NULL removes it. EINVAL for an unbound backend or an
- * inconsistent block. */
+ * bell += 1. A fused launch (the default entry point, batch 1..4) runs it in its own last
+ * workgroup once every worker is out, and its completion word follows the epilogue; the split
+ * entry point and the dense path (batch 5..32) launch it after the layer, where the
+ * completion word does not cover it. A failed layer -- its launch raised a status bit (sticky
+ * until ls_hip_clear_status) or its queue's error word is set -- gets neither flag nor the
+ * bell, and its rows are not the layer's output. Readers of hidden wait on the flags. NULL removes
+ * it. EINVAL for an unbound backend or an inconsistent block. */
 typedef struct ls_hip_epilogue {
     const void* residual;
     void* hidden;

@@ -362,6 +362,20 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
     // consumed: a dense layer's groups are all resident).
     lsamd::StageHook hook{arm_final_prediction, arm_context, static_cast<hipEvent_t>(b_done), 0};
     lsamd::StageHook* hk = arm_final_prediction || b_done ? &hook : nullptr;
+    // The fused launch runs the epilogue in its own last workgroup; the split entry point and
+    // the dense path launch epilogue_kernel after the layer.
+    const bool fused_epilogue = p.has_epilogue && !p.dense && entry == lsamd::kEntryFused;
+    if (fused_epilogue) {
+        const HipEpilogue& ep = p.epilogue;
+        a.residual = static_cast<const uint16_t*>(ep.residual);
+        a.hidden = static_cast<uint16_t*>(ep.hidden);
+        a.hidden_flag = ep.hidden_flag;
+        a.norm_weight = static_cast<const uint16_t*>(ep.norm_weight);
+        a.norm_out = static_cast<uint16_t*>(ep.norm_output);
+        a.norm_flag = ep.norm_flag;
+        a.bell = ep.bell;
+        a.norm_eps = ep.norm_eps;
+    }
     if (p.dense) {
         e = lsamd::launch_dense(a, p.bounds, hs);
         if (e == hipSuccess) e = lsamd::run_stage_hook(hk, hs);
@@ -374,7 +388,7 @@ int HipBackend::enqueue(KernelRuntimeState s, const void* input, void* output, v
         return static_cast<int>(e);
     }
     p.last_seq = a.seq;
-    if (p.has_epilogue) {
+    if (p.has_epilogue && !fused_epilogue) {
         const HipEpilogue& ep = p.epilogue;
         lsamd::EpilogueArgs x{};
         x.y = a.y;

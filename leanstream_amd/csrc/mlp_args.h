@@ -217,6 +217,16 @@ struct MlpArgs {
     uint16_t* x16;                // x as fp16 MFMA A fragments, 32 rows x d (dense_x_kernel; rows >= batch zero)
     uint32_t dsplits;
     uint64_t spin_limit;          // bounded waits, in 100 MHz ticks
+    // the layer's epilogue, run by the fused launch's last workgroup once every worker is out
+    // (hidden == nullptr: none); the fields of EpilogueArgs (mlp_launch.h) of the same names
+    const uint16_t* residual;     // fp16 [batch][d]
+    uint16_t* hidden;             // fp16 [batch][d]
+    uint32_t* hidden_flag;
+    const uint16_t* norm_weight;  // optional fp16 [d]
+    uint16_t* norm_out;           // fp16 [batch][d] (with norm_weight)
+    uint32_t* norm_flag;
+    uint32_t* bell;
+    float norm_eps;
 };
 
 }  // namespace lsamd

@@ -708,11 +708,57 @@ __device__ __forceinline__ void st_agent_u64(unsigned long long* p, unsigned lon
     __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned long long word, uint32_t rows) {
+// A column's value from its accumulator word once all `rows` contributions are in.
+__device__ __forceinline__ float acc_value(unsigned long long word, uint32_t rows) {
     const long long sum = (long long)(word & kAccValueMask) - (long long)rows * kAccBias;
-    const float v = (float)((double)sum * kAccInv);
+    return (float)((double)sum * kAccInv);
+}
+
+__device__ __forceinline__ void write_output(const MlpArgs& a, int col, unsigned long long word, uint32_t rows) {
+    const float v = acc_value(word, rows);
     if (a.y32) a.y32[col] = v;
     a.y[col] = __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// The layer epilogue's arithmetic (LeanStream backends/triton/reduction.py:17-28 with
+// PUBLISH; examples/ministral/native/predictor_shared_input.cu:16-41), shared by
+// epilogue_kernel and the fused launch's last workgroup. hidden = fp16(fp32 residual + fp32
+// y), its square added to the thread's sum (thread t of 256 takes columns t, t + 256, ... in
+// order); inverse = 1 / sqrt(sum / width + eps) over a halving tree of the 256 partial sums;
+// out = fp16(weight * fp16(hidden * inverse)). Nothing is contracted into a fused
+// multiply-add, so the bits are the oracle's.
+__device__ __forceinline__ uint16_t epi_hidden(uint16_t res, uint16_t y, float& sum) {
+#pragma clang fp contract(off)
+    const float a = (float)__builtin_bit_cast(_Float16, res);
+    const float b = (float)__builtin_bit_cast(_Float16, y);
+    float ab = a + b;
+    asm volatile("" : "+v"(ab));   // an fp32 sum rounded to fp16 (no mixed-precision fused form)
+    const _Float16 h = (_Float16)ab;
+    const float v = (float)h;
+    const float sq = v * v;
+    sum = sum + sq;
+    return __builtin_bit_cast(uint16_t, h);
+}
+// The workgroup's 256 partial sums (lanes: 256 floats of LDS) -> the row's inverse RMS.
+__device__ __forceinline__ float epi_inverse(float sum, float* lanes, uint32_t width, float eps) {
+#pragma clang fp contract(off)
+    const uint32_t t = threadIdx.x;
+    __syncthreads();   // a previous row's reads of lanes are done
+    lanes[t] = sum;
+    __syncthreads();
+    for (uint32_t stride = 128; stride; stride >>= 1) {
+        if (t < stride) lanes[t] = lanes[t] + lanes[t + stride];
+        __syncthreads();
+    }
+    return 1.0f / __builtin_sqrtf(lanes[0] / (float)width + eps);
+}
+__device__ __forceinline__ uint16_t epi_norm(uint16_t hid, float inverse, uint16_t weight) {
+#pragma clang fp contract(off)
+    float p = (float)__builtin_bit_cast(_Float16, hid) * inverse;
+    asm volatile("" : "+v"(p));   // the fp32 product, then fp16 (as the reference rounds)
+    const float n = (float)(_Float16)p;
+    const float w = (float)__builtin_bit_cast(_Float16, weight);
+    return __builtin_bit_cast(uint16_t, (_Float16)(w * n));   // the exact product, rounded once
 }
 
 // The accumulator buffer of this launch (two alternate between consecutive launches).

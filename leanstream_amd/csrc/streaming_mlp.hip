@@ -202,7 +202,8 @@ __device__ __forceinline__ void count_out(uint32_t* slot) {
                                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, uint32_t workers) {
+__device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, uint32_t workers,
+                                              bool store_done = true) {
     const uint32_t lane = lane_id();
     const uint32_t want = lane < 8u ? (workers + 7u - lane) / 8u : 0u;   // workers b < W with b % 8 == lane
     Waiter wt(a.spin_limit);
@@ -216,7 +217,87 @@ __device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, 
         __builtin_amdgcn_s_sleep(1);
     }
     stamp(a, kStampMirrorDone);
-    if (lane == 0) __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (store_done && lane == 0) __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+// The layer's epilogue in the fused launch's last workgroup (256 threads), once every worker
+// is out: epilogue_kernel's arithmetic on the same y -- each column's fp16 value formed from
+// its accumulator word as the worker that completed it formed it (acc_value), read back at
+// agent scope -- one batch row after the other. The inputs known before the launch (row 0's
+// residual, the norm weight) are requested while the first wave still waits for the workers
+// (epi_prefetch). The flags and the bell are released only when the launch raised no status
+// bit and its queue carries no error (a launch whose queue was abandoned writes no rows: its
+// columns are incomplete). Then the completion word.
+template <int D>
+struct EpiInputs {
+    uint16_t res[D / kThreads];      // row 0's residual, columns t + 256 j
+    uint16_t weight[D / kThreads];   // the norm weight, columns t + 256 j
+};
+
+template <int D>
+__device__ __forceinline__ void epi_prefetch(const MlpArgs& a, EpiInputs<D>& in) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (uint32_t j = 0; j < D / kThreads; ++j) {
+        in.res[j] = a.residual[t + kThreads * j];
+        in.weight[j] = a.norm_weight ? a.norm_weight[t + kThreads * j] : (uint16_t)0;
+    }
+}
+
+// `decision` (LDS, written by thread 0 before the workgroup's barrier): 0 when the launch
+// left its queue, else 1 | total << 1 with the queue's total from the mirrored epoch word.
+template <int D, bool PACKED>
+__device__ __forceinline__ void fused_epilogue(const MlpArgs& a, float* lanes, uint32_t decision,
+                                               const EpiInputs<D>& in) {
+    constexpr uint32_t PER = D / kThreads;
+    static_assert(kThreads == 256 && D % kThreads == 0, "256 threads, whole columns each");
+    const uint32_t t = threadIdx.x;
+    // the status and queue error words (host memory): their round trip overlaps the rows
+    uint32_t status = 0, error = 0;
+    if (t == 0) {
+        status = ld_sys(a.status);
+        error = ld_sys(&a.control->error);
+    }
+    const bool ok = decision & 1u;
+    if (ok) {
+        const uint32_t U = column_rows<PACKED>(a, decision >> 1);
+        const unsigned long long* acc = launch_acc(a);
+        for (uint32_t r = 0; r < a.batch; ++r) {
+            const size_t base = (size_t)r * D;
+            unsigned long long w[PER];
+            uint16_t res[PER];
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                w[j] = ld_agent_u64(reinterpret_cast<const uint64_t*>(acc) + (base + t + kThreads * j) * kAccStride);
+                res[j] = r ? a.residual[base + t + kThreads * j] : in.res[j];
+            }
+            float sum = 0.f;
+            uint16_t hid[PER];
+#pragma unroll
+            for (uint32_t j = 0; j < PER; ++j) {
+                const uint16_t y = __builtin_bit_cast(uint16_t, (_Float16)acc_value(w[j], U));
+                hid[j] = epi_hidden(res[j], y, sum);
+                a.hidden[base + t + kThreads * j] = hid[j];
+            }
+            if (a.norm_weight) {
+                const float inverse = epi_inverse(sum, lanes, D, a.norm_eps);
+#pragma unroll
+                for (uint32_t j = 0; j < PER; ++j)
+                    a.norm_out[base + t + kThreads * j] = epi_norm(hid[j], inverse, in.weight[j]);
+            }
+        }
+    }
+    // this workgroup's stores are visible at system scope before the flags
+    __atomic_thread_fence(__ATOMIC_RELEASE);
+    __syncthreads();
+    if (t == 0) {
+        if (ok && !status && !error) {
+            if (a.hidden_flag) __hip_atomic_store(a.hidden_flag, a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (a.norm_flag) __hip_atomic_store(a.norm_flag, a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (a.bell) (void)__hip_atomic_fetch_add(a.bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 }
 
 // Completion proof of the split launch sequence, at the end of its last kernel (the
@@ -269,7 +350,7 @@ __device__ __forceinline__ MlpArgs with_hot(const MlpArgs& args, const uint16_t*
 }
 
 // The persistent kernels' argument segment: LS_HOT_PARAMS in order, each at its natural
-// alignment (the code object's argument offsets: args at 56, b at 336).
+// alignment (the code object's argument offsets: args at 56, b right after it).
 struct PersistentParams {
     const uint16_t* x;
     const ExecDesc* core;
@@ -280,7 +361,7 @@ struct PersistentParams {
     MlpArgs args;
     Bounds b;
 };
-static_assert(offsetof(PersistentParams, args) == 56 && offsetof(PersistentParams, b) == 336,
+static_assert(offsetof(PersistentParams, args) == 56 && offsetof(PersistentParams, b) == 56 + sizeof(MlpArgs),
               "argument segment layout of LS_HOT_PARAMS");
 
 // The argument blocks, read where this is called. The compiler loads a kernel's arguments
@@ -318,7 +399,21 @@ __global__ __launch_bounds__(kThreads, kWgPerCu) void fused_layer_kernel(LS_HOT_
         const MlpArgs a = LS_HOT_ARGS;
         const uint64_t pre = threadIdx.x == 0 ? ld_sys64(&a.control->total_count) : 0;
         run_mirror(a, slot, pre);
-        if (threadIdx.x < 64) await_workers(a, slot, a.grid - 1);
+        if (a.hidden) {   // the layer's epilogue, here once every worker is out
+            EpiInputs<D> in;
+            epi_prefetch<D>(a, in);
+            uint32_t* decision = reinterpret_cast<uint32_t*>(stage);
+            if (threadIdx.x < 64) {
+                // the epoch word is final once the queue is mirrored; read while the workers finish
+                const uint32_t word = threadIdx.x == 0 ? ld_agent(slot + kSyncEpoch) : 0u;
+                await_workers(a, slot, a.grid - 1, false);
+                if (threadIdx.x == 0) decision[0] = (word & 3u) == 1u ? 1u | (word >> 4) << 1 : 0u;
+            }
+            __syncthreads();
+            fused_epilogue<D, WALK == kWalkPacked>(a, reinterpret_cast<float*>(stage), decision[0], in);
+        } else if (threadIdx.x < 64) {
+            await_workers(a, slot, a.grid - 1);
+        }
     } else {
         WorkerStart<D> st;
         LS_WORKER_START(true, true);
@@ -475,7 +570,7 @@ struct DenseGuParams {
     MlpArgs args;
     Bounds b;
 };
-static_assert(offsetof(DenseGuParams, args) == 16 && offsetof(DenseGuParams, b) == 296,
+static_assert(offsetof(DenseGuParams, args) == 16 && offsetof(DenseGuParams, b) == 16 + sizeof(MlpArgs),
               "argument segment layout of dense_gate_up_kernel");
 
 // The unit's descriptor and the first x16 steps go out from the preloaded arguments; the
@@ -1038,7 +1133,6 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
 // the rows are written but nothing announces them.
 // ---------------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
-#pragma clang fp contract(off)
     __shared__ float lanes[256];
     __shared__ uint32_t last;
     const uint32_t t = threadIdx.x, row = blockIdx.x;
@@ -1046,33 +1140,11 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
     const uint16_t* res = e.residual + (size_t)row * e.width;
     uint16_t* hid = e.hidden + (size_t)row * e.width;
     float sum = 0.f;
-    for (uint32_t i = t; i < e.width; i += 256) {
-        const float a = (float)__builtin_bit_cast(_Float16, res[i]);
-        const float b = (float)__builtin_bit_cast(_Float16, y[i]);
-        float ab = a + b;
-        asm volatile("" : "+v"(ab));   // an fp32 sum rounded to fp16 (no mixed-precision fused form)
-        const _Float16 h = (_Float16)ab;
-        hid[i] = __builtin_bit_cast(uint16_t, h);
-        const float v = (float)h;
-        const float sq = v * v;
-        sum = sum + sq;
-    }
+    for (uint32_t i = t; i < e.width; i += 256) hid[i] = epi_hidden(res[i], y[i], sum);
     if (e.norm_weight) {
-        lanes[t] = sum;
-        __syncthreads();
-        for (uint32_t stride = 128; stride; stride >>= 1) {
-            if (t < stride) lanes[t] = lanes[t] + lanes[t + stride];
-            __syncthreads();
-        }
-        const float inverse = 1.0f / __builtin_sqrtf(lanes[0] / (float)e.width + e.eps);
+        const float inverse = epi_inverse(sum, lanes, e.width, e.eps);
         uint16_t* out = e.norm_out + (size_t)row * e.width;
-        for (uint32_t i = t; i < e.width; i += 256) {
-            float p = (float)__builtin_bit_cast(_Float16, hid[i]) * inverse;
-            asm volatile("" : "+v"(p));   // the fp32 product, then fp16 (as the reference rounds)
-            const float n = (float)(_Float16)p;
-            const float w = (float)__builtin_bit_cast(_Float16, e.norm_weight[i]);
-            out[i] = __builtin_bit_cast(uint16_t, (_Float16)(w * n));   // the exact product, rounded once
-        }
+        for (uint32_t i = t; i < e.width; i += 256) out[i] = epi_norm(hid[i], inverse, e.norm_weight[i]);
     }
     if (!e.hidden_flag && !e.norm_flag && !e.bell) return;
     // this workgroup's stores are visible at system scope before it counts itself in
