@@ -2,8 +2,9 @@
 (LeanStream backends/triton/reduction.py:17-28) and its RMSNorm
 (examples/ministral/native/predictor_shared_input.cu:16-41) bit for bit against the oracle on
 the layer's own y, the flags carrying the enqueue's epoch and the bell counting launches;
-batch rows each normalized on their own, the flags released once per launch; also after a
-dense (batch 32, matrix-core) launch."""
+batch rows each normalized on their own, the flags released once per launch. A fused launch
+runs it in its own last workgroup (batch 1 and 4); the split entry point and a dense (batch 32,
+matrix-core) launch run it as a kernel after the layer."""
 import numpy as np
 import pytest
 
@@ -19,12 +20,15 @@ def log(msg):
     print(msg, flush=True)
 
 
-@pytest.mark.parametrize("key", ["c2", "c1b4", "c1d32"])
-def test_epilogue_publishes_hidden_and_rmsnorm(torch_gpu, key):
+# fused launches run the epilogue in their last workgroup; the split entry point (candidate 4)
+# and the dense path (batch 32) launch epilogue_kernel after the layer
+@pytest.mark.parametrize("key,table", [("c2", None), ("c2", [[4]]), ("c1b4", None), ("c1d32", None)],
+                         ids=["c2-fused", "c2-split", "c1b4-fused", "c1d32-dense"])
+def test_epilogue_publishes_hidden_and_rmsnorm(torch_gpu, key, table):
     torch = torch_gpu
     cfg = synth.CONFIGS[key]
-    log(f"case: epilogue {cfg.name}")
-    layer = DeviceLayer(cfg)
+    log(f"case: epilogue {cfg.name} table {table}")
+    layer = DeviceLayer(cfg, offline_table=table) if table else DeviceLayer(cfg)
     d, rows = cfg.width, cfg.batch
     rng = np.random.default_rng(17)
     residual_h = rng.standard_normal(rows * d).astype(np.float16)
@@ -44,6 +48,8 @@ def test_epilogue_publishes_hidden_and_rmsnorm(torch_gpu, key):
         layer.run_core(epoch=epoch)
         torch.cuda.synchronize()
         assert layer.backend.status() == 0
+        if table:
+            assert layer.backend.last_candidate() == table[0][0]
         assert flags.host.tolist() == [epoch, epoch, launch + 1]
         y = layer.y.cpu().numpy()
         want_hidden = oracle.publish_hidden(residual_h, y)
