@@ -1589,7 +1589,7 @@ __device__ __forceinline__ void dn_accumulate_tile(const u32x4* sl, const uint16
 }
 
 #ifndef LS_DN_PRE
-#define LS_DN_PRE 1
+#define LS_DN_PRE 2
 #endif
 // Row pairs of a staged down tile dequantised while the unit's h is on its way.
 constexpr int kDnPre = LS_DN_PRE;
