@@ -471,6 +471,14 @@ __device__ __forceinline__ void chain_gu_dots(const u32x4* sl, const u32x4* xl, 
     gu_finish<D, 1>(acc, m.hrow, kStagedGroup, m.n0, Gm::NPI, seq, 1u);
 }
 
+// Row pairs of a chained down tile dequantised before its h is in. A chained layer's tiles
+// land long before their h (they are requested while the previous layer finishes), so at
+// d = 1024 the whole tile is dequantised ahead (246 registers; 36-layer C1 chain 8.13 ->
+// 7.88 us per layer); at d = 4096 two pairs, as in the single-layer kernels (four measured
+// equal there: the layer's time is not in its post-h tile work).
+template <int D>
+constexpr int kChainDnPre = D <= 1024 ? 4 : kDnPre;
+
 // A down tile: the residuals of the lane's four columns and the first look at h requested,
 // part of the tile dequantised while they travel, then the dot products, the row-group
 // tree, the re-deal through the slot and four column additions.
@@ -483,8 +491,8 @@ __device__ __forceinline__ bool chain_dn(const ChainArgs& c, const MlpArgs& a, C
     uint16_t* hs = sh.hs[wave_id()];
     DnItem it;
     it.h = ld_agent_u64(uniform_ptr(m.hrow) + lane);
-    h2 pre[kDnPre > 0 ? kDnPre : 1][4][8];
-    dn_dequant_tile<kDnPre>(sl, pre);
+    h2 pre[kChainDnPre<D> > 0 ? kChainDnPre<D> : 1][4][8];
+    dn_dequant_tile<kChainDnPre<D>>(sl, pre);
     if (!wait_h_word(a, c.csync, m.hrow, 0, it.h)) return false;
     // The residual of a column: the previous layer's hidden word, or the first layer's
     // residual row. Requested once h is in: h of this layer exists only after the previous
@@ -502,7 +510,7 @@ __device__ __forceinline__ bool chain_dn(const ChainArgs& c, const MlpArgs& a, C
     hs[lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)it.h));   // exact: h is fp16
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     float acc[32], cs[4];
-    dn_accumulate_tile_pre<kDnPre>(sl, hs, pre, acc);
+    dn_accumulate_tile_pre<kChainDnPre<D>>(sl, hs, pre, acc);
     dn_reduce(acc, cs);
     float* red = reinterpret_cast<float*>(sl);
     *reinterpret_cast<float4*>(red + 32 * (lane & 7) + 4 * (lane >> 3)) = float4{cs[0], cs[1], cs[2], cs[3]};
