@@ -332,7 +332,23 @@ __device__ bool chain_stage_part(const ChainArgs& c, const MlpArgs& a, const Lay
             }
             if (__all(all)) break;
             if (wave_should_stop(a, c.csync, wtime)) return false;
-            __builtin_amdgcn_s_sleep(1);
+            // Every workgroup reads the whole row, so while most of it is missing (the previous
+            // layer still running) each poll round is D * 4 bytes per workgroup from beyond
+            // L2, competing with that layer's own traffic: at d = 4096 the wave sleeps about
+            // 1 us between rounds then (C2 chain 14.23 -> 13.62 us per layer), and polls at
+            // once when at most a quarter of its words are missing. At d = 1024 (a quarter of
+            // the reads, a shorter layer) the longer sleep cost more than it saved.
+            if constexpr (D > 1024) {
+                uint32_t miss = 0;
+#pragma unroll
+                for (int m = 0; m < Q; ++m) miss += (uint32_t)__popcll(__ballot(!have[m]));
+                if (miss * 4u > 64u * Q)
+                    __builtin_amdgcn_s_sleep(40);
+                else
+                    __builtin_amdgcn_s_sleep(1);
+            } else {
+                __builtin_amdgcn_s_sleep(1);
+            }
         }
         // the input is here: every wave of the workgroup waits for its staging, which now takes
         // the SIMD's issue slots ahead of the co-resident wave (the poll above did not)
