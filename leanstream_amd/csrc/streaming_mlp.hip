@@ -287,8 +287,12 @@ __device__ __forceinline__ void fused_epilogue(const MlpArgs& a, float* lanes, u
             }
         }
     }
-    // this workgroup's stores are visible at system scope before the flags
-    __atomic_thread_fence(__ATOMIC_RELEASE);
+    // this workgroup's stores are visible at system scope before the flags; without flags the
+    // completion word orders after them as after a launch's outputs (acknowledged stores)
+    if (a.hidden_flag || a.norm_flag || a.bell)
+        __atomic_thread_fence(__ATOMIC_RELEASE);
+    else
+        drain_vmem();
     __syncthreads();
     if (t == 0) {
         if (ok && !status && !error) {
