@@ -556,7 +556,13 @@ __device__ __forceinline__ bool wait_h_word(const MlpArgs& a, uint32_t* slot, co
     Waiter wt(a.spin_limit);
     for (;;) {
         if (wave_should_stop(a, slot, wt)) return false;
-        __builtin_amdgcn_s_sleep(1);
+        // While more than a quarter of the words are missing the wave waits about 0.2 us
+        // between rounds: fewer reads from beyond L2 while the layer's bytes still stream (C2
+        // 14.12 -> 13.99 us); with few words missing it polls at once.
+        if (__popcll(__ballot((h >> 32) != want)) > 16)
+            __builtin_amdgcn_s_sleep(8);
+        else
+            __builtin_amdgcn_s_sleep(1);
         if ((h >> 32) != want) h = ld_agent_u64(hrow + n);   // only rows < G can be stale
         if (__all((h >> 32) == want)) return true;
     }
