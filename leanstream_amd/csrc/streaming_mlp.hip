@@ -214,7 +214,12 @@ __device__ __forceinline__ void await_workers(const MlpArgs& a, uint32_t* slot, 
             if (lane == 0) raise_status(a, slot, kStatusTimeout);
             break;
         }
-        __builtin_amdgcn_s_sleep(1);
+        // about 0.45 us between rounds while any group is less than half out, then at once
+        // (C1 10.28 -> 10.23 us)
+        if (__any(lane < 8u && got * 2u < want))
+            __builtin_amdgcn_s_sleep(16);
+        else
+            __builtin_amdgcn_s_sleep(1);
     }
     stamp(a, kStampMirrorDone);
     if (store_done && lane == 0) __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
