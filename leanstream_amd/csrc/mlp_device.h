@@ -548,6 +548,7 @@ __device__ __forceinline__ void dn_issue(const uint8_t* grp, const uint16_t* sc,
 
 // Waits until the h of every row of the pass carries the launch sequence. False when
 // the wait was abandoned (abort or timeout).
+template <bool BACKOFF = true>
 __device__ __forceinline__ bool wait_h_word(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int r0,
                                             uint64_t& h) {
     const uint64_t want = a.seq;
@@ -558,8 +559,9 @@ __device__ __forceinline__ bool wait_h_word(const MlpArgs& a, uint32_t* slot, co
         if (wave_should_stop(a, slot, wt)) return false;
         // While more than a quarter of the words are missing the wave waits about 0.2 us
         // between rounds: fewer reads from beyond L2 while the layer's bytes still stream (C2
-        // 14.12 -> 13.99 us); with few words missing it polls at once.
-        if (__popcll(__ballot((h >> 32) != want)) > 16)
+        // 14.12 -> 13.99 us); with few words missing it polls at once. The batch 2-4 kernels
+        // wait without it (C4 batch 4 52.5 -> 52.9 us with it).
+        if (BACKOFF && __popcll(__ballot((h >> 32) != want)) > 16)
             __builtin_amdgcn_s_sleep(8);
         else
             __builtin_amdgcn_s_sleep(1);
@@ -567,10 +569,11 @@ __device__ __forceinline__ bool wait_h_word(const MlpArgs& a, uint32_t* slot, co
         if (__all((h >> 32) == want)) return true;
     }
 }
+template <bool BACKOFF = true>
 __device__ __forceinline__ bool dn_wait_h(const MlpArgs& a, uint32_t* slot, const uint64_t* hrow, int G, int r0,
                                           DnItem& it) {
     (void)G;
-    return wait_h_word(a, slot, hrow, r0, it.h);
+    return wait_h_word<BACKOFF>(a, slot, hrow, r0, it.h);
 }
 
 // Adds one pass into the lane's 32 column partials. The pass's h and scales go through
@@ -1334,7 +1337,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
                                                               : (uint64_t)a.seq << 32;
 #pragma unroll
                 for (int r = 0; r < NB; ++r) {
-                    if (!wait_h_word(a, slot, m.hrow + (size_t)r * G, 0, hr[r])) return false;
+                    if (!wait_h_word<false>(a, slot, m.hrow + (size_t)r * G, 0, hr[r])) return false;
                     hb[r][lane] = __builtin_bit_cast(uint16_t, (_Float16)__uint_as_float((uint32_t)hr[r]));   // exact
                 }
                 float part[NB][4];
@@ -1367,7 +1370,7 @@ __device__ __forceinline__ bool process_items(const MlpArgs& a, Shared& sh, u32x
         } else {
             for (int r0 = 0; r0 < (int)G; r0 += kDnRows) {
                 if (r0) dn_issue<D>(m.grp, m.sc, m.hrow, (int)G, (int)m.tile, r0, a.seq, di);
-                if (!dn_wait_h(a, slot, m.hrow, (int)G, r0, di)) return false;
+                if (!dn_wait_h<NB == 1>(a, slot, m.hrow, (int)G, r0, di)) return false;
                 dn_accumulate(di, hs, ss, acc);
             }
         }
