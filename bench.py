@@ -118,7 +118,7 @@ def host_cpu():
     return os.cpu_count() or 1, model
 
 
-# The GPU box gives one GPU's job a share of 16 host CPUs (OMP_NUM_THREADS there): the
+# A one-GPU job gets a share of 16 host CPUs (OMP_NUM_THREADS is set to it): the
 # baseline's thread pool stays within that share whatever the host's CPU count.
 CPU_SHARE = 16
 

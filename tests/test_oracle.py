@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the GPU results are checked against it.
 
 Checks, chosen so that a plausible oracle mistake fails one of them:
   * generator: numpy mirror == C oracle, bit for bit (catches seed/counter/rounding slips);

@@ -45,7 +45,7 @@ def test_runtime_reproduces_reference_trace(tmp_path):
 
 
 def test_golden_trace_is_current_with_the_reference_build():
-    """Where LeanStream's sources are present (never on the GPU box), the committed fixture
+    """Where LeanStream's sources are present (not on GPU test machines), the committed fixture
     must still be what the reference runtime prints."""
     ref = ROOT / "oracle" / "_ref" / "runtime_trace_ref"
     if not Path(os.environ.get("LEANSTREAM_REFERENCE", "/root/reference")).is_dir():

@@ -50,7 +50,7 @@ def test_host_staging_trace_is_race_free(tmp_path):
 
 
 def test_staging_golden_is_current_with_the_reference_build():
-    """Where LeanStream's sources are present (never on the GPU box), the committed fixture
+    """Where LeanStream's sources are present (not on GPU test machines), the committed fixture
     must still be what the reference engine prints."""
     if not Path(os.environ.get("LEANSTREAM_REFERENCE", "/root/reference")).is_dir():
         pytest.skip("reference sources not present")
