@@ -563,7 +563,7 @@ def chain_bench(a):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
+        print(json.dumps({"error": "the path runs on one GPU; --gpus must be 1 (multi-GPU sharding is design-only)"}))
         sys.exit(2)
     if a.copy_calibration:
         copy_calibration()

@@ -1,6 +1,6 @@
 // Per-layer residency and descriptor producer (LeanStream weight_manager.h:9-72).
 // This implementation publishes READY groups through a borrowed IOBackend; the
-// reference's O_DIRECT stream engine is not part of this build, so an empty
+// reference's O_DIRECT stream engine is not part of this library, so an empty
 // io_backend is rejected at construction.
 // Interface kept alike with LeanStream's (MIT, Copyright (c) 2026 LeanStream Authors): see THIRD_PARTY_NOTICES.md.
 #pragma once

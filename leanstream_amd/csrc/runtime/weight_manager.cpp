@@ -22,7 +22,7 @@
 // The observable behaviour -- descriptors, publication order, queue words, return codes
 // and transport calls -- is pinned line by line against LeanStream's own runtime
 // (tests/golden/runtime_trace.txt, tests/golden/staging_trace.txt). The transport is
-// always a borrowed IOBackend; LeanStream's O_DIRECT engine is not part of this build.
+// always a borrowed IOBackend; LeanStream's O_DIRECT engine is not part of this library.
 #include "leanstream/weight_manager.h"
 #include <algorithm>
 #include <atomic>
