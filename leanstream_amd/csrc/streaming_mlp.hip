@@ -301,8 +301,10 @@ __device__ __forceinline__ void fused_epilogue(const MlpArgs& a, float* lanes, u
     __syncthreads();
     if (t == 0) {
         if (ok && !status && !error) {
-            if (a.hidden_flag) __hip_atomic_store(a.hidden_flag, a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (a.norm_flag) __hip_atomic_store(a.norm_flag, a.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            // both flags follow the rows (the release above, then the barrier); the bell follows
+            // the flags: one release between them instead of one per flag
+            if (a.hidden_flag) __hip_atomic_store(a.hidden_flag, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (a.norm_flag) __hip_atomic_store(a.norm_flag, a.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (a.bell) (void)__hip_atomic_fetch_add(a.bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         __hip_atomic_store(a.done, a.seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -1135,8 +1137,8 @@ hipError_t launch_dense(const MlpArgs& args, const Bounds& bounds, hipStream_t s
 // inverse = 1 / sqrt(sum / width + eps) (IEEE square root and division), out =
 // fp16(weight * fp16(hidden * inverse)). Products and sums are not contracted into fused
 // multiply-adds, so the result is the oracle's bit for bit. The last row's workgroup to
-// finish publishes the flags with system-scope release stores: hidden_flag, then
-// norm_flag, then bell += 1 -- unless the layer failed: its launch raised a status bit (a
+// finish publishes the flags after a system-scope release: hidden_flag and norm_flag, then
+// (released after them) bell += 1 -- unless the layer failed: its launch raised a status bit (a
 // bounded wait expired, a descriptor or a value was rejected) or its queue carries an error
 // (the runtime cancelled the layer; the launch left early). Then y is not the layer's output:
 // the rows are written but nothing announces them.
@@ -1168,8 +1170,10 @@ __global__ __launch_bounds__(256) void epilogue_kernel(EpilogueArgs e) {
             if (__hip_atomic_load(e.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) ||
                 (e.queue_error && __hip_atomic_load(e.queue_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM)))
                 return;
-            if (e.hidden_flag) __hip_atomic_store(e.hidden_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (e.norm_flag) __hip_atomic_store(e.norm_flag, e.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+            // one release for both flags (every row acquired above), one between them and the bell
+            __atomic_thread_fence(__ATOMIC_RELEASE);
+            if (e.hidden_flag) __hip_atomic_store(e.hidden_flag, e.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (e.norm_flag) __hip_atomic_store(e.norm_flag, e.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             if (e.bell) (void)__hip_atomic_fetch_add(e.bell, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
         }
     }
